@@ -1,0 +1,244 @@
+#!/usr/bin/env python3
+"""SpartonHead forward+backward throughput on one MI355X.
+
+A step is one training pass of the head over one batch of synthetic inputs already
+resident in HBM: reps = head(hidden, mask); reps.backward(grad) through
+SpartonHead + autograd (grads set to None first, as an optimizer's
+zero_grad(set_to_none=True) does). The workload is BASELINE.json's headline
+configuration (B=32, S=256, D=768, V=30522, bf16) unless --config says otherwise.
+
+Prints ONE JSON line. Besides the throughput it reports:
+  roofline      the forward kernel (MFMA-bound): useful flops 2*D*V*sum_b(len_b)
+                per launch / its mean duration from HIP events, vs 2.5 PFLOP/s.
+  bwd_roofline  the backward kernels (HBM-bound): compulsory bytes per call / their
+                mean duration from HIP events, vs 8 TB/s.
+  cpu_baseline  the reference's torch head (training/model.py:56-62, restated in
+                oracle/) fwd+bwd on the host cores, on a bounded sample of batch rows.
+"""
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+METRIC = "fused head fwd+bwd tokens/sec & MFMA util, B32 S256 V30522 bf16; peak GB"
+PEAK_TFLOPS = {"bf16": 2500.0, "fp16": 2500.0, "fp32": 157.3}
+PEAK_HBM_GBS = 8000.0
+DTYPE_NAME = {"torch.bfloat16": "bf16", "torch.float16": "fp16", "torch.float32": "fp32"}
+
+
+def parse():
+    p = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=50)
+    p.add_argument("--warmup", type=int, default=10)
+    p.add_argument("--config", type=int, default=2, help="workload index (BASELINE.json configs, 1-based)")
+    p.add_argument("--kernel-reps", type=int, default=50, help="back-to-back launches per kernel timing")
+    p.add_argument("--cpu-seconds", type=float, default=25.0, help="budget (s) of the CPU baseline leg")
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    return p.parse_args()
+
+
+def cpu_model():
+    try:
+        for ln in open("/proc/cpuinfo"):
+            if ln.startswith("model name"):
+                return ln.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def time_events(torch, fn, reps):
+    """Mean GPU time of fn() from HIP events on the current stream, fn launched
+    back to back so the GPU never waits for the host between launches."""
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    fn()
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(reps):
+        fn()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / reps
+
+
+def cpu_baseline(torch, w, inp, budget_s):
+    """The reference torch head fwd+bwd on the host, on the first rows of the batch."""
+    import oracle
+    threads = min(os.cpu_count() or 1, 16)
+    torch.set_num_threads(threads)
+    state = {}
+
+    def prepare(rows):
+        state["rows"] = rows
+        state["H"] = inp.hidden[:rows].clone().requires_grad_()
+        state["W"] = inp.weight.clone().requires_grad_()
+        state["b"] = inp.bias.clone().requires_grad_() if inp.bias is not None else None
+        state["m"], state["G"] = inp.mask[:rows], inp.grad[:rows]
+
+    def step():
+        out = oracle.torch_head_chunked(state["H"], state["W"], state["b"], state["m"], v_chunk=8192)
+        out.backward(state["G"])
+
+    def timed():
+        t0 = time.perf_counter()
+        step()
+        return time.perf_counter() - t0
+
+    # Size the sample so that about 5 timed steps fill the budget.
+    prepare(1)
+    timed()  # first call pays one-time costs
+    per_row = timed()
+    rows = max(1, min(w.B, int(budget_s / (5 * per_row))))
+    prepare(rows)
+    timed()  # warm-up at the final size
+    times = [timed() for _ in range(5)]
+    t = statistics.median(times)
+    n = len(times)
+    return {
+        "value": rows * w.S / t,
+        "seconds": round(sum(times), 2),
+        "unit": "tokens/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": (f"torch head (training/model.py:56-62, restated in oracle/) fwd+bwd autograd, "
+                   f"{DTYPE_NAME[str(w.dtype)]}, {rows} of {w.B} batch rows ({rows * w.S} tokens), "
+                   f"V-chunked by 8192, median of {n} after 1 warm-up; host CPU: {cpu_model()}"),
+    }
+
+
+def main():
+    args = parse()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py: this build measures the SpartonHead path on exactly one GPU; "
+              f"--gpus {args.gpus} (WORLD_SIZE={world}) is not supported. "
+              "Multi-GPU sharding is design-only (see DESIGN.md).", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    import sparton
+    from sparton_amd.workloads import WORKLOADS, make_inputs
+
+    assert torch.cuda.is_available(), "bench.py needs a ROCm device"
+    dev = torch.device("cuda:0")
+    w = WORKLOADS[args.config]
+    dname = DTYPE_NAME[str(w.dtype)]
+    inp_cpu = make_inputs(w)
+    inp = inp_cpu.to(dev)
+    has_bias = inp.bias is not None
+
+    head = sparton.SpartonHead(w.V, w.D, use_bias=has_bias).to(dev).to(w.dtype)
+    with torch.no_grad():
+        head.weight.copy_(inp.weight)
+        if has_bias:
+            head.bias.copy_(inp.bias)
+    H = inp.hidden.clone().requires_grad_()
+    mask, G = inp.mask, inp.grad
+    params = [p for p in head.parameters()]
+    torch.cuda.synchronize()
+    input_bytes = torch.cuda.memory_allocated()
+
+    def step():
+        H.grad = None
+        for p in params:
+            p.grad = None
+        reps = head(H, mask)
+        reps.backward(G)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    torch.cuda.reset_peak_memory_stats()
+
+    # ---- timed region: exactly K steps --------------------------------------------
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    peak_bytes = torch.cuda.max_memory_allocated()
+    ms_per_step = elapsed * 1e3 / args.steps
+    tokens = w.B * w.S
+    value = tokens / (elapsed / args.steps)
+
+    # ---- per-kernel timing (HIP events, back-to-back launches) ----------------------
+    Hd, Wd, bd = H.detach(), head.weight.detach(), (head.bias.detach() if has_bias else None)
+    fwd_ms = time_events(torch, lambda: torch.ops.sparton.fused_sparton_fwd(Hd, Wd, bd, mask), args.kernel_reps)
+    enc_ms = time_events(torch, lambda: torch.ops.sparton.fused_sparton_encode(Hd, Wd, bd, mask), args.kernel_reps)
+    reps, idx = torch.ops.sparton.fused_sparton_fwd(Hd, Wd, bd, mask)
+    bwd_ms = time_events(torch, lambda: torch.ops.sparton.fused_sparton_bwd(G, reps, idx, Hd, Wd, bd, mask),
+                         args.kernel_reps)
+
+    # forward roofline: useful flops on valid positions (masked positions are skipped)
+    valid_tokens = int(inp_cpu.mask.ne(0).sum())
+    useful_flops = 2.0 * w.D * w.V * valid_tokens
+    dense_flops = 2.0 * w.B * w.S * w.D * w.V
+    fwd_tflops = useful_flops / (fwd_ms * 1e-3) / 1e12
+    peak_tf = PEAK_TFLOPS[dname]
+
+    # backward roofline: compulsory bytes (each needed byte moved once)
+    e = torch.tensor([], dtype=w.dtype).element_size()
+    r = reps.float()
+    gp = torch.where(r > 0, G.float() * torch.exp(-r), torch.zeros_like(r))
+    gp = gp * mask.gather(1, idx.long()).float()
+    act = gp != 0
+    nnz = int(act.sum())
+    u_w = int(act.any(0).sum())
+    rows = (torch.arange(w.B, device=dev).view(-1, 1) * w.S + idx.long())[act]
+    u_h = int(torch.unique(rows).numel())
+    bwd_bytes = (w.B * w.V * (e + e + 4) + u_w * w.D * e + u_h * w.D * e
+                 + w.B * w.S * w.D * 4 + w.V * w.D * 4 + (w.V * 4 if has_bias else 0))
+    bwd_gbs = bwd_bytes / (bwd_ms * 1e-3) / 1e9
+
+    out = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": dname,
+        "data": "synthetic (seeded; BASELINE.json distributions), random-init head weights",
+        "config": {"workload": f"{w.name} SpartonHead fwd+bwd", "B": w.B, "S": w.S, "D": w.D, "V": w.V,
+                   "global_batch": w.B, "seq_len": w.S, "use_bias": has_bias,
+                   "valid_tokens": valid_tokens, "parallelism": "none (1 GPU)"},
+        "roofline": {"bound": "mfma", "kernel": "sparton_fwd_kernel", "achieved": round(fwd_tflops, 2),
+                     "peak": peak_tf, "unit": "TFLOP/s", "frac": round(fwd_tflops / peak_tf, 4),
+                     "traffic": None, "flops_per_launch": useful_flops,
+                     "flops_basis": "useful: 2*D*V*valid_tokens (fully masked 32-row blocks are skipped)",
+                     "dense_equiv_tflops": round(dense_flops / (fwd_ms * 1e-3) / 1e12, 2),
+                     "mean_ms": round(fwd_ms, 4)},
+        "bwd_roofline": {"bound": "hbm", "achieved": round(bwd_gbs, 1), "peak": PEAK_HBM_GBS,
+                         "unit": "GB/s", "frac": round(bwd_gbs / PEAK_HBM_GBS, 4),
+                         "bytes_per_call": bwd_bytes, "nnz": nnz, "U_W": u_w, "U_H": u_h,
+                         "mean_ms": round(bwd_ms, 4)},
+        "fwd_ms": round(fwd_ms, 4),
+        "encode_ms": round(enc_ms, 4),
+        "bwd_ms": round(bwd_ms, 4),
+        "fwd_tokens_per_s": round(tokens / (fwd_ms * 1e-3), 1),
+        "encode_tokens_per_s": round(tokens / (enc_ms * 1e-3), 1),
+        "peak_gb": round(peak_bytes / 1e9, 4),
+        "peak_extra_gb": round((peak_bytes - input_bytes) / 1e9, 4),
+        "bsv_logits_gb_avoided": round(w.B * w.S * w.V * e / 1e9, 3),
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu_baseline and int(os.environ.get("RANK", "0")) == 0:
+        out["cpu_baseline"] = cpu_baseline(torch, w, inp_cpu, args.cpu_seconds)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,120 @@
+/*
+ * sparton.h -- C ABI of libsparton_hip.so, the MI355X (gfx950) implementation of
+ * the SpartonHead forward and backward.
+ *
+ * Math (every entry point below computes exactly this):
+ *   x[b,s,v]   = (sum_d H[b,s,d] * W[v,d] + bias[v]) * mask[b,s]
+ *   M[b,v]     = max(0, max_s x[b,s,v])
+ *   I[b,v]     = lowest s with x[b,s,v] == M[b,v] if M[b,v] > 0, else 0
+ *   reps[b,v]  = log1p(M[b,v])
+ *   g'[b,v]    = G[b,v] * exp(-reps[b,v]) * mask[b, I[b,v]]  if reps[b,v] > 0, else 0
+ *   dbias[v]   = sum_b g'[b,v]
+ *   dW[v,:]    = sum_b g'[b,v] * H[b, I[b,v], :]
+ *   dH[b,s,:]  = sum_{v : I[b,v] == s} g'[b,v] * W[v,:]
+ *
+ * Conventions:
+ *   - Every pointer is a device pointer owned by the caller; no entry point allocates,
+ *     frees or synchronises. Work is enqueued on `stream` (a hipStream_t, passed as
+ *     void* so this header does not need the HIP headers; NULL = the null stream).
+ *   - Tensors are dense row-major with unit inner stride and 16-byte aligned bases:
+ *     H [B,S,D], W [V,D], bias [V], mask [B,S], reps/grad [B,V], argmax [B,V] int32,
+ *     d_hidden [B,S,D] fp32, d_weight [V,D] fp32, d_bias [V] fp32.
+ *   - `dtype` (enum sparton_dtype) is the element type of H, W, bias, reps and grad.
+ *   - D must be a multiple of 8 (16-bit dtypes) or 4 (fp32).
+ *   - Return value: 0 on success, < 0 for an invalid argument (nothing is launched),
+ *     > 0 is the hipError_t of a failed launch. sparton_strerror() names each code.
+ *   - Calls are reentrant; the library has no mutable global state.
+ */
+#ifndef SPARTON_H
+#define SPARTON_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum sparton_dtype {
+  SPARTON_F32 = 0,
+  SPARTON_BF16 = 1,
+  SPARTON_F16 = 2,
+};
+
+/* Element type of the attention mask. Any nonzero value takes part in the
+ * multiply; a tokenizer mask is int64 0/1. */
+enum sparton_mask_dtype {
+  SPARTON_MASK_I64 = 0,
+  SPARTON_MASK_I32 = 1,
+  SPARTON_MASK_U8 = 2, /* torch.bool / uint8 */
+  SPARTON_MASK_F32 = 3,
+  SPARTON_MASK_BF16 = 4,
+  SPARTON_MASK_F16 = 5,
+};
+
+enum sparton_status {
+  SPARTON_OK = 0,
+  SPARTON_EINVAL = -1,       /* null pointer, bad shape or bad enum value */
+  SPARTON_EALIGN = -2,       /* a base pointer is not 16-byte aligned */
+  SPARTON_EUNSUPPORTED = -3, /* shape outside the supported range (see sparton_limits) */
+  SPARTON_EWORKSPACE = -4,   /* workspace missing or smaller than sparton_bwd_workspace_bytes */
+};
+
+/*
+ * Forward: reps[B,V] (in `dtype`) and argmax I[B,V] (int32).
+ * `argmax` may be NULL: the inference-only variant then skips the index store.
+ * `bias` may be NULL (use_bias=False).
+ *
+ * Replaces the reference's forward path: fused_sparton_fwd_with_indices
+ * (src/sparton/sparton_kernel.py:226-253), its V-tile GEMM (:204-210) and the
+ * reduce kernel reduce_seq_max_log1p_relu_kernel_with_indices (:85-168); called where
+ * the custom op sparton::fused_sparton_fwd calls it (:651). With argmax == NULL it
+ * replaces the no-index variant fused_sparton_fwd (:372-394, kernel :262-334).
+ * The [B,S,V] logits are never written to memory.
+ */
+int sparton_fwd(const void* hidden, const void* weight, const void* bias,
+                const void* mask, int mask_dtype, void* reps, int32_t* argmax,
+                int64_t B, int64_t S, int64_t D, int64_t V, int dtype,
+                void* stream);
+
+/*
+ * Bytes of device scratch sparton_bwd needs for these sizes (256-byte aligned
+ * sections: per-chunk histograms, segment offsets and the bucketed entry list).
+ * No counterpart in the reference: its backward needs no scratch because it
+ * accumulates with atomics into zero-filled outputs (sparton_kernel.py:676-678).
+ */
+size_t sparton_bwd_workspace_bytes(int64_t B, int64_t S, int64_t D, int64_t V);
+
+/*
+ * Backward: d_hidden, d_weight, d_bias (fp32) from grad_reps [B,V] (`dtype`).
+ * Every element of each non-NULL output is written (no zero-fill needed); a NULL
+ * output is skipped. `mask` is read to apply mask[b, I[b,v]] (1 for a 0/1 mask).
+ * Deterministic: no atomics on floating-point data; every output row is summed in
+ * a fixed order (dW and dbias over b ascending, dH over v ascending).
+ *
+ * Replaces fused_sparton_bwd_with_bias (src/sparton/sparton_kernel.py:567-597), the
+ * kernel fused_sparton_bwd_kernel_with_bias (:473-565) and the zeros_like of the
+ * outputs (:676-678); called where the custom op sparton::fused_sparton_bwd calls it
+ * (:680). Unlike the reference it also runs when bias is absent (d_bias == NULL).
+ */
+int sparton_bwd(const void* grad_reps, const void* reps, const int32_t* argmax,
+                const void* mask, int mask_dtype, const void* hidden,
+                const void* weight, float* d_hidden, float* d_weight,
+                float* d_bias, void* workspace, size_t workspace_bytes,
+                int64_t B, int64_t S, int64_t D, int64_t V, int dtype,
+                void* stream);
+
+/* Static, thread-safe description of a status code. */
+const char* sparton_strerror(int code);
+
+/* Supported ranges: writes max S and max B of the backward. */
+void sparton_limits(int64_t* max_bwd_seq, int64_t* max_bwd_batch);
+
+/* ABI version of this header (bumped on any signature change). */
+int sparton_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SPARTON_H */

@@ -1,0 +1,81 @@
+// Shared device helpers for the SpartonHead HIP kernels (gfx950 / CDNA4, wave64).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/sparton.h"
+
+namespace sparton {
+
+typedef __bf16 bf16;
+typedef _Float16 f16;
+
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
+typedef __attribute__((ext_vector_type(8))) _Float16 f16x8;
+typedef __attribute__((ext_vector_type(4))) __bf16 bf16x4;
+typedef __attribute__((ext_vector_type(4))) _Float16 f16x4;
+typedef __attribute__((ext_vector_type(16))) float f32x16;
+typedef __attribute__((ext_vector_type(4))) float f32x4;
+typedef __attribute__((ext_vector_type(4))) uint32_t u32x4;
+typedef __attribute__((ext_vector_type(2))) uint32_t u32x2;
+
+constexpr int kWave = 64;
+
+__device__ __forceinline__ float to_f32(float x) { return x; }
+__device__ __forceinline__ float to_f32(bf16 x) { return (float)x; }
+__device__ __forceinline__ float to_f32(f16 x) { return (float)x; }
+
+template <typename T> __device__ __forceinline__ T from_f32(float x);
+template <> __device__ __forceinline__ float from_f32<float>(float x) { return x; }
+template <> __device__ __forceinline__ bf16 from_f32<bf16>(float x) { return (bf16)x; }
+template <> __device__ __forceinline__ f16 from_f32<f16>(float x) { return (f16)x; }
+
+// Mask element (b,s) as float, whatever its storage type. `mask_dtype` is uniform
+// across the launch, so the switch is a uniform branch.
+__device__ __forceinline__ float load_mask(const void* mask, int mask_dtype, int64_t off) {
+  switch (mask_dtype) {
+    case SPARTON_MASK_I64: return (float)((const int64_t*)mask)[off];
+    case SPARTON_MASK_I32: return (float)((const int32_t*)mask)[off];
+    case SPARTON_MASK_U8: return (float)((const uint8_t*)mask)[off];
+    case SPARTON_MASK_F32: return ((const float*)mask)[off];
+    case SPARTON_MASK_BF16: return (float)((const bf16*)mask)[off];
+    default: return (float)((const f16*)mask)[off];
+  }
+}
+
+// Four consecutive elements of a row as float (8-byte load for 16-bit types,
+// 16-byte load for fp32). `p` must be aligned to 4 elements.
+__device__ __forceinline__ f32x4 load4(const float* p) { return *(const f32x4*)p; }
+__device__ __forceinline__ f32x4 load4(const bf16* p) {
+  bf16x4 v = *(const bf16x4*)p;
+  return f32x4{(float)v[0], (float)v[1], (float)v[2], (float)v[3]};
+}
+__device__ __forceinline__ f32x4 load4(const f16* p) {
+  f16x4 v = *(const f16x4*)p;
+  return f32x4{(float)v[0], (float)v[1], (float)v[2], (float)v[3]};
+}
+
+// g'[b,v] of the backward: G * exp(-reps) * mask[b, I] where reps > 0, else 0.
+// Entries whose stored index lies outside [0, S) are treated as inactive, so a
+// corrupt index can never turn into an out-of-bounds access.
+// Follows src/sparton/sparton_kernel.py:531 (g' = where(reps>0, G*exp(-reps), 0));
+// the mask factor is the torch head's d x / d logits (training/model.py:60).
+template <typename T>
+__device__ __forceinline__ float grad_coeff(const T* grad, const T* reps, const int32_t* idx,
+                                            const void* mask, int mask_dtype, int64_t b,
+                                            int64_t S, int64_t off, int* s_out) {
+  const float r = to_f32(reps[off]);
+  const int s = idx[off];
+  *s_out = s;
+  if (!(r > 0.0f) || s < 0 || (int64_t)s >= S) return 0.0f;
+  const float g = to_f32(grad[off]);
+  if (g == 0.0f) return 0.0f;
+  const float m = load_mask(mask, mask_dtype, b * S + s);
+  return g * __expf(-r) * m;
+}
+
+__host__ __device__ constexpr int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+__host__ __device__ constexpr int64_t round_up(int64_t a, int64_t b) { return cdiv(a, b) * b; }
+
+}  // namespace sparton

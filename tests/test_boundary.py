@@ -1,0 +1,186 @@
+"""CPU checks of the drop-in boundary: the C-ABI library, the Python ops and the
+SpartonHead module surface. Nothing here launches a kernel."""
+import ctypes
+import os
+import re
+import subprocess
+import sys
+
+import pytest
+import torch
+
+import sparton
+import sparton_amd
+from sparton_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "sparton.h")
+
+
+def header_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(sparton_[a-z_]+)\s*\(", text)))
+
+
+def test_library_is_built_and_exports_every_declared_symbol():
+    L = _lib.load()
+    declared = header_functions()
+    assert set(declared) == set(_lib.EXPORTED_SYMBOLS)
+    for name in declared:
+        assert hasattr(L, name), name
+    nm = subprocess.run(["nm", "-D", "--defined-only", _lib.lib_path()], capture_output=True, text=True)
+    exported = {ln.split()[-1] for ln in nm.stdout.splitlines() if " T " in ln}
+    assert exported == set(declared), exported ^ set(declared)
+
+
+def test_host_side_entry_points():
+    L = _lib.load()
+    assert L.sparton_abi_version() == _lib.ABI_VERSION
+    assert L.sparton_strerror(0) == b"success"
+    for code in (-1, -2, -3, -4, 7, -99):
+        assert len(L.sparton_strerror(code)) > 0
+    max_s, max_b = _lib.limits()
+    assert max_s >= 4096 and max_b >= 1024
+    ws = L.sparton_bwd_workspace_bytes(32, 256, 768, 30522)
+    assert ws % 256 == 0 and ws >= 32 * 30522 * 8 + 2 * 32 * 256 * 4
+    assert L.sparton_bwd_workspace_bytes(0, 256, 768, 30522) == 0
+
+
+# Argument checks that return before any HIP call (fake, never-dereferenced pointers).
+P = 0x10000  # 16-byte aligned dummy address
+
+
+def fwd(**kw):
+    a = dict(hidden=P, weight=P, bias=None, mask=P, mask_dtype=0, reps=P, argmax=P,
+             B=2, S=4, D=64, V=10, dtype=1, stream=None)
+    a.update(kw)
+    return _lib.load().sparton_fwd(*a.values())
+
+
+def bwd(**kw):
+    a = dict(grad=P, reps=P, argmax=P, mask=P, mask_dtype=0, hidden=P, weight=P, dH=P, dW=P,
+             db=None, ws=None, ws_bytes=0, B=2, S=4, D=64, V=10, dtype=1, stream=None)
+    a.update(kw)
+    return _lib.load().sparton_bwd(*a.values())
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(B=-1), -1), (dict(dtype=3), -1), (dict(mask_dtype=6), -1), (dict(hidden=None), -1),
+    (dict(D=60), -1), (dict(D=4, dtype=1), -1), (dict(hidden=P + 8), -2), (dict(weight=P + 4), -2),
+    (dict(B=0), 0), (dict(V=0), 0),
+])
+def test_fwd_argument_validation(kw, code):
+    assert fwd(**kw) == code
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(S=-2), -1), (dict(dtype=-1), -1), (dict(grad=None), -1), (dict(weight=None), -1),
+    (dict(D=12), -1), (dict(dH=P + 4), -2), (dict(ws=None), -4), (dict(ws=P, ws_bytes=16), -4),
+    (dict(S=1 << 20), -3), (dict(B=1 << 20), -3), (dict(dH=None, dW=None, db=None), 0),
+])
+def test_bwd_argument_validation(kw, code):
+    assert bwd(**kw) == code
+
+
+def test_strerror_from_python_check():
+    with pytest.raises(RuntimeError, match="invalid argument"):
+        _lib.check(-1, "x")
+
+
+def test_missing_library_fails_loudly():
+    code = ("import os, torch, sparton_amd.ops as o\n"
+            "h=torch.zeros(1,1,8,dtype=torch.bfloat16,device='meta')\n"
+            "from sparton_amd import _lib\n"
+            "try:\n    _lib.load()\nexcept RuntimeError as e:\n    print('RAISED', e)\n")
+    env = dict(os.environ, SPARTON_HIP_LIB="/nonexistent/libsparton_hip.so", PYTHONPATH=ROOT)
+    out = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, env=env, cwd=ROOT)
+    assert "RAISED" in out.stdout and "python -m sparton_amd.build" in out.stdout, out.stderr
+
+
+def test_product_never_imports_oracle():
+    pkg = os.path.join(ROOT, "sparton_amd")
+    for dirpath, _, files in os.walk(pkg):
+        for f in files:
+            if f.endswith(".py"):
+                src = open(os.path.join(dirpath, f)).read()
+                assert not re.search(r"^\s*(from|import)\s+oracle", src, re.M), f
+
+
+# ---- Python ops and module (CPU / meta tensors only) ----------------------------------
+
+def test_ops_reject_cpu_tensors_like_reference_assert():
+    H = torch.zeros(2, 4, 8)
+    W = torch.zeros(10, 8)
+    m = torch.ones(2, 4, dtype=torch.long)
+    with pytest.raises(RuntimeError, match="only supports ROCm/HIP device"):
+        torch.ops.sparton.fused_sparton_fwd(H, W, None, m)
+    with pytest.raises(RuntimeError, match="only supports ROCm/HIP device"):
+        torch.ops.sparton.fused_sparton_encode(H, W, None, m)
+
+
+@pytest.mark.parametrize("bad", ["hidden_rank", "dim", "bias", "mask", "dtype", "D"])
+def test_ops_validate_shapes(bad):
+    from sparton_amd.ops import _validate
+    H, W, b, m = torch.zeros(2, 4, 16), torch.zeros(10, 16), torch.zeros(10), torch.ones(2, 4)
+    if bad == "hidden_rank":
+        H = H[0]
+    elif bad == "dim":
+        W = torch.zeros(10, 8)
+    elif bad == "bias":
+        b = torch.zeros(9)
+    elif bad == "mask":
+        m = torch.ones(2, 5)
+    elif bad == "dtype":
+        W = W.double()
+    elif bad == "D":
+        H, W = torch.zeros(2, 4, 6), torch.zeros(10, 6)
+    with pytest.raises((ValueError, TypeError)):
+        _validate(H, W, b, m, "op")
+
+
+def test_fake_kernels_give_reference_metadata():
+    from torch._subclasses.fake_tensor import FakeTensorMode
+    with FakeTensorMode():
+        H = torch.empty(3, 5, 16, dtype=torch.bfloat16)
+        W = torch.empty(40, 16, dtype=torch.bfloat16)
+        b = torch.empty(40, dtype=torch.bfloat16)
+        m = torch.empty(3, 5, dtype=torch.long)
+        r, i = torch.ops.sparton.fused_sparton_fwd(H, W, b, m)
+        assert r.shape == (3, 40) and r.dtype == torch.bfloat16 and i.dtype == torch.int32
+        e = torch.ops.sparton.fused_sparton_encode(H, W, None, m)
+        assert e.shape == (3, 40)
+        dh, dw, db = torch.ops.sparton.fused_sparton_bwd(r, r, i, H, W, b, m)
+        assert dh.shape == H.shape and dw.shape == W.shape and db.shape == (40,)
+        assert dh.dtype == dw.dtype == db.dtype == torch.float32
+        _, _, db0 = torch.ops.sparton.fused_sparton_bwd(r, r, i, H, W, None, m)
+        assert db0.shape == (0,)
+
+
+def test_module_surface_matches_reference():
+    assert sparton.SpartonHead is sparton_amd.SpartonHead
+    h = sparton.SpartonHead(50, 16, use_bias=True)
+    assert h.weight.shape == (50, 16) and h.bias.shape == (50,)
+    assert sorted(dict(h.named_parameters())) == ["bias", "weight"]
+    bound = 1 / 16 ** 0.5
+    assert h.bias.abs().max() <= bound and h.weight.abs().max() <= bound  # kaiming_uniform(a=sqrt 5)
+    h2 = sparton.SpartonHead(50, 16)
+    assert h2.bias is None and list(dict(h2.named_parameters())) == ["weight"]
+
+
+def test_tie_weights_aliases_decoder_and_load_copies():
+    dec = torch.nn.Linear(16, 50)
+    h = sparton.SpartonHead(dec.out_features, dec.in_features, use_bias=True)
+    h.tie_weights(dec)
+    assert h.weight is dec.weight and h.bias is dec.bias
+    h3 = sparton.SpartonHead(50, 16, use_bias=True)
+    w, b = torch.randn(50, 16), torch.randn(50)
+    h3.load({"weight": w, "bias": b})
+    assert torch.equal(h3.weight.data, w) and torch.equal(h3.bias.data, b)
+
+
+def test_c_header_compiles_as_c():
+    src = os.path.join(ROOT, "include", "sparton.h")
+    out = subprocess.run(["gcc", "-std=c99", "-Wall", "-Werror", "-fsyntax-only", "-x", "c", src],
+                         capture_output=True, text=True)
+    assert out.returncode == 0, out.stderr

@@ -1,0 +1,298 @@
+"""GPU parity: the HIP kernels (through the C ABI via the torch ops) against the CPU
+oracle on identical, seeded, already-rounded inputs. Every test prints its case
+before touching the GPU."""
+import glob
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+import sparton
+from sparton_amd import _lib
+from sparton_amd.workloads import WORKLOADS, make_inputs
+from _parity import BWD_TOL, F64, FWD_TOL, check_bwd_isolated, check_fwd, say
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = sorted(glob.glob(os.path.join(os.path.dirname(__file__), "golden", "*.npz")))
+DTYPES = {"fp32": torch.float32, "bf16": torch.bfloat16, "fp16": torch.float16}
+
+
+def run_fwd_bwd(H, W, b, m, G, device):
+    Hd, Wd, md, Gd = H.to(device), W.to(device), m.to(device), G.to(device)
+    bd = None if b is None else b.to(device)
+    reps, idx = torch.ops.sparton.fused_sparton_fwd(Hd, Wd, bd, md)
+    dH, dW, db = torch.ops.sparton.fused_sparton_bwd(Gd, reps, idx, Hd, Wd, bd, md)
+    torch.cuda.synchronize()
+    return reps, idx, dH, dW, db
+
+
+@pytest.mark.parametrize("dt", list(DTYPES))
+@pytest.mark.parametrize("path", GOLDEN, ids=[os.path.basename(p)[:-4] for p in GOLDEN])
+def test_golden_fixture_exact_argmax(path, dt, device):
+    """Inputs are exact in every dtype and all partial sums are exact in fp32, so the
+    argmax must match exactly, ties included (lowest s)."""
+    z = np.load(path)
+    t = {k: torch.from_numpy(z[k]) for k in z.files}
+    dtype = DTYPES[dt]
+    H, W = t["hidden"].to(dtype), t["weight"].to(dtype)
+    b = t["bias"].to(dtype) if "bias" in t else None
+    m, G = t["mask"].to(torch.float32), t["grad"].to(dtype)
+    say(f"golden {os.path.basename(path)} {dt} B,S,D,V={tuple(H.shape)}+{W.shape[0]}")
+    reps, idx, dH, dW, db = run_fwd_bwd(H, W, b, m, G, device)
+    assert torch.equal(idx.cpu().long(), t["I"])
+    torch.testing.assert_close(reps.cpu().to(F64), t["reps"], **FWD_TOL)
+    torch.testing.assert_close(dH.cpu().to(F64), t["dH"], **FWD_TOL)
+    torch.testing.assert_close(dW.cpu().to(F64), t["dW"], **FWD_TOL)
+    if b is not None:
+        torch.testing.assert_close(db.cpu().to(F64), t["dbias"], **FWD_TOL)
+    check_bwd_isolated(H, W, b, m, G, reps, idx, dH, dW, db)
+
+
+CASES = [
+    # dtype, B, S, D, V, bias, mask kind
+    ("bf16", 3, 77, 64, 1000, True, "int64"),
+    ("fp16", 2, 300, 128, 777, False, "bool"),
+    ("fp32", 2, 40, 96, 513, True, "frac"),
+    ("bf16", 1, 600, 256, 300, True, "int32"),
+    ("bf16", 4, 1, 32, 100, True, "int64"),
+    ("bf16", 2, 256, 768, 4099, True, "holes"),
+    ("fp16", 3, 33, 16, 70, True, "f16"),
+    ("fp32", 1, 5, 4, 1, False, "int64"),
+]
+
+
+def make_case(dt, B, S, D, V, bias, mk, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    dtype = DTYPES[dt]
+    H = torch.randn(B, S, D, generator=g).to(dtype)
+    W = (torch.randn(V, D, generator=g) * (1.0 / D ** 0.5)).to(dtype)
+    b = (torch.randn(V, generator=g) * 0.1 - 0.2).to(dtype) if bias else None
+    lens = torch.randint(1, S + 1, (B,), generator=g)
+    pad = torch.arange(S)[None] < lens[:, None]
+    if mk == "int64":
+        m = pad.long()
+    elif mk == "int32":
+        m = pad.int()
+    elif mk == "bool":
+        m = pad
+    elif mk == "holes":
+        m = (torch.rand(B, S, generator=g) < 0.5).long()
+        m[0] = 0                                                   # an all-masked row
+    elif mk == "frac":
+        m = torch.randint(0, 3, (B, S), generator=g).float() * 0.5
+    elif mk == "f16":
+        m = pad.half()
+    G = torch.rand(B, V, generator=g).to(dtype) * (torch.rand(B, V, generator=g) < 0.3)
+    return H, W, b, m, G
+
+
+@pytest.mark.parametrize("case", CASES, ids=["-".join(map(str, c)) for c in CASES])
+def test_random_shapes(case, device):
+    say(f"random case {case}")
+    H, W, b, m, G = make_case(*case)
+    reps, idx, dH, dW, db = run_fwd_bwd(H, W, b, m, G, device)
+    n, bad = check_fwd(H, W, b, m, reps, idx)
+    say(f"  checked {n} entries, {bad} near-tie argmax differences")
+    check_bwd_isolated(H, W, b, m, G, reps, idx, dH, dW, db)
+
+
+def sample_cols(V, n=1024, tail=64, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    cols = torch.randperm(V, generator=g)[:n]
+    return torch.unique(torch.cat([cols, torch.arange(max(0, V - tail), V)]))
+
+
+@pytest.mark.parametrize("cfg", [1, 2, 3, 4, 5])
+def test_baseline_config_full_size(cfg, device):
+    w = WORKLOADS[cfg]
+    say(f"config {cfg} {w.name} B={w.B} S={w.S} D={w.D} V={w.V} {w.dtype}")
+    inp = make_inputs(w)
+    H, W, b, m, G = inp.hidden, inp.weight, inp.bias, inp.mask, inp.grad
+    reps, idx, dH, dW, db = run_fwd_bwd(H, W, b, m, G, device)
+    cols = None if cfg == 1 else sample_cols(w.V)
+    n, bad = check_fwd(H, W, b, m, reps, idx, cols)
+    say(f"  fwd: checked {n} entries, {bad} near-tie argmax differences")
+    # Backward: dH in full, dW/dbias on the sampled rows (all rows for config 1).
+    reps_c, idx_c = reps.cpu(), idx.cpu()
+    rH, _, rb = oracle.fused_bwd_ref(G, reps_c, idx_c, H, W, b is not None, m, with_dW=False)
+    torch.testing.assert_close(dH.cpu().to(F64), rH, **BWD_TOL)
+    if cols is None:
+        cols = torch.arange(w.V)
+    _, rW, _ = oracle.fused_bwd_ref(G[:, cols], reps_c[:, cols], idx_c[:, cols], H, W[cols],
+                                      b is not None, m)
+    torch.testing.assert_close(dW[cols.to(device)].cpu().to(F64), rW, **BWD_TOL)
+    if b is not None:
+        torch.testing.assert_close(db.cpu().to(F64), rb, **BWD_TOL)
+    # Size-independent identities over every row, with a library GEMM on the GPU:
+    # sum_s dH[b,s,:] == G' W  and  dbias == sum_b G'.
+    gp = oracle.grad_coeff(G, reps_c, idx_c, m, acc=torch.float32).to(device)
+    Wf = W.to(device).float()
+    torch.testing.assert_close(dH.sum(1), gp @ Wf, rtol=1e-3, atol=1e-4)
+    if b is not None:
+        torch.testing.assert_close(db, gp.sum(0), rtol=1e-4, atol=1e-5)
+    say(f"  bwd: nnz={int((gp != 0).sum())} ok")
+
+
+def test_deterministic_repeat(device):
+    w = WORKLOADS[2]
+    say("determinism, config 2 twice")
+    inp = make_inputs(w).to(device)
+    outs = []
+    for _ in range(2):
+        r, i = torch.ops.sparton.fused_sparton_fwd(inp.hidden, inp.weight, inp.bias, inp.mask)
+        dh, dw, db = torch.ops.sparton.fused_sparton_bwd(inp.grad, r, i, inp.hidden, inp.weight,
+                                                         inp.bias, inp.mask)
+        outs.append([t.clone() for t in (r, i, dh, dw, db)])
+    torch.cuda.synchronize()
+    for a, c in zip(*outs):
+        assert torch.equal(a, c)
+
+
+def test_encode_equals_training_forward(device):
+    say("encode vs fwd, config 3 shape")
+    inp = make_inputs(WORKLOADS[3]).to(device)
+    r, _ = torch.ops.sparton.fused_sparton_fwd(inp.hidden, inp.weight, inp.bias, inp.mask)
+    e = torch.ops.sparton.fused_sparton_encode(inp.hidden, inp.weight, inp.bias, inp.mask)
+    assert torch.equal(r, e)
+    head = sparton.SpartonHead(inp.weight.shape[0], inp.weight.shape[1], use_bias=True).to(device)
+    with torch.no_grad():
+        head.weight.copy_(inp.weight.float())
+        head.bias.copy_(inp.bias.float())
+        out = head.to(torch.float16)(inp.hidden, inp.mask)
+    assert torch.equal(out, e)
+
+
+def test_no_bsv_allocation(device):
+    w = WORKLOADS[2]
+    say("peak memory, config 2")
+    inp = make_inputs(w).to(device)
+    torch.cuda.synchronize()
+    torch.cuda.reset_peak_memory_stats()
+    base = torch.cuda.memory_allocated()
+    r, i = torch.ops.sparton.fused_sparton_fwd(inp.hidden, inp.weight, inp.bias, inp.mask)
+    dh, dw, db = torch.ops.sparton.fused_sparton_bwd(inp.grad, r, i, inp.hidden, inp.weight, inp.bias, inp.mask)
+    torch.cuda.synchronize()
+    peak = torch.cuda.max_memory_allocated() - base
+    bsv = w.B * w.S * w.V * 2
+    say(f"  peak extra {peak / 2**20:.1f} MiB vs [B,S,V] bf16 {bsv / 2**20:.1f} MiB")
+    outputs = (w.B * w.V * 6 + w.B * w.S * w.D * 4 + w.V * w.D * 4 + w.V * 4)
+    assert peak < bsv / 2
+    assert peak <= outputs + _lib.load().sparton_bwd_workspace_bytes(w.B, w.S, w.D, w.V) + (8 << 20)
+
+
+@pytest.mark.parametrize("use_bias", [True, False])
+def test_head_autograd_matches_torch_head(use_bias, device):
+    """End to end through SpartonHead + autograd vs the repo's torch head in fp32."""
+    say(f"SpartonHead autograd vs torch head, bias={use_bias}")
+    B, S, D, V = 4, 96, 128, 3000
+    g = torch.Generator().manual_seed(5)
+    H = torch.randn(B, S, D, generator=g).bfloat16()
+    dec = torch.nn.Linear(D, V, bias=use_bias)
+    with torch.no_grad():
+        dec.weight.copy_(torch.randn(V, D, generator=g) * 0.05)
+        if use_bias:
+            dec.bias.copy_(torch.randn(V, generator=g) * 0.1 - 0.2)
+    dec = dec.bfloat16()
+    Wc = dec.weight.detach().clone()
+    bc = dec.bias.detach().clone() if use_bias else None
+    lens = torch.randint(8, S + 1, (B,), generator=g)
+    m = (torch.arange(S)[None] < lens[:, None]).long()
+    G = torch.rand(B, V, generator=g).bfloat16()
+    # torch head in fp32 on the same rounded values (CPU)
+    Hr = H.float().requires_grad_()
+    Wr = Wc.float().requires_grad_()
+    br = bc.float().requires_grad_() if use_bias else None
+    ref = oracle.torch_head(Hr, Wr, br, m)
+    ref.backward(G.float())
+    # SpartonHead tied to the decoder, as training/model.py:77-80 does
+    decd = dec.to(device)
+    head = sparton.SpartonHead(decd.out_features, decd.in_features, use_bias=use_bias).to(device)
+    head.tie_weights(decd)
+    Hd = H.to(device).requires_grad_()
+    out = head(Hd, m.to(device))
+    out.backward(G.to(device))
+    torch.testing.assert_close(out.detach().cpu().float(), ref.detach(), **FWD_TOL)
+    # rows an argmax near-tie could move are excluded from the gradient comparison
+    _, I, _ = oracle.fused_fwd_ref(H, Wc, bc, m)
+    _, idx = torch.ops.sparton.fused_sparton_fwd(Hd.detach(), decd.weight.detach(),
+                                                 decd.bias.detach() if use_bias else None, m.to(device))
+    idx = idx.cpu().long()
+    moved = idx != I
+    say(f"  near-tie moved entries: {int(moved.sum())}")
+    vok = ~moved.any(0)
+    hok = torch.ones(B, S, dtype=torch.bool)
+    for bb, vv in moved.nonzero().tolist():
+        hok[bb, I[bb, vv]] = False
+        hok[bb, idx[bb, vv]] = False
+    torch.testing.assert_close(decd.weight.grad.cpu().float()[vok], Wr.grad[vok], **FWD_TOL)
+    torch.testing.assert_close(Hd.grad.cpu().float()[hok], Hr.grad[hok], **FWD_TOL)
+    if use_bias:
+        torch.testing.assert_close(decd.bias.grad.cpu().float()[vok], br.grad[vok], **FWD_TOL)
+    assert Hd.grad.dtype == torch.bfloat16 and decd.weight.grad.dtype == torch.bfloat16
+
+
+def test_edge_cases(device):
+    say("edge cases")
+    # empty sequence: every rep is 0 and every index 0
+    H = torch.zeros(2, 0, 16, dtype=torch.bfloat16, device=device)
+    W = torch.randn(40, 16, device=device).bfloat16()
+    m = torch.zeros(2, 0, dtype=torch.long, device=device)
+    r, i = torch.ops.sparton.fused_sparton_fwd(H, W, None, m)
+    assert torch.all(r == 0) and torch.all(i == 0)
+    # non-multiple-of-8 hidden size goes through SpartonHead's zero padding
+    B, S, D, V = 2, 9, 20, 50
+    H = torch.randn(B, S, D).bfloat16()
+    head = sparton.SpartonHead(V, D, use_bias=True)
+    m = torch.ones(B, S, dtype=torch.long)
+    with torch.no_grad():
+        ref = oracle.torch_head(H.float(), head.weight.bfloat16().float(), head.bias.bfloat16().float(), m)
+        out = head.to(device).bfloat16()(H.to(device), m.to(device))
+    torch.testing.assert_close(out.cpu().float(), ref, **FWD_TOL)
+    # a mask on another dtype / non-contiguous hidden
+    H2 = torch.randn(5, 3, 32, device=device).bfloat16().transpose(0, 1)   # [3,5,32] non-contiguous
+    W2 = torch.randn(70, 32, device=device).bfloat16() * 0.2
+    m2 = torch.ones(3, 5, dtype=torch.bool, device=device)
+    r2, i2 = torch.ops.sparton.fused_sparton_fwd(H2, W2, None, m2)
+    M, I, ref2 = oracle.fused_fwd_ref(H2.cpu(), W2.cpu(), None, m2.cpu())
+    torch.testing.assert_close(r2.cpu().to(F64), ref2, **FWD_TOL)
+
+
+def test_autocast_policy(device):
+    say("autocast bf16 with fp32 parameters")
+    B, S, D, V = 2, 64, 64, 500
+    head = sparton.SpartonHead(V, D, use_bias=True).to(device)
+    H = torch.randn(B, S, D, device=device)
+    m = torch.ones(B, S, dtype=torch.long, device=device)
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        out = head(H, m)
+    assert out.dtype == torch.bfloat16
+    ref = oracle.torch_head(H.cpu().bfloat16().double(), head.weight.detach().cpu().bfloat16().double(),
+                            head.bias.detach().cpu().bfloat16().double(), m.cpu())
+    torch.testing.assert_close(out.cpu().double(), ref, **FWD_TOL)
+
+
+def test_opcheck_and_compile(device):
+    say("opcheck + torch.compile(aot_eager)")
+    B, S, D, V = 2, 16, 32, 100
+    H = torch.randn(B, S, D, device=device).bfloat16()
+    W = (torch.randn(V, D, device=device) * 0.2).bfloat16()
+    b = (torch.randn(V, device=device) * 0.1).bfloat16()
+    m = torch.ones(B, S, dtype=torch.long, device=device)
+    torch.library.opcheck(torch.ops.sparton.fused_sparton_fwd.default, (H, W, b, m),
+                          test_utils=("test_schema", "test_faketensor"))
+    head = sparton.SpartonHead(V, D, use_bias=True).to(device).bfloat16()
+
+    def f(h, mm):
+        return head(h, mm).float().sum()
+
+    cf = torch.compile(f, backend="aot_eager", fullgraph=True)
+    Hc = H.clone().requires_grad_()
+    y = cf(Hc, m)
+    y.backward()
+    He = H.clone().requires_grad_()
+    ye = f(He, m)
+    ye.backward()
+    assert torch.equal(y, ye) and torch.equal(Hc.grad, He.grad)
