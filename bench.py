@@ -172,9 +172,10 @@ def main():
 
     # ---- per-kernel timing (HIP events, back-to-back launches) ----------------------
     Hd, Wd, bd = H.detach(), head.weight.detach(), (head.bias.detach() if has_bias else None)
-    fwd_ms = time_events(torch, lambda: torch.ops.sparton.fused_sparton_fwd(Hd, Wd, bd, mask), args.kernel_reps)
+    fwd_ms = time_events(torch, lambda: torch.ops.sparton.fused_sparton_fwd_train(Hd, Wd, bd, mask),
+                         args.kernel_reps)
     enc_ms = time_events(torch, lambda: torch.ops.sparton.fused_sparton_encode(Hd, Wd, bd, mask), args.kernel_reps)
-    reps, idx = torch.ops.sparton.fused_sparton_fwd(Hd, Wd, bd, mask)
+    _, idx, reps = torch.ops.sparton.fused_sparton_fwd_train(Hd, Wd, bd, mask)
     bwd_ms = time_events(torch, lambda: torch.ops.sparton.fused_sparton_bwd(G, reps, idx, Hd, Wd, bd, mask),
                          args.kernel_reps)
 
@@ -195,7 +196,8 @@ def main():
     u_w = int(act.any(0).sum())
     rows = (torch.arange(w.B, device=dev).view(-1, 1) * w.S + idx.long())[act]
     u_h = int(torch.unique(rows).numel())
-    bwd_bytes = (w.B * w.V * (e + e + 4) + u_w * w.D * e + u_h * w.D * e
+    # G (e bytes) + fp32 reps + int32 idx per (b,v), gathered rows, dense fp32 outputs
+    bwd_bytes = (w.B * w.V * (e + 4 + 4) + u_w * w.D * e + u_h * w.D * e
                  + w.B * w.S * w.D * 4 + w.V * w.D * 4 + (w.V * 4 if has_bias else 0))
     bwd_gbs = bwd_bytes / (bwd_ms * 1e-3) / 1e9
 

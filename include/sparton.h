@@ -63,6 +63,8 @@ enum sparton_status {
 /*
  * Forward: reps[B,V] (in `dtype`) and argmax I[B,V] (int32).
  * `argmax` may be NULL: the inference-only variant then skips the index store.
+ * `reps_f32` may be NULL; if given, it receives reps[B,V] unrounded in fp32, which a
+ * training caller keeps for the backward instead of the rounded `reps`.
  * `bias` may be NULL (use_bias=False).
  *
  * Replaces the reference's forward path: fused_sparton_fwd_with_indices
@@ -74,8 +76,8 @@ enum sparton_status {
  */
 int sparton_fwd(const void* hidden, const void* weight, const void* bias,
                 const void* mask, int mask_dtype, void* reps, int32_t* argmax,
-                int64_t B, int64_t S, int64_t D, int64_t V, int dtype,
-                void* stream);
+                float* reps_f32, int64_t B, int64_t S, int64_t D, int64_t V,
+                int dtype, void* stream);
 
 /*
  * Bytes of device scratch sparton_bwd needs for these sizes (256-byte aligned
@@ -87,6 +89,8 @@ size_t sparton_bwd_workspace_bytes(int64_t B, int64_t S, int64_t D, int64_t V);
 
 /*
  * Backward: d_hidden, d_weight, d_bias (fp32) from grad_reps [B,V] (`dtype`).
+ * `reps` is the forward's reps in `reps_dtype` (enum sparton_dtype): the rounded
+ * `dtype` output, as the reference saves it, or the fp32 `reps_f32` output.
  * Every element of each non-NULL output is written (no zero-fill needed); a NULL
  * output is skipped. `mask` is read to apply mask[b, I[b,v]] (1 for a 0/1 mask).
  * Deterministic: no atomics on floating-point data; every output row is summed in
@@ -97,8 +101,8 @@ size_t sparton_bwd_workspace_bytes(int64_t B, int64_t S, int64_t D, int64_t V);
  * outputs (:676-678); called where the custom op sparton::fused_sparton_bwd calls it
  * (:680). Unlike the reference it also runs when bias is absent (d_bias == NULL).
  */
-int sparton_bwd(const void* grad_reps, const void* reps, const int32_t* argmax,
-                const void* mask, int mask_dtype, const void* hidden,
+int sparton_bwd(const void* grad_reps, const void* reps, int reps_dtype,
+                const int32_t* argmax, const void* mask, int mask_dtype, const void* hidden,
                 const void* weight, float* d_hidden, float* d_weight,
                 float* d_bias, void* workspace, size_t workspace_bytes,
                 int64_t B, int64_t S, int64_t D, int64_t V, int dtype,

@@ -1,7 +1,7 @@
 // SpartonHead backward on gfx950: atomic-free, deterministic, HBM-bound.
 //
-// Only entries (b,v) with g'[b,v] != 0 carry gradient (g' = G*exp(-reps)*mask[b,I],
-// zero where reps == 0). The reference scatters them with fp32 atomics into
+// Only entries (b,v) with reps > 0, G != 0 and mask[b,I] != 0 carry gradient
+// (g' = G*exp(-reps)*mask[b,I]). The reference scatters them with fp32 atomics into
 // zero-filled dH/dW/dbias (src/sparton/sparton_kernel.py:473-565, :676-678). Here
 // every output row is produced by exactly one wave, summed in a fixed order:
 //
@@ -53,7 +53,8 @@ static int waves_for(int64_t S) { return S <= 4096 ? 4 : 1; }
 // ---- 1. histogram ----------------------------------------------------------
 template <typename T>
 __global__ __launch_bounds__(256) void bwd_hist_kernel(
-    const T* __restrict__ grad, const T* __restrict__ reps, const int32_t* __restrict__ idx,
+    const T* __restrict__ grad, const void* __restrict__ reps, int reps_dtype,
+    const int32_t* __restrict__ idx,
     const void* __restrict__ mask, int mask_dtype, int S, int V, int nch, int* __restrict__ hist) {
   int* lds = (int*)sparton_bwd_smem;
   const int wpb = blockDim.x >> 6, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -65,8 +66,9 @@ __global__ __launch_bounds__(256) void bwd_hist_kernel(
     const int vend = min(V, (c + 1) * CH);
     for (int v = c * CH + lane; v < vend; v += 64) {
       int s;
-      const float g = grad_coeff(grad, reps, idx, mask, mask_dtype, b, S, (int64_t)b * V + v, &s);
-      if (g != 0.0f) atomicAdd(&h[s], 1);
+      float g;
+      if (grad_entry(grad, reps, reps_dtype, idx, mask, mask_dtype, b, S, (int64_t)b * V + v, &g, &s))
+        atomicAdd(&h[s], 1);
     }
   }
   __syncthreads();
@@ -132,7 +134,8 @@ __global__ __launch_bounds__(256) void bwd_scan_kernel(int* __restrict__ hist, i
 // ---- 3. scatter ------------------------------------------------------------
 template <typename T>
 __global__ __launch_bounds__(256) void bwd_scatter_kernel(
-    const T* __restrict__ grad, const T* __restrict__ reps, const int32_t* __restrict__ idx,
+    const T* __restrict__ grad, const void* __restrict__ reps, int reps_dtype,
+    const int32_t* __restrict__ idx,
     const void* __restrict__ mask, int mask_dtype, int S, int V, int nch,
     const int* __restrict__ hist_base, int2* __restrict__ list) {
   int* lds = (int*)sparton_bwd_smem;
@@ -152,8 +155,8 @@ __global__ __launch_bounds__(256) void bwd_scatter_kernel(
     const int v = vs + lane;
     float g = 0.0f;
     int s = 0;
-    if (v < vend) g = grad_coeff(grad, reps, idx, mask, mask_dtype, b, S, (int64_t)b * V + v, &s);
-    const bool act = g != 0.0f;
+    const bool act =
+        v < vend && grad_entry(grad, reps, reps_dtype, idx, mask, mask_dtype, b, S, (int64_t)b * V + v, &g, &s);
     uint64_t pending = __ballot(act);
     while (pending) {
       const int leader = __ffsll((unsigned long long)pending) - 1;
@@ -202,7 +205,8 @@ __global__ __launch_bounds__(256) void bwd_dh_kernel(
 // ---- 5. dW and dbias ---------------------------------------------------------
 template <typename T>
 __global__ __launch_bounds__(256) void bwd_dw_kernel(
-    const T* __restrict__ grad, const T* __restrict__ reps, const int32_t* __restrict__ idx,
+    const T* __restrict__ grad, const void* __restrict__ reps, int reps_dtype,
+    const int32_t* __restrict__ idx,
     const void* __restrict__ mask, int mask_dtype, const T* __restrict__ H,
     float* __restrict__ dW, float* __restrict__ dbias, int B, int S, int D, int V, int vblk) {
   float* gp = (float*)sparton_bwd_smem;   // [B][vblk]
@@ -213,8 +217,8 @@ __global__ __launch_bounds__(256) void bwd_dw_kernel(
     const int bb = i / vblk, j = i - bb * vblk, v = v0 + j;
     float g = 0.0f;
     int s = 0;
-    if (v < V) g = grad_coeff(grad, reps, idx, mask, mask_dtype, bb, S, (int64_t)bb * V + v, &s);
-    gp[i] = g;
+    if (v < V) grad_entry(grad, reps, reps_dtype, idx, mask, mask_dtype, bb, S, (int64_t)bb * V + v, &g, &s);
+    gp[i] = g;   // 0 for inactive entries, which the gather loop skips
     si[i] = s;
   }
   __syncthreads();
@@ -245,11 +249,10 @@ __global__ __launch_bounds__(256) void bwd_dw_kernel(
 }
 
 template <typename T>
-static int launch(const void* grad, const void* reps, const int32_t* idx, const void* mask,
+static int launch(const void* grad, const void* r, int rdt, const int32_t* idx, const void* mask,
                   int mdt, const void* H, const void* W, float* dH, float* dW, float* dbias,
                   void* ws, int64_t B, int64_t S, int64_t D, int64_t V, hipStream_t st) {
   const T* g = (const T*)grad;
-  const T* r = (const T*)reps;
   if (dH != nullptr && B * S > 0 && D > 0) {
     const Layout L = layout(B, S, V);
     int* hist = (int*)((char*)ws + L.hist);
@@ -260,12 +263,12 @@ static int launch(const void* grad, const void* reps, const int32_t* idx, const 
     const dim3 cgrid((unsigned)cdiv(L.nch, wpb), (unsigned)B);
     const size_t cl = (size_t)wpb * S * 4;
     if (L.nch > 0)
-      hipLaunchKernelGGL(bwd_hist_kernel<T>, cgrid, dim3(64 * wpb), cl, st, g, r, idx, mask, mdt,
+      hipLaunchKernelGGL(bwd_hist_kernel<T>, cgrid, dim3(64 * wpb), cl, st, g, r, rdt, idx, mask, mdt,
                          (int)S, (int)V, (int)L.nch, hist);
     hipLaunchKernelGGL(bwd_scan_kernel, dim3((unsigned)B), dim3(256), (size_t)S * 4, st, hist,
                        seg_start, seg_cnt, (int)S, (int)L.nch);
     if (L.nch > 0)
-      hipLaunchKernelGGL(bwd_scatter_kernel<T>, cgrid, dim3(64 * wpb), cl, st, g, r, idx, mask,
+      hipLaunchKernelGGL(bwd_scatter_kernel<T>, cgrid, dim3(64 * wpb), cl, st, g, r, rdt, idx, mask,
                          mdt, (int)S, (int)V, (int)L.nch, (const int*)hist, list);
     hipLaunchKernelGGL(bwd_dh_kernel<T>, dim3((unsigned)cdiv(B * S, 4)), dim3(256), 0, st,
                        (const T*)W, (const int2*)list, (const int*)seg_start, (const int*)seg_cnt,
@@ -274,7 +277,7 @@ static int launch(const void* grad, const void* reps, const int32_t* idx, const 
   if ((dW != nullptr || dbias != nullptr) && V > 0) {
     const int vblk = B > 0 ? (int)std::min<int64_t>(VBLK_MAX, DW_LDS_ENTRIES / B) : VBLK_MAX;
     hipLaunchKernelGGL(bwd_dw_kernel<T>, dim3((unsigned)cdiv(V, vblk)), dim3(256),
-                       (size_t)B * vblk * 8, st, g, r, idx, mask, mdt, (const T*)H, dW, dbias,
+                       (size_t)B * vblk * 8, st, g, r, rdt, idx, mask, mdt, (const T*)H, dW, dbias,
                        (int)B, (int)S, (int)D, (int)V, vblk);
   }
   const hipError_t e = hipGetLastError();
@@ -293,12 +296,13 @@ extern "C" __attribute__((visibility("default"))) size_t sparton_bwd_workspace_b
 }
 
 extern "C" __attribute__((visibility("default"))) int sparton_bwd(
-    const void* grad_reps, const void* reps, const int32_t* argmax, const void* mask,
-    int mask_dtype, const void* hidden, const void* weight, float* d_hidden, float* d_weight,
-    float* d_bias, void* workspace, size_t workspace_bytes, int64_t B, int64_t S, int64_t D,
-    int64_t V, int dtype, void* stream) {
+    const void* grad_reps, const void* reps, int reps_dtype, const int32_t* argmax,
+    const void* mask, int mask_dtype, const void* hidden, const void* weight, float* d_hidden,
+    float* d_weight, float* d_bias, void* workspace, size_t workspace_bytes, int64_t B, int64_t S,
+    int64_t D, int64_t V, int dtype, void* stream) {
   if (B < 0 || S < 0 || D < 0 || V < 0) return SPARTON_EINVAL;
   if (dtype < SPARTON_F32 || dtype > SPARTON_F16) return SPARTON_EINVAL;
+  if (reps_dtype < SPARTON_F32 || reps_dtype > SPARTON_F16) return SPARTON_EINVAL;
   if (mask_dtype < SPARTON_MASK_I64 || mask_dtype > SPARTON_MASK_F16) return SPARTON_EINVAL;
   if (B * V > 0 && (grad_reps == nullptr || reps == nullptr || argmax == nullptr || mask == nullptr))
     return SPARTON_EINVAL;
@@ -323,13 +327,13 @@ extern "C" __attribute__((visibility("default"))) int sparton_bwd(
   float* dh = need_dh ? d_hidden : nullptr;
   switch (dtype) {
     case SPARTON_BF16:
-      return bwd::launch<bf16>(grad_reps, reps, argmax, mask, mask_dtype, hidden, weight, dh,
+      return bwd::launch<bf16>(grad_reps, reps, reps_dtype, argmax, mask, mask_dtype, hidden, weight, dh,
                                d_weight, d_bias, workspace, B, S, D, V, st);
     case SPARTON_F16:
-      return bwd::launch<f16>(grad_reps, reps, argmax, mask, mask_dtype, hidden, weight, dh,
+      return bwd::launch<f16>(grad_reps, reps, reps_dtype, argmax, mask, mask_dtype, hidden, weight, dh,
                               d_weight, d_bias, workspace, B, S, D, V, st);
     default:
-      return bwd::launch<float>(grad_reps, reps, argmax, mask, mask_dtype, hidden, weight, dh,
+      return bwd::launch<float>(grad_reps, reps, reps_dtype, argmax, mask, mask_dtype, hidden, weight, dh,
                                 d_weight, d_bias, workspace, B, S, D, V, st);
   }
 }

@@ -66,10 +66,12 @@ template <> struct Mfma<float> {
   // 4 floats per lane = four K=2 steps. Lane half h supplies k = 16h + 4p + j for
   // A and B alike, so every k of the slab is paired once.
   static __device__ __forceinline__ void run(const u32x4& a, const u32x4& b, f32x16& c) {
+    // __uint_as_float on the element value: a bit_cast of a vector-element lvalue
+    // would read element 0 every time.
 #pragma unroll
     for (int j = 0; j < 4; ++j)
-      c = __builtin_amdgcn_mfma_f32_32x32x2f32(__builtin_bit_cast(float, a[j]),
-                                               __builtin_bit_cast(float, b[j]), c, 0, 0, 0);
+      c = __builtin_amdgcn_mfma_f32_32x32x2f32(__uint_as_float(a[j]), __uint_as_float(b[j]), c,
+                                               0, 0, 0);
   }
 };
 
@@ -95,7 +97,8 @@ template <typename T>
 __global__ __launch_bounds__(NTHREADS, 1) void sparton_fwd_kernel(
     const T* __restrict__ H, const T* __restrict__ W, const T* __restrict__ bias,
     const void* __restrict__ mask, int mask_dtype, T* __restrict__ reps,
-    int32_t* __restrict__ argmax, int B, int S, int D, int V, int n_vt) {
+    int32_t* __restrict__ argmax, float* __restrict__ reps_f32, int B, int S, int D, int V,
+    int n_vt) {
   __shared__ Smem sm;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave / WAVES_N, wn = wave % WAVES_N;
@@ -258,21 +261,23 @@ __global__ __launch_bounds__(NTHREADS, 1) void sparton_fwd_kernel(
 #pragma unroll
       for (int w = 1; w < WAVES_M; ++w) merge(bv, bi, red_v[w * BN + tid], red_i[w * BN + tid]);
       const int64_t o = (int64_t)b * V + v;
-      reps[o] = from_f32<T>(log1pf(bv));
+      const float r = log1pf(bv);
+      reps[o] = from_f32<T>(r);
       if (argmax != nullptr) argmax[o] = bi;
+      if (reps_f32 != nullptr) reps_f32[o] = r;
     }
   }
 }
 
 template <typename T>
 static int launch(const void* H, const void* W, const void* bias, const void* mask,
-                  int mask_dtype, void* reps, int32_t* argmax, int64_t B, int64_t S,
-                  int64_t D, int64_t V, hipStream_t stream) {
+                  int mask_dtype, void* reps, int32_t* argmax, float* reps_f32, int64_t B,
+                  int64_t S, int64_t D, int64_t V, hipStream_t stream) {
   const int64_t n_vt = cdiv(V, BN);
   const int64_t grid = n_vt * B;
   hipLaunchKernelGGL(sparton_fwd_kernel<T>, dim3((unsigned)grid), dim3(NTHREADS), 0, stream,
                      (const T*)H, (const T*)W, (const T*)bias, mask, mask_dtype, (T*)reps,
-                     argmax, (int)B, (int)S, (int)D, (int)V, (int)n_vt);
+                     argmax, reps_f32, (int)B, (int)S, (int)D, (int)V, (int)n_vt);
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? SPARTON_OK : (int)e;
 }
@@ -284,8 +289,8 @@ using namespace sparton;
 
 extern "C" __attribute__((visibility("default"))) int sparton_fwd(
     const void* hidden, const void* weight, const void* bias, const void* mask,
-    int mask_dtype, void* reps, int32_t* argmax, int64_t B, int64_t S, int64_t D,
-    int64_t V, int dtype, void* stream) {
+    int mask_dtype, void* reps, int32_t* argmax, float* reps_f32, int64_t B, int64_t S,
+    int64_t D, int64_t V, int dtype, void* stream) {
   if (B < 0 || S < 0 || D < 0 || V < 0) return SPARTON_EINVAL;
   if (dtype < SPARTON_F32 || dtype > SPARTON_F16) return SPARTON_EINVAL;
   if (mask_dtype < SPARTON_MASK_I64 || mask_dtype > SPARTON_MASK_F16) return SPARTON_EINVAL;
@@ -303,8 +308,11 @@ extern "C" __attribute__((visibility("default"))) int sparton_fwd(
   if (cdiv(V, fwd::BN) * B > INT32_MAX) return SPARTON_EUNSUPPORTED;
   hipStream_t st = (hipStream_t)stream;
   switch (dtype) {
-    case SPARTON_BF16: return fwd::launch<bf16>(hidden, weight, bias, mask, mask_dtype, reps, argmax, B, S, D, V, st);
-    case SPARTON_F16: return fwd::launch<f16>(hidden, weight, bias, mask, mask_dtype, reps, argmax, B, S, D, V, st);
-    default: return fwd::launch<float>(hidden, weight, bias, mask, mask_dtype, reps, argmax, B, S, D, V, st);
+    case SPARTON_BF16:
+      return fwd::launch<bf16>(hidden, weight, bias, mask, mask_dtype, reps, argmax, reps_f32, B, S, D, V, st);
+    case SPARTON_F16:
+      return fwd::launch<f16>(hidden, weight, bias, mask, mask_dtype, reps, argmax, reps_f32, B, S, D, V, st);
+    default:
+      return fwd::launch<float>(hidden, weight, bias, mask, mask_dtype, reps, argmax, reps_f32, B, S, D, V, st);
   }
 }

@@ -68,6 +68,7 @@ class SpartonHead(nn.Module):
         needs_grad = torch.is_grad_enabled() and (
             hidden.requires_grad or weight.requires_grad or (bias is not None and bias.requires_grad))
         if needs_grad:
-            scores, _idx = torch.ops.sparton.fused_sparton_fwd(hidden, weight, bias, attention_mask)
+            scores, _idx, _scores32 = torch.ops.sparton.fused_sparton_fwd_train(
+                hidden, weight, bias, attention_mask)
             return scores
         return torch.ops.sparton.fused_sparton_encode(hidden, weight, bias, attention_mask)

@@ -8,7 +8,9 @@ Same op names, argument order and outputs as the reference's
 plus fake kernels (for torch.compile tracing) and the autograd registration.
 Differences: `idx` is int32 (it never leaves the op pair), `bias` may be None in
 the backward too (bias_grad is then an empty tensor and autograd gets None), and
-an inference-only op `sparton::fused_sparton_encode` skips the index store.
+an inference-only op `sparton::fused_sparton_encode` skips the index store, and
+`sparton::fused_sparton_fwd_train` (what SpartonHead trains through) also returns
+the unrounded fp32 reps that its backward uses.
 
 Device tensors go to the HIP kernels and nowhere else: there is no CPU or
 fallback path. CPU tensors raise, like the reference's `assert hidden.is_cuda`
@@ -73,19 +75,22 @@ def _stream(device: torch.device) -> int:
 
 
 def _fwd_impl(hidden: Tensor, embed: Tensor, bias: Optional[Tensor], mask: Tensor,
-              with_idx: bool, op: str) -> Tuple[Tensor, Optional[Tensor]]:
-    _require_device(hidden, op)
+              with_idx: bool, with_f32: bool, op: str):
     B, S, D, V = _validate(hidden, embed, bias, mask, op)
+    _require_device(hidden, op)
     hidden, embed, bias, mask = _dense(hidden), _dense(embed), _dense(bias), _dense(mask)
-    reps = torch.empty((B, V), dtype=hidden.dtype, device=hidden.device)
-    idx = torch.empty((B, V), dtype=torch.int32, device=hidden.device) if with_idx else None
+    dev = hidden.device
+    reps = torch.empty((B, V), dtype=hidden.dtype, device=dev)
+    idx = torch.empty((B, V), dtype=torch.int32, device=dev) if with_idx else None
+    reps32 = torch.empty((B, V), dtype=torch.float32, device=dev) if with_f32 else None
     L = _lib.load()
-    with torch.cuda.device(hidden.device):
+    with torch.cuda.device(dev):
         rc = L.sparton_fwd(hidden.data_ptr(), embed.data_ptr(), _lib.ptr(bias), mask.data_ptr(),
                            _lib.MASK_CODE[mask.dtype], reps.data_ptr(), _lib.ptr(idx),
-                           B, S, D, V, _lib.DTYPE_CODE[hidden.dtype], _stream(hidden.device))
+                           _lib.ptr(reps32), B, S, D, V, _lib.DTYPE_CODE[hidden.dtype],
+                           _stream(dev))
     _lib.check(rc, op)
-    return reps, idx
+    return reps, idx, reps32
 
 
 @torch.library.custom_op("sparton::fused_sparton_fwd", mutates_args=())
@@ -94,7 +99,7 @@ def fused_sparton_fwd(hidden: Tensor, embed: Tensor, bias: Optional[Tensor],
     """reps[B,V] (hidden dtype) and argmax-over-S idx[B,V] (int32).
 
     Replaces fused_sparton_fwd_op (src/sparton/sparton_kernel.py:643-652)."""
-    reps, idx = _fwd_impl(hidden, embed, bias, mask, True, "sparton::fused_sparton_fwd")
+    reps, idx, _ = _fwd_impl(hidden, embed, bias, mask, True, False, "sparton::fused_sparton_fwd")
     return reps, idx
 
 
@@ -105,6 +110,27 @@ def _(hidden, embed, bias, mask):
     return hidden.new_empty((B, V)), hidden.new_empty((B, V), dtype=torch.int32)
 
 
+@torch.library.custom_op("sparton::fused_sparton_fwd_train", mutates_args=())
+def fused_sparton_fwd_train(hidden: Tensor, embed: Tensor, bias: Optional[Tensor],
+                            mask: Tensor) -> Tuple[Tensor, Tensor, Tensor]:
+    """(reps [B,V] hidden dtype, idx [B,V] int32, reps_f32 [B,V] float32) from one kernel.
+
+    The training forward of SpartonHead: its autograd keeps the unrounded reps_f32 for
+    the backward's exp(-reps) (sparton_kernel.py:531 uses the rounded scores), so the
+    gradients match the fp32 torch head instead of inheriting bf16/fp16 rounding."""
+    reps, idx, reps32 = _fwd_impl(hidden, embed, bias, mask, True, True,
+                                  "sparton::fused_sparton_fwd_train")
+    return reps, idx, reps32
+
+
+@fused_sparton_fwd_train.register_fake
+def _(hidden, embed, bias, mask):
+    B, S, D = hidden.shape
+    V = embed.shape[0]
+    return (hidden.new_empty((B, V)), hidden.new_empty((B, V), dtype=torch.int32),
+            hidden.new_empty((B, V), dtype=torch.float32))
+
+
 @torch.library.custom_op("sparton::fused_sparton_encode", mutates_args=())
 def fused_sparton_encode(hidden: Tensor, embed: Tensor, bias: Optional[Tensor],
                          mask: Tensor) -> Tensor:
@@ -112,7 +138,7 @@ def fused_sparton_encode(hidden: Tensor, embed: Tensor, bias: Optional[Tensor],
 
     Serves the no-grad path (training/model.py:141-144, SpladeModel.encode) that the
     reference's dead no-index kernel targeted (src/sparton/sparton_kernel.py:262-394)."""
-    reps, _ = _fwd_impl(hidden, embed, bias, mask, False, "sparton::fused_sparton_encode")
+    reps, _, _ = _fwd_impl(hidden, embed, bias, mask, False, False, "sparton::fused_sparton_encode")
     return reps
 
 
@@ -133,11 +159,14 @@ def fused_sparton_bwd(grad_out: Tensor, max_scores: Tensor, max_idx: Tensor, hid
 
     Replaces fused_sparton_bwd_op (src/sparton/sparton_kernel.py:663-685)."""
     op = "sparton::fused_sparton_bwd"
-    _require_device(grad_out, op)
     B, S, D, V = _validate(hidden, embed, bias, mask, op)
-    for name, t, dt in (("max_scores", max_scores, hidden.dtype), ("max_idx", max_idx, torch.int32)):
-        if tuple(t.shape) != (B, V) or t.dtype != dt:
-            raise ValueError(f"{op}: {name} must be [{B},{V}] {dt}, got {tuple(t.shape)} {t.dtype}")
+    _require_device(grad_out, op)
+    if tuple(max_scores.shape) != (B, V) or max_scores.dtype not in (hidden.dtype, torch.float32):
+        raise ValueError(f"{op}: max_scores must be [{B},{V}] {hidden.dtype} or float32, "
+                         f"got {tuple(max_scores.shape)} {max_scores.dtype}")
+    if tuple(max_idx.shape) != (B, V) or max_idx.dtype != torch.int32:
+        raise ValueError(f"{op}: max_idx must be [{B},{V}] int32, got "
+                         f"{tuple(max_idx.shape)} {max_idx.dtype}")
     if tuple(grad_out.shape) != (B, V):
         raise ValueError(f"{op}: grad_out must be [{B},{V}], got {tuple(grad_out.shape)}")
     grad_out = _dense(grad_out.to(hidden.dtype))
@@ -151,8 +180,8 @@ def fused_sparton_bwd(grad_out: Tensor, max_scores: Tensor, max_idx: Tensor, hid
     ws_bytes = int(L.sparton_bwd_workspace_bytes(B, S, D, V))
     ws = torch.empty((max(ws_bytes, 1),), dtype=torch.uint8, device=dev)
     with torch.cuda.device(dev):
-        rc = L.sparton_bwd(grad_out.data_ptr(), max_scores.data_ptr(), max_idx.data_ptr(),
-                           mask.data_ptr(), _lib.MASK_CODE[mask.dtype], hidden.data_ptr(),
+        rc = L.sparton_bwd(grad_out.data_ptr(), max_scores.data_ptr(),
+                           _lib.DTYPE_CODE[max_scores.dtype], max_idx.data_ptr(), mask.data_ptr(), _lib.MASK_CODE[mask.dtype], hidden.data_ptr(),
                            embed.data_ptr(), d_hidden.data_ptr(), d_embed.data_ptr(),
                            d_bias.data_ptr() if bias is not None else None,
                            ws.data_ptr(), ws_bytes, B, S, D, V, _lib.DTYPE_CODE[hidden.dtype],
@@ -183,3 +212,20 @@ def _backward(ctx, grad_scores, grad_idx):
 
 
 fused_sparton_fwd.register_autograd(_backward, setup_context=_setup_context)
+
+
+def _setup_context_train(ctx, inputs, output):
+    hidden, embed, bias, mask = inputs
+    _scores, idx, scores32 = output
+    ctx.mark_non_differentiable(idx, scores32)
+    ctx.save_for_backward(scores32, idx, hidden, embed, bias, mask)
+
+
+def _backward_train(ctx, grad_scores, grad_idx, grad_scores32):
+    scores32, idx, hidden, embed, bias, mask = ctx.saved_tensors
+    d_hidden, d_embed, d_bias = torch.ops.sparton.fused_sparton_bwd(
+        grad_scores, scores32, idx, hidden, embed, bias, mask)
+    return d_hidden, d_embed, (d_bias if bias is not None else None), None
+
+
+fused_sparton_fwd_train.register_autograd(_backward_train, setup_context=_setup_context_train)

@@ -52,15 +52,15 @@ P = 0x10000  # 16-byte aligned dummy address
 
 
 def fwd(**kw):
-    a = dict(hidden=P, weight=P, bias=None, mask=P, mask_dtype=0, reps=P, argmax=P,
+    a = dict(hidden=P, weight=P, bias=None, mask=P, mask_dtype=0, reps=P, argmax=P, reps32=None,
              B=2, S=4, D=64, V=10, dtype=1, stream=None)
     a.update(kw)
     return _lib.load().sparton_fwd(*a.values())
 
 
 def bwd(**kw):
-    a = dict(grad=P, reps=P, argmax=P, mask=P, mask_dtype=0, hidden=P, weight=P, dH=P, dW=P,
-             db=None, ws=None, ws_bytes=0, B=2, S=4, D=64, V=10, dtype=1, stream=None)
+    a = dict(grad=P, reps=P, reps_dtype=1, argmax=P, mask=P, mask_dtype=0, hidden=P, weight=P,
+             dH=P, dW=P, db=None, ws=None, ws_bytes=0, B=2, S=4, D=64, V=10, dtype=1, stream=None)
     a.update(kw)
     return _lib.load().sparton_bwd(*a.values())
 
@@ -75,7 +75,8 @@ def test_fwd_argument_validation(kw, code):
 
 
 @pytest.mark.parametrize("kw,code", [
-    (dict(S=-2), -1), (dict(dtype=-1), -1), (dict(grad=None), -1), (dict(weight=None), -1),
+    (dict(S=-2), -1), (dict(dtype=-1), -1), (dict(reps_dtype=3), -1), (dict(grad=None), -1),
+    (dict(weight=None), -1),
     (dict(D=12), -1), (dict(dH=P + 4), -2), (dict(ws=None), -4), (dict(ws=P, ws_bytes=16), -4),
     (dict(S=1 << 20), -3), (dict(B=1 << 20), -3), (dict(dH=None, dW=None, db=None), 0),
 ])
@@ -150,7 +151,9 @@ def test_fake_kernels_give_reference_metadata():
         assert r.shape == (3, 40) and r.dtype == torch.bfloat16 and i.dtype == torch.int32
         e = torch.ops.sparton.fused_sparton_encode(H, W, None, m)
         assert e.shape == (3, 40)
-        dh, dw, db = torch.ops.sparton.fused_sparton_bwd(r, r, i, H, W, b, m)
+        r3, i3, r32 = torch.ops.sparton.fused_sparton_fwd_train(H, W, b, m)
+        assert r3.dtype == torch.bfloat16 and i3.dtype == torch.int32 and r32.dtype == torch.float32
+        dh, dw, db = torch.ops.sparton.fused_sparton_bwd(r, r32, i, H, W, b, m)
         assert dh.shape == H.shape and dw.shape == W.shape and db.shape == (40,)
         assert dh.dtype == dw.dtype == db.dtype == torch.float32
         _, _, db0 = torch.ops.sparton.fused_sparton_bwd(r, r, i, H, W, None, m)

@@ -21,12 +21,17 @@ DTYPES = {"fp32": torch.float32, "bf16": torch.bfloat16, "fp16": torch.float16}
 
 
 def run_fwd_bwd(H, W, b, m, G, device):
+    """Training path: fwd_train, then the backward from its unrounded fp32 reps.
+    Also checks that the reference-signature forward returns the same reps/idx."""
     Hd, Wd, md, Gd = H.to(device), W.to(device), m.to(device), G.to(device)
     bd = None if b is None else b.to(device)
-    reps, idx = torch.ops.sparton.fused_sparton_fwd(Hd, Wd, bd, md)
-    dH, dW, db = torch.ops.sparton.fused_sparton_bwd(Gd, reps, idx, Hd, Wd, bd, md)
+    reps, idx, reps32 = torch.ops.sparton.fused_sparton_fwd_train(Hd, Wd, bd, md)
+    r2, i2 = torch.ops.sparton.fused_sparton_fwd(Hd, Wd, bd, md)
+    assert torch.equal(reps, r2) and torch.equal(idx, i2)
+    assert torch.equal(reps32.to(reps.dtype), reps)
+    dH, dW, db = torch.ops.sparton.fused_sparton_bwd(Gd, reps32, idx, Hd, Wd, bd, md)
     torch.cuda.synchronize()
-    return reps, idx, dH, dW, db
+    return reps, idx, reps32, dH, dW, db
 
 
 @pytest.mark.parametrize("dt", list(DTYPES))
@@ -41,14 +46,20 @@ def test_golden_fixture_exact_argmax(path, dt, device):
     b = t["bias"].to(dtype) if "bias" in t else None
     m, G = t["mask"].to(torch.float32), t["grad"].to(dtype)
     say(f"golden {os.path.basename(path)} {dt} B,S,D,V={tuple(H.shape)}+{W.shape[0]}")
-    reps, idx, dH, dW, db = run_fwd_bwd(H, W, b, m, G, device)
+    reps, idx, reps32, dH, dW, db = run_fwd_bwd(H, W, b, m, G, device)
     assert torch.equal(idx.cpu().long(), t["I"])
     torch.testing.assert_close(reps.cpu().to(F64), t["reps"], **FWD_TOL)
-    torch.testing.assert_close(dH.cpu().to(F64), t["dH"], **FWD_TOL)
-    torch.testing.assert_close(dW.cpu().to(F64), t["dW"], **FWD_TOL)
+    torch.testing.assert_close(reps32.cpu().to(F64), t["reps"], rtol=1e-6, atol=1e-6)
+    # training path (fp32 reps): matches the fp64 fixture to fp32 accuracy
+    torch.testing.assert_close(dH.cpu().to(F64), t["dH"], **BWD_TOL)
+    torch.testing.assert_close(dW.cpu().to(F64), t["dW"], **BWD_TOL)
     if b is not None:
-        torch.testing.assert_close(db.cpu().to(F64), t["dbias"], **FWD_TOL)
-    check_bwd_isolated(H, W, b, m, G, reps, idx, dH, dW, db)
+        torch.testing.assert_close(db.cpu().to(F64), t["dbias"], **BWD_TOL)
+    # reference-signature path (rounded reps, sparton_kernel.py:531): the oracle at those reps
+    Hd, Wd, md, Gd = H.to(device), W.to(device), m.to(device), G.to(device)
+    bd = None if b is None else b.to(device)
+    dH2, dW2, db2 = torch.ops.sparton.fused_sparton_bwd(Gd, reps, idx, Hd, Wd, bd, md)
+    check_bwd_isolated(H, W, b, m, G, reps, idx, dH2, dW2, db2)
 
 
 CASES = [
@@ -93,10 +104,10 @@ def make_case(dt, B, S, D, V, bias, mk, seed=0):
 def test_random_shapes(case, device):
     say(f"random case {case}")
     H, W, b, m, G = make_case(*case)
-    reps, idx, dH, dW, db = run_fwd_bwd(H, W, b, m, G, device)
+    reps, idx, reps32, dH, dW, db = run_fwd_bwd(H, W, b, m, G, device)
     n, bad = check_fwd(H, W, b, m, reps, idx)
     say(f"  checked {n} entries, {bad} near-tie argmax differences")
-    check_bwd_isolated(H, W, b, m, G, reps, idx, dH, dW, db)
+    check_bwd_isolated(H, W, b, m, G, reps32, idx, dH, dW, db)
 
 
 def sample_cols(V, n=1024, tail=64, seed=0):
@@ -111,12 +122,12 @@ def test_baseline_config_full_size(cfg, device):
     say(f"config {cfg} {w.name} B={w.B} S={w.S} D={w.D} V={w.V} {w.dtype}")
     inp = make_inputs(w)
     H, W, b, m, G = inp.hidden, inp.weight, inp.bias, inp.mask, inp.grad
-    reps, idx, dH, dW, db = run_fwd_bwd(H, W, b, m, G, device)
+    reps, idx, reps32, dH, dW, db = run_fwd_bwd(H, W, b, m, G, device)
     cols = None if cfg == 1 else sample_cols(w.V)
     n, bad = check_fwd(H, W, b, m, reps, idx, cols)
     say(f"  fwd: checked {n} entries, {bad} near-tie argmax differences")
     # Backward: dH in full, dW/dbias on the sampled rows (all rows for config 1).
-    reps_c, idx_c = reps.cpu(), idx.cpu()
+    reps_c, idx_c = reps32.cpu(), idx.cpu()
     rH, _, rb = oracle.fused_bwd_ref(G, reps_c, idx_c, H, W, b is not None, m, with_dW=False)
     torch.testing.assert_close(dH.cpu().to(F64), rH, **BWD_TOL)
     if cols is None:
@@ -142,10 +153,10 @@ def test_deterministic_repeat(device):
     inp = make_inputs(w).to(device)
     outs = []
     for _ in range(2):
-        r, i = torch.ops.sparton.fused_sparton_fwd(inp.hidden, inp.weight, inp.bias, inp.mask)
-        dh, dw, db = torch.ops.sparton.fused_sparton_bwd(inp.grad, r, i, inp.hidden, inp.weight,
+        r, i, r32 = torch.ops.sparton.fused_sparton_fwd_train(inp.hidden, inp.weight, inp.bias, inp.mask)
+        dh, dw, db = torch.ops.sparton.fused_sparton_bwd(inp.grad, r32, i, inp.hidden, inp.weight,
                                                          inp.bias, inp.mask)
-        outs.append([t.clone() for t in (r, i, dh, dw, db)])
+        outs.append([t.clone() for t in (r, i, r32, dh, dw, db)])
     torch.cuda.synchronize()
     for a, c in zip(*outs):
         assert torch.equal(a, c)
@@ -172,13 +183,13 @@ def test_no_bsv_allocation(device):
     torch.cuda.synchronize()
     torch.cuda.reset_peak_memory_stats()
     base = torch.cuda.memory_allocated()
-    r, i = torch.ops.sparton.fused_sparton_fwd(inp.hidden, inp.weight, inp.bias, inp.mask)
-    dh, dw, db = torch.ops.sparton.fused_sparton_bwd(inp.grad, r, i, inp.hidden, inp.weight, inp.bias, inp.mask)
+    r, i, r32 = torch.ops.sparton.fused_sparton_fwd_train(inp.hidden, inp.weight, inp.bias, inp.mask)
+    dh, dw, db = torch.ops.sparton.fused_sparton_bwd(inp.grad, r32, i, inp.hidden, inp.weight, inp.bias, inp.mask)
     torch.cuda.synchronize()
     peak = torch.cuda.max_memory_allocated() - base
     bsv = w.B * w.S * w.V * 2
     say(f"  peak extra {peak / 2**20:.1f} MiB vs [B,S,V] bf16 {bsv / 2**20:.1f} MiB")
-    outputs = (w.B * w.V * 6 + w.B * w.S * w.D * 4 + w.V * w.D * 4 + w.V * 4)
+    outputs = (w.B * w.V * 10 + w.B * w.S * w.D * 4 + w.V * w.D * 4 + w.V * 4)
     assert peak < bsv / 2
     assert peak <= outputs + _lib.load().sparton_bwd_workspace_bytes(w.B, w.S, w.D, w.V) + (8 << 20)
 
