@@ -176,7 +176,7 @@ def main():
                          args.kernel_reps)
     enc_ms = time_events(torch, lambda: torch.ops.sparton.fused_sparton_encode(Hd, Wd, bd, mask), args.kernel_reps)
     _, idx, reps = torch.ops.sparton.fused_sparton_fwd_train(Hd, Wd, bd, mask)
-    bwd_ms = time_events(torch, lambda: torch.ops.sparton.fused_sparton_bwd(G, reps, idx, Hd, Wd, bd, mask),
+    bwd_ms = time_events(torch, lambda: torch.ops.sparton.fused_sparton_bwd_train(G, reps, idx, Hd, Wd, bd, mask),
                          args.kernel_reps)
 
     # forward roofline: useful flops on valid positions (masked positions are skipped)
@@ -196,9 +196,10 @@ def main():
     u_w = int(act.any(0).sum())
     rows = (torch.arange(w.B, device=dev).view(-1, 1) * w.S + idx.long())[act]
     u_h = int(torch.unique(rows).numel())
-    # G (e bytes) + fp32 reps + int32 idx per (b,v), gathered rows, dense fp32 outputs
+    # G (e bytes) + fp32 reps + int32 idx per (b,v), the gathered H and W rows, and the
+    # dense gradients dH, dW, dbias written once in the parameters' dtype (e bytes)
     bwd_bytes = (w.B * w.V * (e + 4 + 4) + u_w * w.D * e + u_h * w.D * e
-                 + w.B * w.S * w.D * 4 + w.V * w.D * 4 + (w.V * 4 if has_bias else 0))
+                 + w.B * w.S * w.D * e + w.V * w.D * e + (w.V * e if has_bias else 0))
     bwd_gbs = bwd_bytes / (bwd_ms * 1e-3) / 1e9
 
     out = {

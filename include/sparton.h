@@ -18,7 +18,7 @@
  *     void* so this header does not need the HIP headers; NULL = the null stream).
  *   - Tensors are dense row-major with unit inner stride and 16-byte aligned bases:
  *     H [B,S,D], W [V,D], bias [V], mask [B,S], reps/grad [B,V], argmax [B,V] int32,
- *     d_hidden [B,S,D] fp32, d_weight [V,D] fp32, d_bias [V] fp32.
+ *     d_hidden [B,S,D], d_weight [V,D], d_bias [V] (fp32 or `dtype`, see sparton_bwd).
  *   - `dtype` (enum sparton_dtype) is the element type of H, W, bias, reps and grad.
  *   - D must be a multiple of 8 (16-bit dtypes) or 4 (fp32).
  *   - Return value: 0 on success, < 0 for an invalid argument (nothing is launched),
@@ -88,9 +88,11 @@ int sparton_fwd(const void* hidden, const void* weight, const void* bias,
 size_t sparton_bwd_workspace_bytes(int64_t B, int64_t S, int64_t D, int64_t V);
 
 /*
- * Backward: d_hidden, d_weight, d_bias (fp32) from grad_reps [B,V] (`dtype`).
+ * Backward: d_hidden, d_weight, d_bias from grad_reps [B,V] (`dtype`).
  * `reps` is the forward's reps in `reps_dtype` (enum sparton_dtype): the rounded
  * `dtype` output, as the reference saves it, or the fp32 `reps_f32` output.
+ * `grad_dtype` is SPARTON_F32 (the reference's fp32 gradients) or `dtype` (the
+ * gradients rounded once to the parameters' dtype, as autograd would cast them).
  * Every element of each non-NULL output is written (no zero-fill needed); a NULL
  * output is skipped. `mask` is read to apply mask[b, I[b,v]] (1 for a 0/1 mask).
  * Deterministic: no atomics on floating-point data; every output row is summed in
@@ -103,10 +105,9 @@ size_t sparton_bwd_workspace_bytes(int64_t B, int64_t S, int64_t D, int64_t V);
  */
 int sparton_bwd(const void* grad_reps, const void* reps, int reps_dtype,
                 const int32_t* argmax, const void* mask, int mask_dtype, const void* hidden,
-                const void* weight, float* d_hidden, float* d_weight,
-                float* d_bias, void* workspace, size_t workspace_bytes,
-                int64_t B, int64_t S, int64_t D, int64_t V, int dtype,
-                void* stream);
+                const void* weight, void* d_hidden, void* d_weight, void* d_bias,
+                int grad_dtype, void* workspace, size_t workspace_bytes, int64_t B,
+                int64_t S, int64_t D, int64_t V, int dtype, void* stream);
 
 /* Static, thread-safe description of a status code. */
 const char* sparton_strerror(int code);

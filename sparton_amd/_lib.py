@@ -67,8 +67,8 @@ def load() -> ctypes.CDLL:
                                   _i64, _i64, _i64, _i64, ctypes.c_int, _vp]
         L.sparton_fwd.restype = ctypes.c_int
         L.sparton_bwd.argtypes = [_vp, _vp, ctypes.c_int, _vp, _vp, ctypes.c_int, _vp, _vp, _vp,
-                                  _vp, _vp, _vp, ctypes.c_size_t, _i64, _i64, _i64, _i64,
-                                  ctypes.c_int, _vp]
+                                  _vp, _vp, ctypes.c_int, _vp, ctypes.c_size_t, _i64, _i64, _i64,
+                                  _i64, ctypes.c_int, _vp]
         L.sparton_bwd.restype = ctypes.c_int
         L.sparton_bwd_workspace_bytes.argtypes = [_i64, _i64, _i64, _i64]
         L.sparton_bwd_workspace_bytes.restype = ctypes.c_size_t

@@ -1,20 +1,25 @@
-// SpartonHead backward on gfx950: atomic-free, deterministic, HBM-bound.
+// SpartonHead backward on gfx950: atomic-free on floating-point data, deterministic,
+// HBM-bound.
 //
 // Only entries (b,v) with reps > 0, G != 0 and mask[b,I] != 0 carry gradient
 // (g' = G*exp(-reps)*mask[b,I]). The reference scatters them with fp32 atomics into
 // zero-filled dH/dW/dbias (src/sparton/sparton_kernel.py:473-565, :676-678). Here
-// every output row is produced by exactly one wave, summed in a fixed order:
+// every output row is produced by exactly one wave and summed in a fixed order:
 //
-//   dW / dbias  (bwd_dw_kernel)     row v gathers H[b, I[b,v], :] for b ascending.
-//   dH          (hist -> scan -> scatter -> bwd_dh_kernel)
-//       1. hist:    per (b, chunk of CH vocab ids), count active entries per s.
+//   dW / dbias  (bwd_dw_kernel)   row v gathers H[b, I[b,v], :] for b ascending.
+//   dH          (count -> scan -> scatter -> bwd_dh_kernel)
+//       1. count:   per (b, wave chunk of CHW vocab ids), active entries per s.
 //       2. scan:    per b, exclusive scan in (s, chunk) order -> each (b,s) segment
-//                   start, and each chunk's first slot inside every segment.
-//       3. scatter: per (b, chunk), write (v, g') to its slot; the rank among equal
-//                   s inside a 64-lane step comes from ballots, so each segment is
-//                   ordered by v ascending (a stable counting sort by s).
+//                   start and each chunk's first slot inside every segment.
+//       3. scatter: per (b, chunk), write (v, g') to its slot. Entries are visited in
+//                   v order and ranked among equal s with ballots, so each segment
+//                   lists its vocab ids in ascending order (a stable counting sort).
 //       4. dh:      one wave per (b,s) row sums g' * W[v,:] over its segment.
-// Integer counts are the only LDS atomics; they are order-independent.
+// The only atomics are integer counts in LDS, which are order-independent.
+//
+// Gradients are written as fp32 (what the reference returns) or in the input dtype
+// (what autograd would cast them to for bf16/fp16 parameters), rounded once from
+// the fp32 sums.
 
 #include "sparton_common.h"
 
@@ -23,12 +28,11 @@ extern __shared__ __attribute__((aligned(16))) unsigned char sparton_bwd_smem[];
 namespace sparton {
 namespace bwd {
 
-constexpr int CH = 2048;          // vocab ids per histogram chunk (one wave)
-constexpr int MAX_S = 16384;      // per-wave LDS counters: S ints
-constexpr int MAX_B = 8192;       // dW kernel stages g' for B x vblk entries in LDS
-constexpr int DW_LDS_ENTRIES = 8192;  // B * vblk (8 bytes each -> 64 KB)
-constexpr int VBLK_MAX = 16;      // vocab rows per dW workgroup
-constexpr int PASS = 256;         // hidden elements per wave pass (4 per lane)
+constexpr int CHW = 1024;          // vocab ids per wave chunk (16 rounds of 64 lanes)
+constexpr int ROUNDS = CHW / 64;
+constexpr int MAX_S = 16384;       // LDS: S mask floats + S counters per wave
+constexpr int MAX_B = 8192;
+constexpr int MAX_NP = 16;         // D up to 16 * 256 per register pass
 
 struct Layout {
   int64_t nch;
@@ -37,7 +41,7 @@ struct Layout {
 
 static Layout layout(int64_t B, int64_t S, int64_t V) {
   Layout L;
-  L.nch = cdiv(V, CH);
+  L.nch = cdiv(V, CHW);
   size_t off = 0;
   auto take = [&](size_t bytes) { size_t o = off; off += (size_t)round_up((int64_t)bytes, 256); return o; };
   L.hist = take((size_t)(B * L.nch * S) * 4);
@@ -48,27 +52,77 @@ static Layout layout(int64_t B, int64_t S, int64_t V) {
   return L;
 }
 
-static int waves_for(int64_t S) { return S <= 4096 ? 4 : 1; }
+// Waves per block of the count/scatter kernels: LDS holds S mask floats plus S
+// counters per wave (at most 40 KB with 4 waves, 128 KB with one wave at MAX_S).
+static int waves_for(int64_t S) { return S <= 2048 ? 4 : 1; }
 
-// ---- 1. histogram ----------------------------------------------------------
+// Stage mask row b as floats in LDS.
+__device__ __forceinline__ void stage_mask(float* maskf, const void* mask, int mdt, int64_t b,
+                                           int S) {
+  for (int s = threadIdx.x; s < S; s += blockDim.x) maskf[s] = load_mask(mask, mdt, b * S + s);
+}
+
+// Entry (b, v): whether it carries gradient, its coefficient g' and index s.
+// Activity is decided by comparisons of loaded values only (never by the float
+// product), so the count and scatter kernels agree on every entry; an index outside
+// [0, S) makes the entry inactive, so it can never turn into an out-of-bounds access.
+// g' = G * exp(-reps) (src/sparton/sparton_kernel.py:531) times mask[b, I], the torch
+// head's d x / d logits (training/model.py:60); 1 for a 0/1 mask.
 template <typename T>
-__global__ __launch_bounds__(256) void bwd_hist_kernel(
-    const T* __restrict__ grad, const void* __restrict__ reps, int reps_dtype,
-    const int32_t* __restrict__ idx,
-    const void* __restrict__ mask, int mask_dtype, int S, int V, int nch, int* __restrict__ hist) {
-  int* lds = (int*)sparton_bwd_smem;
+__device__ __forceinline__ bool entry(T g_raw, float r, int s, const float* maskf, int S,
+                                      float* g_out) {
+  *g_out = 0.0f;
+  if (!(r > 0.0f) || s < 0 || s >= S) return false;
+  const float g = to_f32(g_raw);
+  if (g == 0.0f) return false;
+  const float m = maskf[s];
+  if (m == 0.0f) return false;
+  *g_out = g * expf(-r) * m;
+  return true;
+}
+
+// This wave's chunk of row b: round j, lane l holds entry v = base + j*64 + l, so every
+// load instruction reads consecutive elements; all 3 * ROUNDS loads are issued up front.
+template <typename T>
+struct ChunkData {
+  T g[ROUNDS];
+  float r[ROUNDS];
+  int s[ROUNDS];
+  __device__ __forceinline__ void load(const T* grad, const void* reps, int rdt,
+                                       const int32_t* idx, int64_t row, int base, int V,
+                                       int lane) {
+#pragma unroll
+    for (int j = 0; j < ROUNDS; ++j) {
+      const int v = base + j * 64 + lane;
+      const bool in = v < V;
+      const int64_t o = row + (in ? v : 0);
+      g[j] = in ? grad[o] : from_f32<T>(0.0f);
+      r[j] = in ? load_float(reps, rdt, o) : 0.0f;
+      s[j] = in ? idx[o] : -1;
+    }
+  }
+};
+
+// ---- 1. count ----------------------------------------------------------------
+template <typename T>
+__global__ __launch_bounds__(256) void bwd_count_kernel(
+    const T* __restrict__ grad, const void* __restrict__ reps, int rdt,
+    const int32_t* __restrict__ idx, const void* __restrict__ mask, int mdt, int S, int V,
+    int nch, int* __restrict__ hist) {
+  float* maskf = (float*)sparton_bwd_smem;
   const int wpb = blockDim.x >> 6, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  int* h = (int*)(maskf + S) + wave * S;
   const int b = blockIdx.y, c = blockIdx.x * wpb + wave;
-  int* h = lds + wave * S;
+  stage_mask(maskf, mask, mdt, b, S);
   for (int s = lane; s < S; s += 64) h[s] = 0;
   __syncthreads();
   if (c < nch) {
-    const int vend = min(V, (c + 1) * CH);
-    for (int v = c * CH + lane; v < vend; v += 64) {
-      int s;
+    ChunkData<T> d;
+    d.load(grad, reps, rdt, idx, (int64_t)b * V, c * CHW, V, lane);
+#pragma unroll
+    for (int j = 0; j < ROUNDS; ++j) {
       float g;
-      if (grad_entry(grad, reps, reps_dtype, idx, mask, mask_dtype, b, S, (int64_t)b * V + v, &g, &s))
-        atomicAdd(&h[s], 1);
+      if (entry(d.g[j], d.r[j], d.s[j], maskf, S, &g)) atomicAdd(&h[d.s[j]], 1);
     }
   }
   __syncthreads();
@@ -95,7 +149,7 @@ __device__ __forceinline__ int block_excl_scan(int x, int* tmp4) {
   return base + v - x;
 }
 
-// ---- 2. scan ---------------------------------------------------------------
+// ---- 2. scan -----------------------------------------------------------------
 __global__ __launch_bounds__(256) void bwd_scan_kernel(int* __restrict__ hist, int* __restrict__ seg_start,
                                                        int* __restrict__ seg_cnt, int S, int nch) {
   int* tot = (int*)sparton_bwd_smem;  // [S]
@@ -131,32 +185,33 @@ __global__ __launch_bounds__(256) void bwd_scan_kernel(int* __restrict__ hist, i
   }
 }
 
-// ---- 3. scatter ------------------------------------------------------------
+// ---- 3. scatter ----------------------------------------------------------------
 template <typename T>
 __global__ __launch_bounds__(256) void bwd_scatter_kernel(
-    const T* __restrict__ grad, const void* __restrict__ reps, int reps_dtype,
-    const int32_t* __restrict__ idx,
-    const void* __restrict__ mask, int mask_dtype, int S, int V, int nch,
-    const int* __restrict__ hist_base, int2* __restrict__ list) {
-  int* lds = (int*)sparton_bwd_smem;
+    const T* __restrict__ grad, const void* __restrict__ reps, int rdt,
+    const int32_t* __restrict__ idx, const void* __restrict__ mask, int mdt, int S, int V,
+    int nch, const int* __restrict__ hist_base, int2* __restrict__ list) {
+  float* maskf = (float*)sparton_bwd_smem;
   const int wpb = blockDim.x >> 6, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  int* cur = (int*)(maskf + S) + wave * S;
   const int b = blockIdx.y, c = blockIdx.x * wpb + wave;
-  int* cur = lds + wave * S;
+  stage_mask(maskf, mask, mdt, b, S);
   if (c < nch) {
     const int* in = hist_base + ((int64_t)b * nch + c) * S;
     for (int s = lane; s < S; s += 64) cur[s] = in[s];
   }
   __syncthreads();
   if (c >= nch) return;
+  ChunkData<T> d;
+  d.load(grad, reps, rdt, idx, (int64_t)b * V, c * CHW, V, lane);
   int2* lb = list + (int64_t)b * V;
   const uint64_t lt = (1ull << lane) - 1ull;
-  const int vend = min(V, (c + 1) * CH);
-  for (int vs = c * CH; vs < vend; vs += 64) {
-    const int v = vs + lane;
-    float g = 0.0f;
-    int s = 0;
-    const bool act =
-        v < vend && grad_entry(grad, reps, reps_dtype, idx, mask, mask_dtype, b, S, (int64_t)b * V + v, &g, &s);
+#pragma unroll
+  for (int j = 0; j < ROUNDS; ++j) {
+    float g;
+    const bool act = entry(d.g[j], d.r[j], d.s[j], maskf, S, &g);
+    const int s = d.s[j];
+    const int v = c * CHW + j * 64 + lane;
     uint64_t pending = __ballot(act);
     while (pending) {
       const int leader = __ffsll((unsigned long long)pending) - 1;
@@ -171,88 +226,163 @@ __global__ __launch_bounds__(256) void bwd_scatter_kernel(
   }
 }
 
-// ---- 4. dH -----------------------------------------------------------------
-template <typename T>
+// Store four fp32 values as O.
+__device__ __forceinline__ void store4(float* p, const f32x4& a) { *(f32x4*)p = a; }
+__device__ __forceinline__ void store4(bf16* p, const f32x4& a) {
+  *(bf16x4*)p = bf16x4{(bf16)a[0], (bf16)a[1], (bf16)a[2], (bf16)a[3]};
+}
+__device__ __forceinline__ void store4(f16* p, const f32x4& a) {
+  *(f16x4*)p = f16x4{(f16)a[0], (f16)a[1], (f16)a[2], (f16)a[3]};
+}
+
+// ---- 4. dH ---------------------------------------------------------------------
+// One wave per (b,s) row; lane l owns elements d0 + p*256 + 4l .. +3 for p < NP. The NP
+// loads of two W rows are issued together before they are accumulated.
+template <typename T, typename O, int NP>
 __global__ __launch_bounds__(256) void bwd_dh_kernel(
     const T* __restrict__ W, const int2* __restrict__ list, const int* __restrict__ seg_start,
-    const int* __restrict__ seg_cnt, float* __restrict__ dH, int B, int S, int D, int V) {
+    const int* __restrict__ seg_cnt, O* __restrict__ dH, int B, int S, int D, int V) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * 4 + wave;
   if (row >= (int64_t)B * S) return;
   const int64_t b = row / S;
   const int start = seg_start[row], cnt = seg_cnt[row];
   const int2* seg = list + b * V + start;
-  float* out = dH + row * D;
-  for (int d0 = 0; d0 < D; d0 += PASS) {
-    const int d = d0 + lane * 4;
-    const bool dv = d < D;
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  for (int d0 = 0; d0 < D; d0 += NP * 256) {
+    f32x4 acc[NP];
+#pragma unroll
+    for (int p = 0; p < NP; ++p) acc[p] = f32x4{0.f, 0.f, 0.f, 0.f};
     for (int e0 = 0; e0 < cnt; e0 += 64) {
       const int2 ent = e0 + lane < cnt ? seg[e0 + lane] : make_int2(0, 0);
       const int n = min(64, cnt - e0);
-      if (dv) {
-        for (int j = 0; j < n; ++j) {
-          const int v = __builtin_amdgcn_readlane(ent.x, j);
-          const float g = __int_as_float(__builtin_amdgcn_readlane(ent.y, j));
-          acc += g * load4(W + (int64_t)v * D + d);
+      int j = 0;
+      for (; j + 1 < n; j += 2) {
+        const int v0 = __builtin_amdgcn_readlane(ent.x, j);
+        const int v1 = __builtin_amdgcn_readlane(ent.x, j + 1);
+        const float g0 = __int_as_float(__builtin_amdgcn_readlane(ent.y, j));
+        const float g1 = __int_as_float(__builtin_amdgcn_readlane(ent.y, j + 1));
+        f32x4 w0[NP], w1[NP];
+#pragma unroll
+        for (int p = 0; p < NP; ++p) {
+          const int d = d0 + p * 256 + lane * 4;
+          w0[p] = d < D ? load4(W + (int64_t)v0 * D + d) : f32x4{0.f, 0.f, 0.f, 0.f};
+          w1[p] = d < D ? load4(W + (int64_t)v1 * D + d) : f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+#pragma unroll
+        for (int p = 0; p < NP; ++p) acc[p] += g0 * w0[p] + g1 * w1[p];
+      }
+      if (j < n) {
+        const int v0 = __builtin_amdgcn_readlane(ent.x, j);
+        const float g0 = __int_as_float(__builtin_amdgcn_readlane(ent.y, j));
+#pragma unroll
+        for (int p = 0; p < NP; ++p) {
+          const int d = d0 + p * 256 + lane * 4;
+          if (d < D) acc[p] += g0 * load4(W + (int64_t)v0 * D + d);
         }
       }
     }
-    if (dv) *(f32x4*)(out + d) = acc;
+    O* out = dH + row * D;
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+      const int d = d0 + p * 256 + lane * 4;
+      if (d < D) store4(out + d, acc[p]);
+    }
   }
 }
 
-// ---- 5. dW and dbias ---------------------------------------------------------
-template <typename T>
+// ---- 5. dW and dbias -------------------------------------------------------------
+// One wave per vocab row v: lanes hold batch rows b (64 per pass), a ballot lists the
+// active ones, and their H rows are gathered in ascending b, two at a time.
+template <typename T, typename O, int NP>
 __global__ __launch_bounds__(256) void bwd_dw_kernel(
-    const T* __restrict__ grad, const void* __restrict__ reps, int reps_dtype,
-    const int32_t* __restrict__ idx,
-    const void* __restrict__ mask, int mask_dtype, const T* __restrict__ H,
-    float* __restrict__ dW, float* __restrict__ dbias, int B, int S, int D, int V, int vblk) {
-  float* gp = (float*)sparton_bwd_smem;   // [B][vblk]
-  int* si = (int*)(gp + (int64_t)B * vblk);  // [B][vblk]
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int v0 = blockIdx.x * vblk;
-  for (int i = tid; i < B * vblk; i += 256) {
-    const int bb = i / vblk, j = i - bb * vblk, v = v0 + j;
-    float g = 0.0f;
-    int s = 0;
-    if (v < V) grad_entry(grad, reps, reps_dtype, idx, mask, mask_dtype, bb, S, (int64_t)bb * V + v, &g, &s);
-    gp[i] = g;   // 0 for inactive entries, which the gather loop skips
-    si[i] = s;
-  }
-  __syncthreads();
-  if (dbias != nullptr && tid < vblk && v0 + tid < V) {
-    float sum = 0.0f;
-    for (int bb = 0; bb < B; ++bb) sum += gp[bb * vblk + tid];
-    dbias[v0 + tid] = sum;
-  }
-  if (dW == nullptr) return;
-  for (int j = wave; j < vblk; j += 4) {
-    const int v = v0 + j;
-    if (v >= V) break;
-    for (int d0 = 0; d0 < D; d0 += PASS) {
-      const int d = d0 + lane * 4;
-      if (d < D) {
-        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-        for (int bb = 0; bb < B; ++bb) {
-          const float g = gp[bb * vblk + j];
-          if (g != 0.0f) {
-            const int s = si[bb * vblk + j];
-            acc += g * load4(H + ((int64_t)bb * S + s) * D + d);
+    const T* __restrict__ grad, const void* __restrict__ reps, int rdt,
+    const int32_t* __restrict__ idx, const void* __restrict__ mask, int mdt,
+    const T* __restrict__ H, O* __restrict__ dW, O* __restrict__ dbias, int B, int S, int D,
+    int V) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int v = blockIdx.x * 4 + wave;
+  if (v >= V) return;
+  const int dend = max(D, 1);  // one pass even when D == 0, for dbias
+  for (int d0 = 0; d0 < dend; d0 += NP * 256) {
+    f32x4 acc[NP];
+#pragma unroll
+    for (int p = 0; p < NP; ++p) acc[p] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float bsum = 0.0f;
+    for (int b0 = 0; b0 < B; b0 += 64) {
+      const int bb = b0 + lane;
+      float g = 0.0f;
+      int s = 0;
+      bool act = false;
+      if (bb < B) {
+        const int64_t o = (int64_t)bb * V + v;
+        const float r = load_float(reps, rdt, o);
+        s = idx[o];
+        if (r > 0.0f && s >= 0 && s < S) {
+          const float gr = to_f32(grad[o]);
+          if (gr != 0.0f) {
+            const float m = load_mask(mask, mdt, (int64_t)bb * S + s);
+            if (m != 0.0f) {
+              act = true;
+              g = gr * expf(-r) * m;
+            }
           }
         }
-        *(f32x4*)(dW + (int64_t)v * D + d) = acc;
+      }
+      uint64_t pending = __ballot(act);
+      while (pending) {
+        const int l0 = __ffsll((unsigned long long)pending) - 1;
+        pending &= pending - 1;
+        const int s0 = __builtin_amdgcn_readlane(s, l0);
+        const float g0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(g), l0));
+        const T* h0 = H + ((int64_t)(b0 + l0) * S + s0) * D;
+        bsum += g0;
+        if (pending) {
+          const int l1 = __ffsll((unsigned long long)pending) - 1;
+          pending &= pending - 1;
+          const int s1 = __builtin_amdgcn_readlane(s, l1);
+          const float g1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(g), l1));
+          const T* h1 = H + ((int64_t)(b0 + l1) * S + s1) * D;
+          bsum += g1;
+          f32x4 x0[NP], x1[NP];
+#pragma unroll
+          for (int p = 0; p < NP; ++p) {
+            const int d = d0 + p * 256 + lane * 4;
+            x0[p] = d < D ? load4(h0 + d) : f32x4{0.f, 0.f, 0.f, 0.f};
+            x1[p] = d < D ? load4(h1 + d) : f32x4{0.f, 0.f, 0.f, 0.f};
+          }
+#pragma unroll
+          for (int p = 0; p < NP; ++p) acc[p] += g0 * x0[p] + g1 * x1[p];
+        } else {
+#pragma unroll
+          for (int p = 0; p < NP; ++p) {
+            const int d = d0 + p * 256 + lane * 4;
+            if (d < D) acc[p] += g0 * load4(h0 + d);
+          }
+        }
+      }
+    }
+    if (d0 == 0 && dbias != nullptr && lane == 0) dbias[v] = from_f32<O>(bsum);
+    if (dW != nullptr) {
+      O* out = dW + (int64_t)v * D;
+#pragma unroll
+      for (int p = 0; p < NP; ++p) {
+        const int d = d0 + p * 256 + lane * 4;
+        if (d < D) store4(out + d, acc[p]);
       }
     }
   }
 }
 
-template <typename T>
-static int launch(const void* grad, const void* r, int rdt, const int32_t* idx, const void* mask,
-                  int mdt, const void* H, const void* W, float* dH, float* dW, float* dbias,
-                  void* ws, int64_t B, int64_t S, int64_t D, int64_t V, hipStream_t st) {
-  const T* g = (const T*)grad;
+// Register passes for a row of D elements (4 per lane, 256 per pass), capped at MAX_NP
+// (longer rows loop over D in chunks of MAX_NP * 256).
+static int passes_for(int64_t D) {
+  return (int)std::min<int64_t>(MAX_NP, std::max<int64_t>(1, cdiv(D, 256)));
+}
+
+template <typename T, typename O, int NP>
+static void launch_rows(const T* g, const void* r, int rdt, const int32_t* idx, const void* mask,
+                        int mdt, const T* H, const T* W, O* dH, O* dW, O* dbias, void* ws,
+                        int64_t B, int64_t S, int64_t D, int64_t V, hipStream_t st) {
   if (dH != nullptr && B * S > 0 && D > 0) {
     const Layout L = layout(B, S, V);
     int* hist = (int*)((char*)ws + L.hist);
@@ -261,25 +391,45 @@ static int launch(const void* grad, const void* r, int rdt, const int32_t* idx, 
     int2* list = (int2*)((char*)ws + L.list);
     const int wpb = waves_for(S);
     const dim3 cgrid((unsigned)cdiv(L.nch, wpb), (unsigned)B);
-    const size_t cl = (size_t)wpb * S * 4;
+    const size_t cl = (size_t)S * 4 * (1 + wpb);
     if (L.nch > 0)
-      hipLaunchKernelGGL(bwd_hist_kernel<T>, cgrid, dim3(64 * wpb), cl, st, g, r, rdt, idx, mask, mdt,
-                         (int)S, (int)V, (int)L.nch, hist);
+      hipLaunchKernelGGL(bwd_count_kernel<T>, cgrid, dim3(64 * wpb), cl, st, g, r, rdt, idx,
+                         mask, mdt, (int)S, (int)V, (int)L.nch, hist);
     hipLaunchKernelGGL(bwd_scan_kernel, dim3((unsigned)B), dim3(256), (size_t)S * 4, st, hist,
                        seg_start, seg_cnt, (int)S, (int)L.nch);
     if (L.nch > 0)
-      hipLaunchKernelGGL(bwd_scatter_kernel<T>, cgrid, dim3(64 * wpb), cl, st, g, r, rdt, idx, mask,
-                         mdt, (int)S, (int)V, (int)L.nch, (const int*)hist, list);
-    hipLaunchKernelGGL(bwd_dh_kernel<T>, dim3((unsigned)cdiv(B * S, 4)), dim3(256), 0, st,
-                       (const T*)W, (const int2*)list, (const int*)seg_start, (const int*)seg_cnt,
-                       dH, (int)B, (int)S, (int)D, (int)V);
+      hipLaunchKernelGGL(bwd_scatter_kernel<T>, cgrid, dim3(64 * wpb), cl, st, g, r, rdt, idx,
+                         mask, mdt, (int)S, (int)V, (int)L.nch, (const int*)hist, list);
+    hipLaunchKernelGGL((bwd_dh_kernel<T, O, NP>), dim3((unsigned)cdiv(B * S, 4)), dim3(256), 0,
+                       st, W, (const int2*)list, (const int*)seg_start, (const int*)seg_cnt, dH,
+                       (int)B, (int)S, (int)D, (int)V);
   }
-  if ((dW != nullptr || dbias != nullptr) && V > 0) {
-    const int vblk = B > 0 ? (int)std::min<int64_t>(VBLK_MAX, DW_LDS_ENTRIES / B) : VBLK_MAX;
-    hipLaunchKernelGGL(bwd_dw_kernel<T>, dim3((unsigned)cdiv(V, vblk)), dim3(256),
-                       (size_t)B * vblk * 8, st, g, r, rdt, idx, mask, mdt, (const T*)H, dW, dbias,
-                       (int)B, (int)S, (int)D, (int)V, vblk);
+  if ((dW != nullptr || dbias != nullptr) && V > 0)
+    hipLaunchKernelGGL((bwd_dw_kernel<T, O, NP>), dim3((unsigned)cdiv(V, 4)), dim3(256), 0, st,
+                       g, r, rdt, idx, mask, mdt, H, dW, dbias, (int)B, (int)S, (int)D, (int)V);
+}
+
+template <typename T, typename O>
+static int launch(const void* grad, const void* r, int rdt, const int32_t* idx, const void* mask,
+                  int mdt, const void* H, const void* W, void* dH, void* dW, void* dbias,
+                  void* ws, int64_t B, int64_t S, int64_t D, int64_t V, hipStream_t st) {
+  const T* g = (const T*)grad;
+  const T* h = (const T*)H;
+  const T* w = (const T*)W;
+#define SPARTON_ROWS(NP)                                                                      \
+  launch_rows<T, O, NP>(g, r, rdt, idx, mask, mdt, h, w, (O*)dH, (O*)dW, (O*)dbias, ws, B, S, \
+                        D, V, st)
+  switch (passes_for(D)) {
+    case 1: SPARTON_ROWS(1); break;
+    case 2: SPARTON_ROWS(2); break;
+    case 3: SPARTON_ROWS(3); break;
+    case 4: SPARTON_ROWS(4); break;
+    case 5: case 6: SPARTON_ROWS(6); break;
+    case 7: case 8: SPARTON_ROWS(8); break;
+    case 9: case 10: case 11: case 12: SPARTON_ROWS(12); break;
+    default: SPARTON_ROWS(16); break;
   }
+#undef SPARTON_ROWS
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? SPARTON_OK : (int)e;
 }
@@ -297,12 +447,13 @@ extern "C" __attribute__((visibility("default"))) size_t sparton_bwd_workspace_b
 
 extern "C" __attribute__((visibility("default"))) int sparton_bwd(
     const void* grad_reps, const void* reps, int reps_dtype, const int32_t* argmax,
-    const void* mask, int mask_dtype, const void* hidden, const void* weight, float* d_hidden,
-    float* d_weight, float* d_bias, void* workspace, size_t workspace_bytes, int64_t B, int64_t S,
-    int64_t D, int64_t V, int dtype, void* stream) {
+    const void* mask, int mask_dtype, const void* hidden, const void* weight, void* d_hidden,
+    void* d_weight, void* d_bias, int grad_dtype, void* workspace, size_t workspace_bytes,
+    int64_t B, int64_t S, int64_t D, int64_t V, int dtype, void* stream) {
   if (B < 0 || S < 0 || D < 0 || V < 0) return SPARTON_EINVAL;
   if (dtype < SPARTON_F32 || dtype > SPARTON_F16) return SPARTON_EINVAL;
   if (reps_dtype < SPARTON_F32 || reps_dtype > SPARTON_F16) return SPARTON_EINVAL;
+  if (grad_dtype != SPARTON_F32 && grad_dtype != dtype) return SPARTON_EINVAL;
   if (mask_dtype < SPARTON_MASK_I64 || mask_dtype > SPARTON_MASK_F16) return SPARTON_EINVAL;
   if (B * V > 0 && (grad_reps == nullptr || reps == nullptr || argmax == nullptr || mask == nullptr))
     return SPARTON_EINVAL;
@@ -312,8 +463,10 @@ extern "C" __attribute__((visibility("default"))) int sparton_bwd(
   if (need_dw && d_weight != nullptr && D > 0 && B * S > 0 && hidden == nullptr) return SPARTON_EINVAL;
   const int64_t esz = dtype == SPARTON_F32 ? 4 : 2;
   if ((D * esz) % 16 != 0) return SPARTON_EINVAL;
-  if (((uintptr_t)hidden | (uintptr_t)weight | (uintptr_t)d_hidden | (uintptr_t)d_weight) % 16 != 0)
-    return SPARTON_EALIGN;
+  if (((uintptr_t)hidden | (uintptr_t)weight) % 16 != 0) return SPARTON_EALIGN;
+  // Outputs are written 4 elements at a time: 16 bytes (fp32) or 8 bytes (16-bit).
+  const uintptr_t oalign = grad_dtype == SPARTON_F32 ? 16 : 8;
+  if (((uintptr_t)d_hidden | (uintptr_t)d_weight) % oalign != 0) return SPARTON_EALIGN;
   if (B > bwd::MAX_B || S > bwd::MAX_S) return SPARTON_EUNSUPPORTED;
   if (D > INT32_MAX || V > INT32_MAX || B * S > INT32_MAX || B * V > INT32_MAX)
     return SPARTON_EUNSUPPORTED;
@@ -324,16 +477,17 @@ extern "C" __attribute__((visibility("default"))) int sparton_bwd(
   }
   if (!need_dh && !need_dw) return SPARTON_OK;
   hipStream_t st = (hipStream_t)stream;
-  float* dh = need_dh ? d_hidden : nullptr;
+  void* dh = need_dh ? d_hidden : nullptr;
+  const bool f32out = grad_dtype == SPARTON_F32;
+#define SPARTON_BWD(T)                                                                           \
+  (f32out ? bwd::launch<T, float>(grad_reps, reps, reps_dtype, argmax, mask, mask_dtype, hidden, \
+                                  weight, dh, d_weight, d_bias, workspace, B, S, D, V, st)       \
+          : bwd::launch<T, T>(grad_reps, reps, reps_dtype, argmax, mask, mask_dtype, hidden,     \
+                              weight, dh, d_weight, d_bias, workspace, B, S, D, V, st))
   switch (dtype) {
-    case SPARTON_BF16:
-      return bwd::launch<bf16>(grad_reps, reps, reps_dtype, argmax, mask, mask_dtype, hidden, weight, dh,
-                               d_weight, d_bias, workspace, B, S, D, V, st);
-    case SPARTON_F16:
-      return bwd::launch<f16>(grad_reps, reps, reps_dtype, argmax, mask, mask_dtype, hidden, weight, dh,
-                              d_weight, d_bias, workspace, B, S, D, V, st);
-    default:
-      return bwd::launch<float>(grad_reps, reps, reps_dtype, argmax, mask, mask_dtype, hidden, weight, dh,
-                                d_weight, d_bias, workspace, B, S, D, V, st);
+    case SPARTON_BF16: return SPARTON_BWD(bf16);
+    case SPARTON_F16: return SPARTON_BWD(f16);
+    default: return SPARTON_BWD(float);
   }
+#undef SPARTON_BWD
 }

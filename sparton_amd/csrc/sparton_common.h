@@ -65,32 +65,6 @@ __device__ __forceinline__ f32x4 load4(const f16* p) {
   return f32x4{(float)v[0], (float)v[1], (float)v[2], (float)v[3]};
 }
 
-// One backward entry (b,v): returns whether it carries gradient, with its
-// coefficient g' = G * exp(-reps) * mask[b, I] and its index s = I[b,v].
-// Activity is decided by comparisons of loaded values only (reps > 0, G != 0,
-// mask != 0, s in [0, S)), never by the float product, so every kernel that asks
-// gets the same answer for the same entry. An index outside [0, S) makes the entry
-// inactive, so a corrupt index can never turn into an out-of-bounds access.
-// Follows src/sparton/sparton_kernel.py:531 (g' = where(reps>0, G*exp(-reps), 0));
-// the mask factor is the torch head's d x / d logits (training/model.py:60).
-template <typename T>
-__device__ __forceinline__ bool grad_entry(const T* grad, const void* reps, int reps_dtype,
-                                           const int32_t* idx, const void* mask, int mask_dtype,
-                                           int64_t b, int64_t S, int64_t off, float* g_out,
-                                           int* s_out) {
-  const float r = load_float(reps, reps_dtype, off);
-  const int s = idx[off];
-  *s_out = s;
-  *g_out = 0.0f;
-  if (!(r > 0.0f) || s < 0 || (int64_t)s >= S) return false;
-  const float g = to_f32(grad[off]);
-  if (g == 0.0f) return false;
-  const float m = load_mask(mask, mask_dtype, b * S + s);
-  if (m == 0.0f) return false;
-  *g_out = g * expf(-r) * m;
-  return true;
-}
-
 __host__ __device__ constexpr int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 __host__ __device__ constexpr int64_t round_up(int64_t a, int64_t b) { return cdiv(a, b) * b; }
 

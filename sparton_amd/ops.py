@@ -10,7 +10,8 @@ Differences: `idx` is int32 (it never leaves the op pair), `bias` may be None in
 the backward too (bias_grad is then an empty tensor and autograd gets None), and
 an inference-only op `sparton::fused_sparton_encode` skips the index store, and
 `sparton::fused_sparton_fwd_train` (what SpartonHead trains through) also returns
-the unrounded fp32 reps that its backward uses.
+the unrounded fp32 reps that its backward `sparton::fused_sparton_bwd_train` uses;
+that backward writes the gradients in the parameters' dtype.
 
 Device tensors go to the HIP kernels and nowhere else: there is no CPU or
 fallback path. CPU tensors raise, like the reference's `assert hidden.is_cuda`
@@ -151,14 +152,7 @@ def bwd_workspace_bytes(B: int, S: int, D: int, V: int) -> int:
     return int(_lib.load().sparton_bwd_workspace_bytes(B, S, D, V))
 
 
-@torch.library.custom_op("sparton::fused_sparton_bwd", mutates_args=())
-def fused_sparton_bwd(grad_out: Tensor, max_scores: Tensor, max_idx: Tensor, hidden: Tensor,
-                      embed: Tensor, bias: Optional[Tensor],
-                      mask: Tensor) -> Tuple[Tensor, Tensor, Tensor]:
-    """(dH [B,S,D], dW [V,D], dbias [V] or [0]) in float32.
-
-    Replaces fused_sparton_bwd_op (src/sparton/sparton_kernel.py:663-685)."""
-    op = "sparton::fused_sparton_bwd"
+def _bwd_impl(grad_out, max_scores, max_idx, hidden, embed, bias, mask, grad_dtype, op):
     B, S, D, V = _validate(hidden, embed, bias, mask, op)
     _require_device(grad_out, op)
     if tuple(max_scores.shape) != (B, V) or max_scores.dtype not in (hidden.dtype, torch.float32):
@@ -173,21 +167,33 @@ def fused_sparton_bwd(grad_out: Tensor, max_scores: Tensor, max_idx: Tensor, hid
     max_scores, max_idx = _dense(max_scores), _dense(max_idx)
     hidden, embed, bias, mask = _dense(hidden), _dense(embed), _dense(bias), _dense(mask)
     dev = hidden.device
-    d_hidden = torch.empty((B, S, D), dtype=torch.float32, device=dev)
-    d_embed = torch.empty((V, D), dtype=torch.float32, device=dev)
-    d_bias = torch.empty((V if bias is not None else 0,), dtype=torch.float32, device=dev)
+    d_hidden = torch.empty((B, S, D), dtype=grad_dtype, device=dev)
+    d_embed = torch.empty((V, D), dtype=grad_dtype, device=dev)
+    d_bias = torch.empty((V if bias is not None else 0,), dtype=grad_dtype, device=dev)
     L = _lib.load()
     ws_bytes = int(L.sparton_bwd_workspace_bytes(B, S, D, V))
     ws = torch.empty((max(ws_bytes, 1),), dtype=torch.uint8, device=dev)
     with torch.cuda.device(dev):
         rc = L.sparton_bwd(grad_out.data_ptr(), max_scores.data_ptr(),
-                           _lib.DTYPE_CODE[max_scores.dtype], max_idx.data_ptr(), mask.data_ptr(), _lib.MASK_CODE[mask.dtype], hidden.data_ptr(),
-                           embed.data_ptr(), d_hidden.data_ptr(), d_embed.data_ptr(),
+                           _lib.DTYPE_CODE[max_scores.dtype], max_idx.data_ptr(), mask.data_ptr(),
+                           _lib.MASK_CODE[mask.dtype], hidden.data_ptr(), embed.data_ptr(),
+                           d_hidden.data_ptr(), d_embed.data_ptr(),
                            d_bias.data_ptr() if bias is not None else None,
-                           ws.data_ptr(), ws_bytes, B, S, D, V, _lib.DTYPE_CODE[hidden.dtype],
-                           _stream(dev))
+                           _lib.DTYPE_CODE[grad_dtype], ws.data_ptr(), ws_bytes, B, S, D, V,
+                           _lib.DTYPE_CODE[hidden.dtype], _stream(dev))
     _lib.check(rc, op)
     return d_hidden, d_embed, d_bias
+
+
+@torch.library.custom_op("sparton::fused_sparton_bwd", mutates_args=())
+def fused_sparton_bwd(grad_out: Tensor, max_scores: Tensor, max_idx: Tensor, hidden: Tensor,
+                      embed: Tensor, bias: Optional[Tensor],
+                      mask: Tensor) -> Tuple[Tensor, Tensor, Tensor]:
+    """(dH [B,S,D], dW [V,D], dbias [V] or [0]) in float32.
+
+    Replaces fused_sparton_bwd_op (src/sparton/sparton_kernel.py:663-685)."""
+    return _bwd_impl(grad_out, max_scores, max_idx, hidden, embed, bias, mask, torch.float32,
+                     "sparton::fused_sparton_bwd")
 
 
 @fused_sparton_bwd.register_fake
@@ -195,6 +201,23 @@ def _(grad_out, max_scores, max_idx, hidden, embed, bias, mask):
     return (torch.empty_like(hidden, dtype=torch.float32),
             torch.empty_like(embed, dtype=torch.float32),
             hidden.new_empty((embed.shape[0] if bias is not None else 0,), dtype=torch.float32))
+
+
+@torch.library.custom_op("sparton::fused_sparton_bwd_train", mutates_args=())
+def fused_sparton_bwd_train(grad_out: Tensor, max_scores: Tensor, max_idx: Tensor,
+                            hidden: Tensor, embed: Tensor, bias: Optional[Tensor],
+                            mask: Tensor) -> Tuple[Tensor, Tensor, Tensor]:
+    """The backward of fused_sparton_fwd_train: gradients in hidden's dtype, each rounded
+    once from its fp32 sum (the values autograd's cast of fp32 gradients would give,
+    without the extra pass over dW and dH)."""
+    return _bwd_impl(grad_out, max_scores, max_idx, hidden, embed, bias, mask, hidden.dtype,
+                     "sparton::fused_sparton_bwd_train")
+
+
+@fused_sparton_bwd_train.register_fake
+def _(grad_out, max_scores, max_idx, hidden, embed, bias, mask):
+    return (torch.empty_like(hidden), torch.empty_like(embed),
+            hidden.new_empty((embed.shape[0] if bias is not None else 0,)))
 
 
 def _setup_context(ctx, inputs, output):
@@ -218,12 +241,15 @@ def _setup_context_train(ctx, inputs, output):
     hidden, embed, bias, mask = inputs
     _scores, idx, scores32 = output
     ctx.mark_non_differentiable(idx, scores32)
+    ctx.set_materialize_grads(False)  # no zero tensors for the two index/aux outputs
     ctx.save_for_backward(scores32, idx, hidden, embed, bias, mask)
 
 
 def _backward_train(ctx, grad_scores, grad_idx, grad_scores32):
     scores32, idx, hidden, embed, bias, mask = ctx.saved_tensors
-    d_hidden, d_embed, d_bias = torch.ops.sparton.fused_sparton_bwd(
+    if grad_scores is None:
+        return None, None, None, None
+    d_hidden, d_embed, d_bias = torch.ops.sparton.fused_sparton_bwd_train(
         grad_scores, scores32, idx, hidden, embed, bias, mask)
     return d_hidden, d_embed, (d_bias if bias is not None else None), None
 

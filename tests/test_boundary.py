@@ -60,7 +60,8 @@ def fwd(**kw):
 
 def bwd(**kw):
     a = dict(grad=P, reps=P, reps_dtype=1, argmax=P, mask=P, mask_dtype=0, hidden=P, weight=P,
-             dH=P, dW=P, db=None, ws=None, ws_bytes=0, B=2, S=4, D=64, V=10, dtype=1, stream=None)
+             dH=P, dW=P, db=None, grad_dtype=0, ws=None, ws_bytes=0, B=2, S=4, D=64, V=10, dtype=1,
+             stream=None)
     a.update(kw)
     return _lib.load().sparton_bwd(*a.values())
 
@@ -75,7 +76,9 @@ def test_fwd_argument_validation(kw, code):
 
 
 @pytest.mark.parametrize("kw,code", [
-    (dict(S=-2), -1), (dict(dtype=-1), -1), (dict(reps_dtype=3), -1), (dict(grad=None), -1),
+    (dict(S=-2), -1), (dict(dtype=-1), -1), (dict(reps_dtype=3), -1), (dict(grad_dtype=2), -1),
+    (dict(grad=None), -1), (dict(dH=P + 4, grad_dtype=1, ws=P, ws_bytes=1 << 30), -2),
+    (dict(dW=P + 8, grad_dtype=0, ws=P, ws_bytes=1 << 30), -2),
     (dict(weight=None), -1),
     (dict(D=12), -1), (dict(dH=P + 4), -2), (dict(ws=None), -4), (dict(ws=P, ws_bytes=16), -4),
     (dict(S=1 << 20), -3), (dict(B=1 << 20), -3), (dict(dH=None, dW=None, db=None), 0),
@@ -156,6 +159,8 @@ def test_fake_kernels_give_reference_metadata():
         dh, dw, db = torch.ops.sparton.fused_sparton_bwd(r, r32, i, H, W, b, m)
         assert dh.shape == H.shape and dw.shape == W.shape and db.shape == (40,)
         assert dh.dtype == dw.dtype == db.dtype == torch.float32
+        th, tw, tb = torch.ops.sparton.fused_sparton_bwd_train(r, r32, i, H, W, b, m)
+        assert th.dtype == tw.dtype == tb.dtype == torch.bfloat16 and tw.shape == W.shape
         _, _, db0 = torch.ops.sparton.fused_sparton_bwd(r, r, i, H, W, None, m)
         assert db0.shape == (0,)
 

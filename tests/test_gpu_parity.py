@@ -72,6 +72,9 @@ CASES = [
     ("bf16", 2, 256, 768, 4099, True, "holes"),
     ("fp16", 3, 33, 16, 70, True, "f16"),
     ("fp32", 1, 5, 4, 1, False, "int64"),
+    ("bf16", 2, 50, 72, 300, True, "int64"),    # K tail: 144-byte rows (2 slabs + tail)
+    ("fp32", 2, 20, 40, 260, False, "holes"),   # K tail: 160-byte rows
+    ("fp16", 3, 130, 24, 520, True, "int64"),   # rows shorter than one slab, 3 vocab tiles
 ]
 
 
@@ -160,6 +163,22 @@ def test_deterministic_repeat(device):
     torch.cuda.synchronize()
     for a, c in zip(*outs):
         assert torch.equal(a, c)
+
+
+@pytest.mark.parametrize("cfg", [2, 3])
+def test_training_backward_is_fp32_rounded_once(cfg, device):
+    """fused_sparton_bwd_train writes each gradient in the input dtype, rounded once from
+    the same fp32 sum the fp32 op returns: bitwise equal to that output's cast."""
+    w = WORKLOADS[cfg]
+    say(f"bwd_train vs bwd, config {cfg}")
+    inp = make_inputs(w).to(device)
+    r, i, r32 = torch.ops.sparton.fused_sparton_fwd_train(inp.hidden, inp.weight, inp.bias, inp.mask)
+    f = torch.ops.sparton.fused_sparton_bwd(inp.grad, r32, i, inp.hidden, inp.weight, inp.bias, inp.mask)
+    t = torch.ops.sparton.fused_sparton_bwd_train(inp.grad, r32, i, inp.hidden, inp.weight, inp.bias,
+                                                 inp.mask)
+    for a, c in zip(t, f):
+        assert a.dtype == w.dtype
+        assert torch.equal(a, c.to(w.dtype))
 
 
 def test_encode_equals_training_forward(device):
