@@ -9,9 +9,13 @@ configuration (B=32, S=256, D=768, V=30522, bf16) unless --config says otherwise
 
 Prints ONE JSON line. Besides the throughput it reports:
   roofline      the forward kernel (MFMA-bound): useful flops 2*D*V*sum_b(len_b)
-                per launch / its mean duration from HIP events, vs 2.5 PFLOP/s.
+                per launch / its mean duration, measured with HIP events around the
+                forward of every timed step (on torch's current stream, where the
+                kernel is launched), vs 2.5 PFLOP/s. `traffic` is the kernel's HBM
+                bytes per launch from rocprofv3 FETCH_SIZE/WRITE_SIZE passes, read from
+                profiles/hbm_traffic_cfg<N>.json when that file covers this workload.
   bwd_roofline  the backward kernels (HBM-bound): compulsory bytes per call / their
-                mean duration from HIP events, vs 8 TB/s.
+                mean duration from the same in-step HIP events, vs 8 TB/s.
   cpu_baseline  the reference's torch head (training/model.py:56-62, restated in
                 oracle/) fwd+bwd on the host cores, on a bounded sample of batch rows.
 """
@@ -41,6 +45,8 @@ def parse():
     p.add_argument("--kernel-reps", type=int, default=50, help="back-to-back launches per kernel timing")
     p.add_argument("--cpu-seconds", type=float, default=25.0, help="budget (s) of the CPU baseline leg")
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--copy-probe-mib", type=int, default=0,
+                   help="after timing, launch one device copy of this many MiB (PMC calibration)")
     return p.parse_args()
 
 
@@ -52,6 +58,22 @@ def cpu_model():
     except OSError:
         pass
     return "unknown"
+
+
+FWD_KERNEL = "sparton::fwd::sparton_fwd_kernel<%s>"
+KNAME = {"bf16": "bf16", "fp16": "f16", "fp32": "f32"}
+
+
+def measured_traffic(config, kernel):
+    """HBM bytes per launch of `kernel` from the committed PMC summary for this config
+    (sparton_amd.profiling traffic output), or (None, reason)."""
+    path = os.path.join(ROOT, "profiles", f"hbm_traffic_cfg{config}.json")
+    try:
+        with open(path) as f:
+            k = json.load(f)["kernels"][kernel]
+    except (OSError, KeyError, ValueError):
+        return None, "no PMC summary for this workload"
+    return k["traffic_bytes"], os.path.relpath(path, ROOT)
 
 
 def time_events(torch, fn, reps):
@@ -158,26 +180,49 @@ def main():
     torch.cuda.synchronize()
     torch.cuda.reset_peak_memory_stats()
 
+    # Events bracket the forward and the backward of every timed step; they are
+    # recorded on torch's current stream, the stream the kernels are launched on.
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
+
+    def timed_step(e):
+        H.grad = None
+        for p in params:
+            p.grad = None
+        e[0].record()
+        reps = head(H, mask)
+        e[1].record()
+        reps.backward(G)
+        e[2].record()
+
     # ---- timed region: exactly K steps --------------------------------------------
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for _ in range(args.steps):
-        step()
+    for i in range(args.steps):
+        timed_step(ev[i])
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
+    fwd_live = statistics.mean(e[0].elapsed_time(e[1]) for e in ev)
+    bwd_live = statistics.mean(e[1].elapsed_time(e[2]) for e in ev)
     peak_bytes = torch.cuda.max_memory_allocated()
     ms_per_step = elapsed * 1e3 / args.steps
     tokens = w.B * w.S
     value = tokens / (elapsed / args.steps)
 
-    # ---- per-kernel timing (HIP events, back-to-back launches) ----------------------
+    # ---- per-op timing outside the step (HIP events, back-to-back launches) ----------
     Hd, Wd, bd = H.detach(), head.weight.detach(), (head.bias.detach() if has_bias else None)
-    fwd_ms = time_events(torch, lambda: torch.ops.sparton.fused_sparton_fwd_train(Hd, Wd, bd, mask),
-                         args.kernel_reps)
+    fwd_b2b = time_events(torch, lambda: torch.ops.sparton.fused_sparton_fwd_train(Hd, Wd, bd, mask),
+                          args.kernel_reps)
     enc_ms = time_events(torch, lambda: torch.ops.sparton.fused_sparton_encode(Hd, Wd, bd, mask), args.kernel_reps)
     _, idx, reps = torch.ops.sparton.fused_sparton_fwd_train(Hd, Wd, bd, mask)
-    bwd_ms = time_events(torch, lambda: torch.ops.sparton.fused_sparton_bwd_train(G, reps, idx, Hd, Wd, bd, mask),
-                         args.kernel_reps)
+    bwd_b2b = time_events(torch, lambda: torch.ops.sparton.fused_sparton_bwd_train(G, reps, idx, Hd, Wd, bd, mask),
+                          args.kernel_reps)
+    fwd_ms, bwd_ms = fwd_live, bwd_live
+    if args.copy_probe_mib > 0:
+        src = torch.empty(args.copy_probe_mib << 20, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
 
     # forward roofline: useful flops on valid positions (masked positions are skipped)
     valid_tokens = int(inp_cpu.mask.ne(0).sum())
@@ -201,6 +246,7 @@ def main():
     bwd_bytes = (w.B * w.V * (e + 4 + 4) + u_w * w.D * e + u_h * w.D * e
                  + w.B * w.S * w.D * e + w.V * w.D * e + (w.V * e if has_bias else 0))
     bwd_gbs = bwd_bytes / (bwd_ms * 1e-3) / 1e9
+    traffic, traffic_src = measured_traffic(args.config, FWD_KERNEL % KNAME[dname])
 
     out = {
         "metric": METRIC,
@@ -218,16 +264,17 @@ def main():
         "config": {"workload": f"{w.name} SpartonHead fwd+bwd", "B": w.B, "S": w.S, "D": w.D, "V": w.V,
                    "global_batch": w.B, "seq_len": w.S, "use_bias": has_bias,
                    "valid_tokens": valid_tokens, "parallelism": "none (1 GPU)"},
-        "roofline": {"bound": "mfma", "kernel": "sparton_fwd_kernel", "achieved": round(fwd_tflops, 2),
+        "roofline": {"bound": "mfma", "kernel": FWD_KERNEL % KNAME[dname], "achieved": round(fwd_tflops, 2),
                      "peak": peak_tf, "unit": "TFLOP/s", "frac": round(fwd_tflops / peak_tf, 4),
-                     "traffic": None, "flops_per_launch": useful_flops,
+                     "traffic": traffic, "traffic_source": traffic_src, "flops_per_launch": useful_flops,
                      "flops_basis": "useful: 2*D*V*valid_tokens (fully masked 32-row blocks are skipped)",
                      "dense_equiv_tflops": round(dense_flops / (fwd_ms * 1e-3) / 1e12, 2),
-                     "mean_ms": round(fwd_ms, 4)},
+                     "mean_ms": round(fwd_ms, 4), "timing": "HIP events around each timed step's forward",
+                     "mean_ms_back_to_back": round(fwd_b2b, 4)},
         "bwd_roofline": {"bound": "hbm", "achieved": round(bwd_gbs, 1), "peak": PEAK_HBM_GBS,
                          "unit": "GB/s", "frac": round(bwd_gbs / PEAK_HBM_GBS, 4),
                          "bytes_per_call": bwd_bytes, "nnz": nnz, "U_W": u_w, "U_H": u_h,
-                         "mean_ms": round(bwd_ms, 4)},
+                         "mean_ms": round(bwd_ms, 4), "mean_ms_back_to_back": round(bwd_b2b, 4)},
         "fwd_ms": round(fwd_ms, 4),
         "encode_ms": round(enc_ms, 4),
         "bwd_ms": round(bwd_ms, 4),
