@@ -75,6 +75,16 @@ CASES = [
     ("bf16", 2, 50, 72, 300, True, "int64"),    # K tail: 144-byte rows (2 slabs + tail)
     ("fp32", 2, 20, 40, 260, False, "holes"),   # K tail: 160-byte rows
     ("fp16", 3, 130, 24, 520, True, "int64"),   # rows shorter than one slab, 3 vocab tiles
+    ("bf16", 3, 900, 64, 2100, True, "gaps"),   # fully masked middle chunk, masked row
+]
+
+# Cases run again with several vocab tiles per workgroup (the unit stream then crosses
+# vocab tiles and chunks inside one workgroup, including a partial last group).
+MULTI_TILE_CASES = [
+    (("bf16", 3, 900, 64, 2100, True, "gaps"), 3),
+    (("fp32", 2, 40, 96, 1300, True, "frac"), 2),
+    (("fp16", 2, 300, 24, 1800, False, "bool"), 4),
+    (("bf16", 2, 256, 768, 4099, True, "holes"), 16),
 ]
 
 
@@ -95,6 +105,9 @@ def make_case(dt, B, S, D, V, bias, mk, seed=0):
     elif mk == "holes":
         m = (torch.rand(B, S, generator=g) < 0.5).long()
         m[0] = 0                                                   # an all-masked row
+    elif mk == "gaps":
+        m = (pad & ((torch.arange(S)[None] // 256) != 1)).long()  # chunk 1 all masked
+        m[1] = 0                                                   # an all-masked row
     elif mk == "frac":
         m = torch.randint(0, 3, (B, S), generator=g).float() * 0.5
     elif mk == "f16":
@@ -106,6 +119,17 @@ def make_case(dt, B, S, D, V, bias, mk, seed=0):
 @pytest.mark.parametrize("case", CASES, ids=["-".join(map(str, c)) for c in CASES])
 def test_random_shapes(case, device):
     say(f"random case {case}")
+    H, W, b, m, G = make_case(*case)
+    reps, idx, reps32, dH, dW, db = run_fwd_bwd(H, W, b, m, G, device)
+    n, bad = check_fwd(H, W, b, m, reps, idx)
+    say(f"  checked {n} entries, {bad} near-tie argmax differences")
+    check_bwd_isolated(H, W, b, m, G, reps32, idx, dH, dW, db)
+
+
+@pytest.mark.parametrize("case,P", MULTI_TILE_CASES, ids=[f"{'-'.join(map(str, c))}-P{p}" for c, p in MULTI_TILE_CASES])
+def test_multi_tile_workgroups(case, P, device, monkeypatch):
+    say(f"random case {case} with {P} vocab tiles per workgroup")
+    monkeypatch.setenv("SPARTON_FWD_TILES_PER_GROUP", str(P))
     H, W, b, m, G = make_case(*case)
     reps, idx, reps32, dH, dW, db = run_fwd_bwd(H, W, b, m, G, device)
     n, bad = check_fwd(H, W, b, m, reps, idx)
@@ -272,6 +296,15 @@ def test_edge_cases(device):
     m = torch.zeros(2, 0, dtype=torch.long, device=device)
     r, i = torch.ops.sparton.fused_sparton_fwd(H, W, None, m)
     assert torch.all(r == 0) and torch.all(i == 0)
+    # D == 0: x = bias * mask, the first valid position wins every positive column
+    H0 = torch.zeros(2, 5, 0, dtype=torch.bfloat16)
+    W0 = torch.zeros(40, 0, dtype=torch.bfloat16)
+    b0 = (torch.randn(40) * 0.5).bfloat16()
+    m0 = torch.tensor([[0, 1, 1, 0, 0], [1, 1, 1, 1, 1]])
+    r0, i0 = torch.ops.sparton.fused_sparton_fwd(H0.to(device), W0.to(device), b0.to(device), m0.to(device))
+    M0, I0, ref0 = oracle.fused_fwd_ref(H0, W0, b0, m0)
+    torch.testing.assert_close(r0.cpu().to(F64), ref0, **FWD_TOL)
+    assert torch.equal(i0.cpu().long(), I0)
     # non-multiple-of-8 hidden size goes through SpartonHead's zero padding
     B, S, D, V = 2, 9, 20, 50
     H = torch.randn(B, S, D).bfloat16()
