@@ -57,15 +57,24 @@ enum sparton_status {
   SPARTON_EINVAL = -1,       /* null pointer, bad shape or bad enum value */
   SPARTON_EALIGN = -2,       /* a base pointer is not 16-byte aligned */
   SPARTON_EUNSUPPORTED = -3, /* shape outside the supported range (see sparton_limits) */
-  SPARTON_EWORKSPACE = -4,   /* workspace missing or smaller than sparton_bwd_workspace_bytes */
+  SPARTON_EWORKSPACE = -4,   /* workspace missing or smaller than sparton_{fwd,bwd}_workspace_bytes */
 };
+
+/*
+ * Bytes of device scratch sparton_fwd needs for these sizes (256-byte aligned
+ * sections: the per-row block plan and the partial results of batch rows whose
+ * positions span several row tiles). No counterpart in the reference: its forward
+ * materializes a [B,S,C] logits tile per vocab tile instead (sparton_kernel.py:245-247).
+ */
+size_t sparton_fwd_workspace_bytes(int64_t B, int64_t S, int64_t D, int64_t V, int dtype);
 
 /*
  * Forward: reps[B,V] (in `dtype`) and argmax I[B,V] (int32).
  * `argmax` may be NULL: the inference-only variant then skips the index store.
  * `reps_f32` may be NULL; if given, it receives reps[B,V] unrounded in fp32, which a
  * training caller keeps for the backward instead of the rounded `reps`.
- * `bias` may be NULL (use_bias=False).
+ * `bias` may be NULL (use_bias=False). `workspace` (256-byte aligned, at least
+ * sparton_fwd_workspace_bytes) is overwritten; S <= 16384.
  *
  * Replaces the reference's forward path: fused_sparton_fwd_with_indices
  * (src/sparton/sparton_kernel.py:226-253), its V-tile GEMM (:204-210) and the
@@ -77,7 +86,7 @@ enum sparton_status {
 int sparton_fwd(const void* hidden, const void* weight, const void* bias,
                 const void* mask, int mask_dtype, void* reps, int32_t* argmax,
                 float* reps_f32, int64_t B, int64_t S, int64_t D, int64_t V,
-                int dtype, void* stream);
+                int dtype, void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * Bytes of device scratch sparton_bwd needs for these sizes (256-byte aligned

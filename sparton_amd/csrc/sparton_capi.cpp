@@ -4,7 +4,7 @@
 #define SPARTON_EXPORT extern "C" __attribute__((visibility("default")))
 
 namespace {
-constexpr int kAbiVersion = 1;
+constexpr int kAbiVersion = 2;
 constexpr int64_t kMaxBwdSeq = 16384;   // must match bwd::MAX_S in sparton_bwd.hip
 constexpr int64_t kMaxBwdBatch = 8192;  // must match bwd::MAX_B in sparton_bwd.hip
 }  // namespace
@@ -15,7 +15,7 @@ SPARTON_EXPORT const char* sparton_strerror(int code) {
     case SPARTON_EINVAL: return "invalid argument (null pointer, negative size, bad dtype, or D not a multiple of 16 bytes)";
     case SPARTON_EALIGN: return "a tensor base pointer is not 16-byte aligned (workspace: 256-byte)";
     case SPARTON_EUNSUPPORTED: return "shape outside the supported range (see sparton_limits)";
-    case SPARTON_EWORKSPACE: return "workspace missing or smaller than sparton_bwd_workspace_bytes()";
+    case SPARTON_EWORKSPACE: return "workspace missing or smaller than sparton_fwd/bwd_workspace_bytes()";
     default: return code > 0 ? "HIP kernel launch failed (code is the hipError_t)" : "unknown sparton status";
   }
 }

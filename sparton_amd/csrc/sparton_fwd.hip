@@ -1,30 +1,34 @@
-// SpartonHead forward on gfx950: one kernel, MFMA mainloop + fused reduction epilogue.
+// SpartonHead forward on gfx950: a plan pass, one MFMA kernel with a fused reduction
+// epilogue, and a small fixup pass.
 //
-// A workgroup owns one batch row b and P consecutive vocab tiles of BN columns. It
-// sweeps the sequence in chunks of BM positions; one (vocab tile, chunk) pair is a
-// "unit". For each unit it computes the BM x BN logit tile
-//     H[b, s0:s0+BM, :] . W[v0:v0+BN, :]^T
-// with bf16/fp16 (or fp32) MFMA, K = D streamed through double-buffered LDS, then folds
-// the tile into a running (max, argmax) per column in registers:
-//     x = (acc + bias[v]) * mask[b, s];  take x if x > best (strict, s ascending)
-// so the [B,S,V] logits never reach HBM. After the last chunk of a vocab tile the
-// per-column winners of the two M-waves are merged (larger value, ties -> lower s) and
-// the workgroup writes reps[b, v] = log1p(max(0, best)) and argmax[b, v].
+// Math (reference src/sparton/sparton_kernel.py):
+//     x[b,s,v] = (H[b,s,:] . W[v,:] + bias[v]) * mask[b,s]     bias :209-210/:245, mask :147
+//     M[b,v]   = max(0, max_s x),  I[b,v] = lowest s attaining M (0 if M == 0)
+//                                             init 0/0 :112-114, ties :151-156
+//     reps     = log1p(M)                                        :159-161 (log(1+x) there)
+// The [B,S,V] logits never reach HBM.
 //
-// Reference semantics followed (src/sparton/sparton_kernel.py):
-//   bias added to the GEMM output            :209-210, :245
-//   logits multiplied by mask                :147
-//   running max initialised to 0, idx to 0   :112-114
-//   lowest s wins ties (tl.argmax + strict >) :151-156
-//   reps = log(1 + relu(max))                :159-161 (log1p here)
+// Packing. Positions are grouped in 32-row blocks (b, j) = rows 32j..32j+31 of batch
+// row b. A block whose mask is all zero contributes x = 0, which never beats the
+// initial 0, so it is dropped. The plan pass lists the remaining ("active") blocks in
+// (b, j) order, and the main kernel multiplies them eight at a time: M-tile m holds
+// active blocks 8m..8m+7, i.e. 256 rows that may belong to several batch rows. Every
+// tile except the last is full, so each decoder tile loaded from memory is used for
+// 256 live rows instead of one batch row's (often partly padded) 256 positions.
 //
-// Pipeline: the K slabs of all units of a workgroup form one stream through the two
-// LDS stages, so the first two slabs of a unit are loaded while the previous unit
-// finishes its last slab and runs its epilogue (no per-tile load latency on the
-// critical path). The mask row of b is scanned once per workgroup: all-zero 32-row
-// blocks contribute x = 0, which never beats the initial 0, so chunks without an
-// active block are skipped and, inside a chunk, a wave only multiplies its blocks up
-// to the last active one and A rows past it are not loaded.
+// Main kernel. A workgroup owns one M-tile and P consecutive vocab tiles of BN columns
+// (a "unit" per vocab tile). For each unit it computes the 256 x BN logit tile with
+// bf16/fp16 (or fp32) MFMA, K = D streamed through two LDS stages; the K slabs of all
+// its units form one stream, so a unit's first slabs load while the previous unit
+// finishes. The epilogue folds each 32-row block into a per-column (max, argmax),
+// merges consecutive blocks of the same batch row in s order (larger value; on ties
+// the lower s, which is the earlier block), and per batch-row segment either writes
+// reps/argmax (segment complete in this tile) or, when the segment continues into a
+// neighbouring tile, writes the partial (max, argmax) to the workspace.
+//
+// Fixup kernel. For each batch row whose blocks span several M-tiles it merges those
+// partials in tile order (= s order) and writes reps/argmax; for a batch row with no
+// active block it writes reps = 0, argmax = 0.
 //
 // Data movement: K slabs of 128 bytes per row go straight from global memory into
 // LDS (global_load_lds_dwordx4, no VGPR staging). LDS rows are 128 bytes with the
@@ -39,18 +43,20 @@
 
 #include <stdlib.h>
 
+#include <algorithm>
+
 #include "sparton_common.h"
 
 namespace sparton {
 namespace fwd {
 
-constexpr int BM = 256;              // sequence positions per chunk
+constexpr int BM = 256;              // rows per M-tile
 constexpr int BN = 256;              // vocab columns per tile
-constexpr int WAVES_M = 2;           // waves along M (sequence)
+constexpr int WAVES_M = 2;           // waves along M
 constexpr int WAVES_N = 4;           // waves along N (vocab)
 constexpr int NWAVES = WAVES_M * WAVES_N;
 constexpr int NTHREADS = 64 * NWAVES;
-constexpr int MBLK = BM / 32;        // 32-row MFMA blocks per chunk (8)
+constexpr int MBLK = BM / 32;        // 32-row blocks per M-tile (8)
 constexpr int NB_PER_WAVE = BN / WAVES_N / 32;     // 2
 constexpr int SLAB = 128;            // bytes of K per row per pipeline stage
 constexpr int CHUNKS = SLAB / 16;    // 16-byte chunks per row slab (8)
@@ -58,24 +64,131 @@ constexpr int ROWS_PER_LOAD = 64 / CHUNKS;          // rows one wave-wide load c
 constexpr int A_LOADS = BM / ROWS_PER_LOAD / NWAVES;  // wave-wide loads per slab for A (4)
 constexpr int B_LOADS = BN / ROWS_PER_LOAD / NWAVES;  // and for B (4)
 constexpr int GROUP_V = 4;           // vocab-tile groups per scheduling group (L2 reuse)
-constexpr int MAX_CHUNKS = 64;       // S <= MAX_CHUNKS * BM
-constexpr int MAX_P = 16;            // vocab tiles per workgroup
+constexpr int MAX_P = 8;             // vocab tiles per workgroup
+constexpr int MAX_S = 16384;         // positions per batch row (512 blocks)
+constexpr int PLAN_THREADS = 1024;
+
+// ---- workspace ------------------------------------------------------------------
+
+// Device scratch of one launch, carved from the caller's workspace (256-byte aligned
+// sections). nblk = blocks per batch row, n_mt_max = M-tiles if every block is active.
+struct Work {
+  int* meta;          // [0] active blocks
+  int* count;         // [B] active blocks per batch row
+  int* first;         // [B] index of its first active block in `list`
+  uint8_t* flag;      // [B][nblk] 1 = block has a nonzero mask entry
+  int* list;          // [B*nblk] active blocks as b * nblk + j, in (b, j) order
+  float2* part;       // [n_mt_max][2][V] partial (max, argmax bits) of edge segments
+  size_t total;
+};
+
+static Work carve(void* base, int64_t B, int64_t S, int64_t V) {
+  const int64_t nblk = cdiv(S, 32);
+  const int64_t n_mt_max = cdiv(B * nblk, 8);
+  char* p = (char*)base;
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    const size_t o = off;
+    off += (size_t)round_up((int64_t)bytes, 256);
+    return p != nullptr ? p + o : nullptr;
+  };
+  Work w;
+  w.meta = (int*)take(16);
+  w.count = (int*)take((size_t)B * 4);
+  w.first = (int*)take((size_t)B * 4);
+  w.flag = (uint8_t*)take((size_t)(B * nblk));
+  w.list = (int*)take((size_t)(B * nblk) * 4);
+  w.part = (float2*)take((size_t)(n_mt_max * 2 * V) * sizeof(float2));
+  w.total = off;
+  return w;
+}
+
+// ---- plan -------------------------------------------------------------------------
+
+// One wave per batch row: which 32-row blocks have a nonzero mask entry.
+__global__ __launch_bounds__(256) void fwd_plan_rows_kernel(const void* __restrict__ mask,
+                                                            int mask_dtype, int B, int S, int nblk,
+                                                            uint8_t* __restrict__ flag,
+                                                            int* __restrict__ count) {
+  const int lane = threadIdx.x & 63;
+  const int b = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (b >= B) return;
+  int n = 0;
+  for (int s0 = 0; s0 < nblk * 32; s0 += 64) {
+    const int s = s0 + lane;
+    const bool nz = s < S && load_mask(mask, mask_dtype, (int64_t)b * S + s) != 0.0f;
+    const uint64_t bal = __ballot(nz);
+    const int j = s0 / 32;
+    const int lo = (bal & 0xffffffffull) != 0 ? 1 : 0;
+    const int hi = (j + 1 < nblk && (bal >> 32) != 0) ? 1 : 0;
+    if (lane == 0) flag[(int64_t)b * nblk + j] = (uint8_t)lo;
+    if (lane == 1 && j + 1 < nblk) flag[(int64_t)b * nblk + j + 1] = (uint8_t)hi;
+    n += lo + hi;
+  }
+  if (lane == 0) count[b] = n;
+}
+
+// One workgroup: exclusive scan of the per-row counts, then the block list.
+__global__ __launch_bounds__(PLAN_THREADS) void fwd_plan_list_kernel(
+    int B, int nblk, const uint8_t* __restrict__ flag, const int* __restrict__ count,
+    int* __restrict__ first, int* __restrict__ list, int* __restrict__ meta) {
+  __shared__ int wsum[PLAN_THREADS / 64];
+  __shared__ int carry;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  if (tid == 0) carry = 0;
+  __syncthreads();
+  for (int b0 = 0; b0 < B; b0 += PLAN_THREADS) {
+    const int b = b0 + tid;
+    const int c = b < B ? count[b] : 0;
+    int x = c;  // inclusive scan within the wave, then across waves
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const int y = __shfl_up(x, d);
+      if (lane >= d) x += y;
+    }
+    if (lane == 63) wsum[wave] = x;
+    __syncthreads();
+    int before = carry;
+    for (int w = 0; w < wave; ++w) before += wsum[w];
+    const int start = before + x - c;
+    if (b < B) first[b] = start;
+    __syncthreads();
+    if (tid == PLAN_THREADS - 1) carry = start + c;
+    __syncthreads();
+  }
+  if (tid == 0) meta[0] = carry;
+  for (int b = tid; b < B; b += PLAN_THREADS) {
+    int k = first[b];
+    const uint8_t* f = flag + (int64_t)b * nblk;
+    for (int j = 0; j < nblk; ++j)
+      if (f[j]) list[k++] = b * nblk + j;
+  }
+}
+
+// ---- main kernel ------------------------------------------------------------------
 
 struct Smem {
   u32x4 a[2][BM * CHUNKS];   // [stage][row * 8 + (chunk ^ f(row))]
   u32x4 b[2][BN * CHUNKS];
-  float maskf[BM];           // mask of the current unit's chunk
+  float maskf[BM];           // mask of the tile's rows (0 past S or past the last block)
   float biasf[MAX_P * BN];   // bias of the workgroup's vocab tiles
-  float red_v[WAVES_M][BN];  // cross-wave merge of the per-column winners
-  int red_i[WAVES_M][BN];
-  uint8_t chunk_fl[MAX_CHUNKS];  // per chunk: bit j = block j has a nonzero mask entry
-  uint8_t chunk_list[MAX_CHUNKS];
-  int n_active;                  // chunks with an active block
+  float pv[MBLK][BN];        // per block, per column: (max, argmax) of the block's rows
+  int pi[MBLK][BN];
+  int blk_b[MBLK + 2];       // batch row of each block; [MBLK], [MBLK+1]: rows of the
+                             // blocks just before / after the tile (-1 if none)
+  int blk_s[MBLK];           // first position of each block (32 j)
 };
 
 typedef __attribute__((address_space(3))) void lds_void;
 
 __device__ __forceinline__ int swz_key(int row) { return (row & 7) ^ ((row >> 3) & 1); }
+
+// Byte offset, within a 128-byte row slab, of the 16-byte chunk that lane L copies in
+// a wave-wide load of tile row `row` (= 8g + L/8): physical chunk L%8 holds logical
+// chunk (L%8) ^ f(row), so the lane reads that logical chunk from global memory.
+__device__ __forceinline__ uint32_t lane_chunk(int row, int lane) {
+  return (uint32_t)(((lane & 7) ^ swz_key(row)) * 16);
+}
 
 // One MFMA "step" consumes 16 bytes of A and B per lane.
 template <typename T> struct Mfma;
@@ -106,75 +219,60 @@ template <> struct Mfma<float> {
   }
 };
 
-// Map the hardware workgroup id to (b, vocab-tile group). Workgroups are dispatched
-// round-robin over the 8 XCDs; first make ids that share an XCD consecutive, then
-// walk groups of GROUP_V vocab-tile groups x all batch rows so the workgroups
-// resident on one XCD at a time share a few W tiles and a few H rows in its L2.
-__device__ __forceinline__ void tile_of(int wg, int grid, int B, int n_vg, int* b, int* vg) {
+// Map the hardware workgroup id to (M-tile, vocab-tile group). Workgroups are
+// dispatched round-robin over the 8 XCDs; first make ids that share an XCD
+// consecutive, then walk groups of GROUP_V vocab-tile groups x all M-tiles, so the
+// workgroups resident on one XCD at a time share a few W tiles and a few M-tiles'
+// rows in its L2.
+__device__ __forceinline__ void tile_of(int wg, int grid, int n_mt, int n_vg, int* m, int* vg) {
   const int xcd = wg & 7, local = wg >> 3, q = grid >> 3, r = grid & 7;
   const int lin = (xcd < r ? xcd * (q + 1) : r * (q + 1) + (xcd - r) * q) + local;
-  const int group = lin / (GROUP_V * B);
-  const int rem = lin - group * GROUP_V * B;
+  const int group = lin / (GROUP_V * n_mt);
+  const int rem = lin - group * GROUP_V * n_mt;
   const int gv = min(GROUP_V, n_vg - group * GROUP_V);
-  *b = rem / gv;
+  *m = rem / gv;
   *vg = group * GROUP_V + rem % gv;
 }
 
-__device__ __forceinline__ void merge(float& v, int& i, float ov, int oi) {
-  if (ov > v || (ov == v && oi < i)) { v = ov; i = oi; }
-}
-
-// One (vocab tile, chunk) unit: workgroup-uniform scalars.
-struct Unit {
-  int v0, s0;
-  int last_blk;   // highest 32-row block of the chunk with a nonzero mask entry
-};
-
-// Wave w, load i covers the 8-row group g = i * NWAVES + w; lane L lands at LDS chunk
-// g*64 + L, i.e. row 8g + L/8, physical chunk L%8, which holds logical chunk (L%8) ^ f(row).
-__device__ __forceinline__ void load_rows(int i, int wave, int lane, int* row, int* chunk) {
-  const int g = i * NWAVES + wave;
-  *row = g * ROWS_PER_LOAD + (lane >> 3);
-  *chunk = (lane & 7) ^ swz_key(*row);
-}
-
 struct Geo {
-  const char* H;      // row (b, 0) of H
+  const char* H;      // H[0, 0, :]
   const char* W;
   int row_bytes;      // D * sizeof(T)
   int nk_full;        // slabs lying entirely inside the row
-  int S, V;
+  int V;
+  int n_valid;        // active blocks in this M-tile (1..8)
+  uint32_t a_off[A_LOADS];  // per lane: byte offset from H of its A row and chunk
 };
 
-// Issue the direct global -> LDS copies of K slab k of unit u into stage buf. Chunks
-// past the row end (tail or padding slabs) re-read slab 0 -- valid, finite data -- and
-// their W copies are zeroed by zero_tail() before use. Rows past S or V re-read the
-// last row (their results are masked out or never stored).
-__device__ __forceinline__ void issue_slab(Smem& sm, const Geo& g, const Unit& u, int k, int buf,
+// Issue the direct global -> LDS copies of K slab k of vocab tile v0 into stage buf.
+// Wave w, load i covers the 8-row group g = i * NWAVES + w (rows 8g..8g+7 of the
+// tile, in block g / 4); lane L lands at LDS chunk g*64 + L. Chunks past the row end
+// (tail or padding slabs) re-read slab 0 -- valid, finite data -- and their W copies
+// are zeroed by zero_tail() before use. W rows past V re-read row V-1 (never stored);
+// A loads of blocks past the last active one are skipped.
+__device__ __forceinline__ void issue_slab(Smem& sm, const Geo& g, int v0, int k, int buf,
                                            int wave, int lane) {
   const uint32_t kb = (uint32_t)k * SLAB;
   const bool tail = k >= g.nk_full;
-  const char* ab = g.H + (int64_t)u.s0 * g.row_bytes;
-  const char* bb = g.W + (int64_t)u.v0 * g.row_bytes;
-  const int a_groups = (u.last_blk + 1) * (32 / ROWS_PER_LOAD);
+  const int a_groups = g.n_valid * (32 / ROWS_PER_LOAD);
 #pragma unroll
   for (int i = 0; i < A_LOADS; ++i) {
     const int grp = i * NWAVES + wave;
-    if (grp < a_groups) {
-      int row, c;
-      load_rows(i, wave, lane, &row, &c);
-      uint32_t off = (uint32_t)min(row, g.S - 1 - u.s0) * (uint32_t)g.row_bytes + c * 16;
-      off += (!tail || kb + c * 16 < (uint32_t)g.row_bytes) ? kb : 0u;
-      __builtin_amdgcn_global_load_lds((const void*)(ab + off), (lds_void*)&sm.a[buf][grp * 64], 16, 0, 0);
-    }
+    const uint32_t c16 = lane_chunk(grp * ROWS_PER_LOAD + (lane >> 3), lane);
+    const uint32_t step = (!tail || kb + c16 < (uint32_t)g.row_bytes) ? kb : 0u;
+    if (grp < a_groups)
+      __builtin_amdgcn_global_load_lds((const void*)(g.H + (g.a_off[i] + step)),
+                                       (lds_void*)&sm.a[buf][grp * 64], 16, 0, 0);
   }
+  const char* bb = g.W + (int64_t)v0 * g.row_bytes;
+  const int b_last = g.V - 1 - v0;
 #pragma unroll
   for (int i = 0; i < B_LOADS; ++i) {
     const int grp = i * NWAVES + wave;
-    int row, c;
-    load_rows(i, wave, lane, &row, &c);
-    uint32_t off = (uint32_t)min(row, g.V - 1 - u.v0) * (uint32_t)g.row_bytes + c * 16;
-    off += (!tail || kb + c * 16 < (uint32_t)g.row_bytes) ? kb : 0u;
+    const int row = grp * ROWS_PER_LOAD + (lane >> 3);
+    const uint32_t c16 = lane_chunk(row, lane);
+    const uint32_t step = (!tail || kb + c16 < (uint32_t)g.row_bytes) ? kb : 0u;
+    const uint32_t off = (uint32_t)min(row, b_last) * (uint32_t)g.row_bytes + c16 + step;
     __builtin_amdgcn_global_load_lds((const void*)(bb + off), (lds_void*)&sm.b[buf][grp * 64], 16, 0, 0);
   }
 }
@@ -185,10 +283,9 @@ __device__ __forceinline__ void zero_tail(Smem& sm, int row_bytes, int k, int bu
   const uint32_t kb = (uint32_t)k * SLAB;
 #pragma unroll
   for (int i = 0; i < B_LOADS; ++i) {
-    int row, c;
-    load_rows(i, wave, lane, &row, &c);
-    if (kb + c * 16 >= (uint32_t)row_bytes)
-      sm.b[buf][(i * NWAVES + wave) * 64 + lane] = u32x4{0, 0, 0, 0};
+    const int grp = i * NWAVES + wave;
+    if (kb + lane_chunk(grp * ROWS_PER_LOAD + (lane >> 3), lane) >= (uint32_t)row_bytes)
+      sm.b[buf][grp * 64 + lane] = u32x4{0, 0, 0, 0};
   }
 }
 
@@ -225,24 +322,15 @@ __device__ __forceinline__ void wait_loads_at_most(int n) {
   }
 }
 
-// Prefetched state for the next unit.
-struct Next {
-  bool valid;
-  bool new_tile;      // next unit starts another vocab tile
-  Unit u;
-};
-
-// Mainloop + chunk epilogue of one unit, for a wave with JM blocks to multiply.
+// Mainloop + block epilogue of one unit (vocab tile v0), for a wave with JM blocks.
 // On entry slab 0 of the unit has landed in stage `buf` (and is visible) and slab 1 is
-// in flight or landed in the other stage. On exit slab 0 of the next unit has landed
-// and its slab 1 is in flight. Returns the stage of the next unit's slab 0.
+// in flight or landed in the other stage. On exit the next unit's slab 0 (if any) has
+// landed and its slab 1 is in flight, and pv/pi hold this wave's blocks' results.
+// Returns the stage of the next unit's slab 0.
 template <typename T, int JM>
-__device__ __forceinline__ int run_unit(Smem& sm, const Geo& g, const Unit& u, const Next& nx,
-                                        int nk, int buf, int wave, int lane, int wm, int wn,
-                                        const void* mask, int mask_dtype, int64_t mrow,
-                                        int S, int btile, float* best, int* bidx) {
+__device__ __forceinline__ int run_unit(Smem& sm, const Geo& g, int v0, int v0_next, int nk,
+                                        int buf, int btile, int wave, int lane, int wm, int wn) {
   constexpr int JA = JM > 0 ? JM : 1;
-  const int tid = threadIdx.x;
   const int l32 = lane & 31, h = lane >> 5;
   f32x16 acc[JA][NB_PER_WAVE];
 #pragma unroll
@@ -254,25 +342,12 @@ __device__ __forceinline__ int run_unit(Smem& sm, const Geo& g, const Unit& u, c
       for (int i = 0; i < 16; ++i) acc[j][nb][i] = bc;
   }
 
-  // This unit's mask: loaded at step 0, stored at step 1 (the previous unit's
-  // epilogue is done with maskf by then), read by the epilogue below.
-  float mv = 0.0f;
-  if (nk == 0) {  // D == 0: no slabs; store the mask between two barriers
-    lds_barrier();
-    if (tid < BM) sm.maskf[tid] = u.s0 + tid < S ? load_mask(mask, mask_dtype, mrow + u.s0 + tid) : 0.0f;
-    lds_barrier();
-  }
   for (int k = 0; k < nk; ++k) {
     const int cur = buf ^ (k & 1);
     if (k >= g.nk_full) {  // tail / padding slab: clear W past D before use
       zero_tail(sm, g.row_bytes, k, cur, wave, lane);
       lds_barrier();
     }
-    if (k == 0 && tid < BM) {
-      const int s = u.s0 + tid;
-      mv = s < S ? load_mask(mask, mask_dtype, mrow + s) : 0.0f;
-    }
-    if (k == 1 && tid < BM) sm.maskf[tid] = mv;
     if (JM > 0) {
       // Every operand row is (multiple of 32) + l32, so its swizzle key is key(l32):
       // a fragment's LDS index is a per-lane offset plus a compile-time row offset.
@@ -315,252 +390,290 @@ __device__ __forceinline__ int run_unit(Smem& sm, const Geo& g, const Unit& u, c
     drain_and_sync();
     // Stage `cur` is free: refill it with the slab two ahead in the stream.
     const bool own = k + 2 < nk;
-    if (own || nx.valid) {
-      Unit t;
-      t.v0 = own ? u.v0 : nx.u.v0;
-      t.s0 = own ? u.s0 : nx.u.s0;
-      t.last_blk = own ? u.last_blk : nx.u.last_blk;
-      issue_slab(sm, g, t, own ? k + 2 : k + 2 - nk, cur, wave, lane);
-    }
+    if (own || v0_next >= 0) issue_slab(sm, g, own ? v0 : v0_next, own ? k + 2 : k + 2 - nk, cur, wave, lane);
   }
 
-  // Chunk epilogue: 32x32 accumulator layout -- lane holds column l32, and for
-  // register i the row 8*(i/4) + 4*h + (i%4). Rows rise with i, blocks rise with j,
-  // chunks rise with s0, so a strict '>' keeps the lowest s within the lane.
+  // Block epilogue: 32x32 accumulator layout -- lane holds column l32, and for register
+  // i the row 8*(i/4) + 4*h + (i%4) of the block. Rows rise with i, so a strict '>'
+  // keeps the lowest s within the lane; lanes l and l^32 are then merged.
+  // Per-lane bases; the block offsets below are compile-time constants, which keeps
+  // them in the LDS instructions' offset fields instead of in registers.
+  const float* mrow = &sm.maskf[wm * 32 + 4 * h];
+  float* pvw = &sm.pv[wm][wn * 64 + l32];
+  int* piw = &sm.pi[wm][wn * 64 + l32];
 #pragma unroll
   for (int j = 0; j < JM; ++j) {
-    const int rbase = (wm + WAVES_M * j) * 32 + 4 * h;
+    const int s_blk = sm.blk_s[wm + WAVES_M * j];
+    float bv[NB_PER_WAVE];
+    int bi[NB_PER_WAVE];
+#pragma unroll
+    for (int nb = 0; nb < NB_PER_WAVE; ++nb) {
+      bv[nb] = 0.0f;
+      bi[nb] = 0;
+    }
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      const f32x4 m4 = *(const f32x4*)(&sm.maskf[rbase + 8 * q]);
+      const f32x4 m4 = *(const f32x4*)(mrow + j * WAVES_M * 32 + 8 * q);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const int s = u.s0 + rbase + 8 * q + e;
+        const int s = s_blk + 8 * q + 4 * h + e;
 #pragma unroll
         for (int nb = 0; nb < NB_PER_WAVE; ++nb) {
           const float x = acc[j][nb][q * 4 + e] * m4[e];
-          if (x > best[nb]) { best[nb] = x; bidx[nb] = s; }
+          if (x > bv[nb]) {
+            bv[nb] = x;
+            bi[nb] = s;
+          }
         }
+      }
+    }
+#pragma unroll
+    for (int nb = 0; nb < NB_PER_WAVE; ++nb) {
+      // v_permlane32_swap exchanges the lane halves: element 1 of the result holds, in
+      // lanes 0..31, the values of lanes 32..63 (the only lanes that store below).
+      const float ov = __uint_as_float(
+          __builtin_amdgcn_permlane32_swap(__float_as_uint(bv[nb]), __float_as_uint(bv[nb]), false, false)[1]);
+      const int oi = (int)__builtin_amdgcn_permlane32_swap((unsigned)bi[nb], (unsigned)bi[nb], false, false)[1];
+      if (ov > bv[nb] || (ov == bv[nb] && oi < bi[nb])) {
+        bv[nb] = ov;
+        bi[nb] = oi;
+      }
+      if (h == 0) {
+        pvw[j * WAVES_M * BN + nb * 32] = bv[nb];
+        piw[j * WAVES_M * BN + nb * 32] = bi[nb];
       }
     }
   }
   return buf ^ (nk & 1);
 }
 
-// Merge the per-column winners of all waves and write reps / argmax for vocab tile v0.
+// Merge the blocks of each batch-row segment of the tile (thread = column) and write
+// reps/argmax for complete segments, or the partial for a segment that continues into
+// the previous M-tile (slot 0) or the next one (slot 1).
 template <typename T>
-__device__ __forceinline__ void write_tile(Smem& sm, int v0, int64_t orow, int V, int wm, int wn,
-                                           int lane, float* best, int* bidx, T* reps,
-                                           int32_t* argmax, float* reps_f32) {
-  const int tid = threadIdx.x, l32 = lane & 31, h = lane >> 5;
-  // Lanes l and l^32 hold the same column (different rows): merge them.
-#pragma unroll
-  for (int nb = 0; nb < NB_PER_WAVE; ++nb) {
-    const float ov = __shfl_xor(best[nb], 32);
-    const int oi = __shfl_xor(bidx[nb], 32);
-    merge(best[nb], bidx[nb], ov, oi);
-  }
-  if (h == 0) {
-#pragma unroll
-    for (int nb = 0; nb < NB_PER_WAVE; ++nb) {
-      const int col = wn * 64 + nb * 32 + l32;
-      sm.red_v[wm][col] = best[nb];
-      sm.red_i[wm][col] = bidx[nb];
-    }
-  }
-  lds_barrier();
-  if (tid < BN) {
+__device__ __forceinline__ void write_unit(Smem& sm, int m, int v0, int V, int n_valid, T* reps,
+                                           int32_t* argmax, float* reps_f32, float2* part) {
+  const int tid = threadIdx.x;
+  lds_barrier();  // every block's pv/pi are written
+  if (tid < BN && v0 + tid < V) {
     const int v = v0 + tid;
-    if (v < V) {
-      float bv = sm.red_v[0][tid];
-      int bi = sm.red_i[0][tid];
-#pragma unroll
-      for (int w = 1; w < WAVES_M; ++w) merge(bv, bi, sm.red_v[w][tid], sm.red_i[w][tid]);
-      const int64_t o = orow + v;
-      const float r = log1pf(bv);
-      reps[o] = from_f32<T>(r);
-      if (argmax != nullptr) argmax[o] = bi;
-      if (reps_f32 != nullptr) reps_f32[o] = r;
+    const int b_prev = sm.blk_b[MBLK], b_next = sm.blk_b[MBLK + 1];
+    float bv = 0.0f;
+    int bi = 0;
+    for (int r = 0; r < n_valid; ++r) {
+      const float pv = sm.pv[r][tid];
+      if (pv > bv) {  // earlier blocks hold lower s: strict '>' keeps them on ties
+        bv = pv;
+        bi = sm.pi[r][tid];
+      }
+      const int b = sm.blk_b[r];
+      if (r + 1 == n_valid || sm.blk_b[r + 1] != b) {  // the segment of batch row b ends
+        const bool cont_prev = b == sm.blk_b[0] && b == b_prev;
+        const bool cont_next = r + 1 == n_valid && b == b_next;
+        if (cont_prev || cont_next) {
+          part[((int64_t)m * 2 + (cont_prev ? 0 : 1)) * V + v] = make_float2(bv, __int_as_float(bi));
+        } else {
+          const int64_t o = (int64_t)b * V + v;
+          const float rv = log1pf(bv);
+          reps[o] = from_f32<T>(rv);
+          if (argmax != nullptr) argmax[o] = bi;
+          if (reps_f32 != nullptr) reps_f32[o] = rv;
+        }
+        bv = 0.0f;
+        bi = 0;
+      }
     }
   }
-  lds_barrier();  // red_v/red_i are reused by the next tile
+  lds_barrier();  // pv/pi are reused by the next unit
 }
 
 template <typename T>
 __global__ __launch_bounds__(NTHREADS, 1) void sparton_fwd_kernel(
     const T* __restrict__ H, const T* __restrict__ W, const T* __restrict__ bias,
     const void* __restrict__ mask, int mask_dtype, T* __restrict__ reps,
-    int32_t* __restrict__ argmax, float* __restrict__ reps_f32, int B, int S, int D, int V,
-    int n_vt, int P) {
+    int32_t* __restrict__ argmax, float* __restrict__ reps_f32, int S, int D, int V,
+    int n_vt, int P, int nblk, int n_mt_max, const int* __restrict__ meta,
+    const int* __restrict__ list, float2* __restrict__ part) {
   __shared__ Smem sm;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: keep it scalar
   const int wm = wave / WAVES_N, wn = wave % WAVES_N;
-  const int l32 = lane & 31;
 
   const int n_vg = (n_vt + P - 1) / P;
-  int b, vg;
-  tile_of(blockIdx.x, gridDim.x, B, n_vg, &b, &vg);
+  int m, vg;
+  tile_of(blockIdx.x, gridDim.x, n_mt_max, n_vg, &m, &vg);
+  const int n_blk = __builtin_amdgcn_readfirstlane(meta[0]);
+  if (m * MBLK >= n_blk) return;  // fewer active blocks than the launch allowed for
   const int vt_lo = vg * P, n_tiles = min(P, n_vt - vt_lo);
-  const int64_t mrow = (int64_t)b * S;
+  const int n_valid = min(MBLK, n_blk - m * MBLK);
 
-  Geo g;
-  g.row_bytes = D * (int)sizeof(T);
-  g.H = (const char*)(H + mrow * D);
-  g.W = (const char*)W;
-  const int slab_elems = SLAB / (int)sizeof(T);
-  g.nk_full = D / slab_elems;
-  g.S = S;
-  g.V = V;
-  // At least two slabs per unit (a padding slab contributes zero); none when D == 0,
-  // where x = bias * mask and nothing is loaded.
-  const int nk = D == 0 ? 0 : max(2, (int)cdiv(D, slab_elems));
-
-  // Slab 0 of the first unit is started before anything else, on the guess that the
-  // first unit is chunk 0 of the first vocab tile (reloaded below if it is not); all
-  // A rows are loaded, as the active blocks are not known yet.
-  Unit u0;
-  u0.v0 = vt_lo * BN;
-  u0.s0 = 0;
-  u0.last_blk = MBLK - 1;
-  if (nk > 0 && S > 0) issue_slab(sm, g, u0, 0, 0, wave, lane);
-
-  // Scan the mask row once: per 32-row block, whether any entry is nonzero.
-  const int n_chunks = (int)cdiv(S, BM);
-  if (tid < MAX_CHUNKS) sm.chunk_fl[tid] = 0;
-  lds_barrier();
-  for (int s_base = 0; s_base < n_chunks * BM; s_base += NTHREADS) {
-    const int s = s_base + tid;
-    const bool nz = s < S && load_mask(mask, mask_dtype, mrow + s) != 0.0f;
-    const uint64_t bal = __ballot(nz);
-    if (lane == 0 && bal != 0) {
-      const int blk0 = (s_base + wave * 64) / 32;  // two 32-row blocks per wave
-      const uint32_t bits = ((bal & 0xffffffffull) != 0 ? 1u : 0u) << (blk0 & 7) |
-                            ((bal >> 32) != 0 ? 1u : 0u) << ((blk0 + 1) & 7);
-      atomicOr((unsigned*)&sm.chunk_fl[0] + (blk0 / 8) / 4, bits << (8 * ((blk0 / 8) & 3)));
-    }
+  // The tile's blocks, and the batch rows of the blocks just before and after it.
+  if (tid < MBLK + 2) {
+    const int e = tid < MBLK ? m * MBLK + tid : (tid == MBLK ? m * MBLK - 1 : m * MBLK + MBLK);
+    const bool ok = e >= 0 && e < n_blk && (tid >= MBLK || tid < n_valid);
+    const int code = ok ? list[e] : -1;
+    sm.blk_b[tid] = ok ? code / nblk : -1;
+    if (tid < MBLK) sm.blk_s[tid] = ok ? (code % nblk) * 32 : 0;
   }
   for (int i = tid; i < n_tiles * BN; i += NTHREADS) {
     const int col = vt_lo * BN + i;
     sm.biasf[i] = (bias != nullptr && col < V) ? to_f32(bias[col]) : 0.0f;
   }
   lds_barrier();
-  if (tid == 0) {
-    int n = 0;
-    for (int c = 0; c < n_chunks; ++c)
-      if (sm.chunk_fl[c] != 0) sm.chunk_list[n++] = (uint8_t)c;
-    sm.n_active = n;
+
+  Geo g;
+  g.row_bytes = D * (int)sizeof(T);
+  g.H = (const char*)H;
+  g.W = (const char*)W;
+  const int slab_elems = SLAB / (int)sizeof(T);
+  g.nk_full = D / slab_elems;
+  g.V = V;
+  g.n_valid = n_valid;
+  // At least two slabs per unit (a padding slab contributes zero); none when D == 0,
+  // where x = bias * mask and nothing is loaded.
+  const int nk = D == 0 ? 0 : max(2, (int)cdiv(D, slab_elems));
+#pragma unroll
+  for (int i = 0; i < A_LOADS; ++i) {
+    const int grp = i * NWAVES + wave;
+    const int row = grp * ROWS_PER_LOAD + (lane >> 3);  // row of the tile
+    const int r = min(row >> 5, n_valid - 1);            // its block (loads past n_valid are skipped)
+    const int s = min(sm.blk_s[r] + (row & 31), S - 1);  // positions past S: any valid row
+    g.a_off[i] = (uint32_t)(((int64_t)sm.blk_b[r] * S + s) * g.row_bytes) + lane_chunk(row, lane);
   }
-  lds_barrier();
-  const int n_active = __builtin_amdgcn_readfirstlane(sm.n_active);
-
-  if (n_active == 0) {  // fully masked row: M = 0, I = 0 for every column
-    __builtin_amdgcn_s_waitcnt(0);  // no direct load may land after the workgroup ends
-    for (int t = 0; t < n_tiles; ++t) {
-      if (tid < BN) {
-        const int v = (vt_lo + t) * BN + tid;
-        if (v < V) {
-          const int64_t o = (int64_t)b * V + v;
-          reps[o] = from_f32<T>(0.0f);
-          if (argmax != nullptr) argmax[o] = 0;
-          if (reps_f32 != nullptr) reps_f32[o] = 0.0f;
-        }
-      }
-    }
-    return;
+  // Row mask of the tile (0 past S and past the last active block).
+  if (tid < BM) {
+    const int r = tid >> 5;
+    const int s = sm.blk_s[r] + (tid & 31);
+    sm.maskf[tid] = (r < n_valid && s < S) ? load_mask(mask, mask_dtype, (int64_t)sm.blk_b[r] * S + s) : 0.0f;
   }
 
-  // Unit descriptors are read from LDS: readfirstlane keeps them in SGPRs (they are
-  // workgroup-uniform), so the loads use the SGPR-base + VGPR-offset form.
-  auto unit_at = [&](int idx) {
-    Unit u;
-    const int t = idx / n_active;
-    const int c = __builtin_amdgcn_readfirstlane(sm.chunk_list[idx - t * n_active]);
-    const uint32_t fl = __builtin_amdgcn_readfirstlane(sm.chunk_fl[c]);
-    u.v0 = (vt_lo + t) * BN;
-    u.s0 = c * BM;
-    u.last_blk = 31 - __builtin_clz(fl);
-    return u;
-  };
-  const int n_units = n_tiles * n_active;
-
-  Unit u = unit_at(0);
+  const int jm = n_valid <= wm ? 0 : min(4, (n_valid - wm + 1) / WAVES_M);
   if (nk > 0) {
-    if (u.s0 != 0) {  // the guess was wrong: drain it and load the right rows
-      __builtin_amdgcn_s_waitcnt(0);
-      issue_slab(sm, g, u, 0, 0, wave, lane);
-    }
-    issue_slab(sm, g, u, 1, 1, wave, lane);
+    issue_slab(sm, g, vt_lo * BN, 0, 0, wave, lane);
+    issue_slab(sm, g, vt_lo * BN, 1, 1, wave, lane);
     // Slab 0 must have landed everywhere; slab 1 stays in flight.
-    const int a_groups = (u.last_blk + 1) * (32 / ROWS_PER_LOAD);
+    const int a_groups = n_valid * (32 / ROWS_PER_LOAD);
     int n1 = B_LOADS;
 #pragma unroll
     for (int i = 0; i < A_LOADS; ++i) n1 += (i * NWAVES + wave < a_groups) ? 1 : 0;
     wait_loads_at_most(n1);
   }
-  float best[NB_PER_WAVE];
-  int bidx[NB_PER_WAVE];
-#pragma unroll
-  for (int nb = 0; nb < NB_PER_WAVE; ++nb) {
-    best[nb] = 0.0f;
-    bidx[nb] = 0;
-  }
-  lds_barrier();
+  lds_barrier();  // also publishes maskf
 
   int buf = 0;
-  for (int idx = 0; idx < n_units; ++idx) {
-    Next nx;
-    nx.valid = idx + 1 < n_units;
-    nx.new_tile = nx.valid && ((idx + 1) % n_active == 0);
-    if (nx.valid) nx.u = unit_at(idx + 1);
-    // Blocks of this wave are wm, wm+2, ...: multiply those up to the last active
-    // one (masked rows below it give x = 0 and cannot win).
-    const int jm = u.last_blk < wm ? 0 : (u.last_blk - wm) / WAVES_M + 1;
+  for (int t = 0; t < n_tiles; ++t) {
+    const int v0 = (vt_lo + t) * BN;
+    const int v0_next = t + 1 < n_tiles ? v0 + BN : -1;
     switch (jm) {
-      case 0: buf = run_unit<T, 0>(sm, g, u, nx, nk, buf, wave, lane, wm, wn, mask, mask_dtype, mrow, S, idx / n_active, best, bidx); break;
-      case 1: buf = run_unit<T, 1>(sm, g, u, nx, nk, buf, wave, lane, wm, wn, mask, mask_dtype, mrow, S, idx / n_active, best, bidx); break;
-      case 2: buf = run_unit<T, 2>(sm, g, u, nx, nk, buf, wave, lane, wm, wn, mask, mask_dtype, mrow, S, idx / n_active, best, bidx); break;
-      case 3: buf = run_unit<T, 3>(sm, g, u, nx, nk, buf, wave, lane, wm, wn, mask, mask_dtype, mrow, S, idx / n_active, best, bidx); break;
-      default: buf = run_unit<T, 4>(sm, g, u, nx, nk, buf, wave, lane, wm, wn, mask, mask_dtype, mrow, S, idx / n_active, best, bidx); break;
+      case 0: buf = run_unit<T, 0>(sm, g, v0, v0_next, nk, buf, t, wave, lane, wm, wn); break;
+      case 1: buf = run_unit<T, 1>(sm, g, v0, v0_next, nk, buf, t, wave, lane, wm, wn); break;
+      case 2: buf = run_unit<T, 2>(sm, g, v0, v0_next, nk, buf, t, wave, lane, wm, wn); break;
+      case 3: buf = run_unit<T, 3>(sm, g, v0, v0_next, nk, buf, t, wave, lane, wm, wn); break;
+      default: buf = run_unit<T, 4>(sm, g, v0, v0_next, nk, buf, t, wave, lane, wm, wn); break;
     }
-    if (!nx.valid || nx.new_tile) {
-      write_tile<T>(sm, u.v0, (int64_t)b * V, V, wm, wn, lane, best, bidx, reps, argmax, reps_f32);
-#pragma unroll
-      for (int nb = 0; nb < NB_PER_WAVE; ++nb) {
-        best[nb] = 0.0f;
-        bidx[nb] = 0;
-      }
-    }
-    if (nx.valid) u = nx.u;
+    write_unit<T>(sm, m, v0, V, n_valid, reps, argmax, reps_f32, part);
   }
 }
 
+// ---- fixup ------------------------------------------------------------------------
+
+// Per batch row: no active block -> reps = 0, argmax = 0; blocks spread over several
+// M-tiles -> merge their partials in tile order (= s order).
 template <typename T>
-static int launch(const void* H, const void* W, const void* bias, const void* mask,
-                  int mask_dtype, void* reps, int32_t* argmax, float* reps_f32, int64_t B,
-                  int64_t S, int64_t D, int64_t V, int P, hipStream_t stream) {
-  const int64_t n_vt = cdiv(V, BN);
-  const int64_t grid = cdiv(n_vt, P) * B;
-  hipLaunchKernelGGL(sparton_fwd_kernel<T>, dim3((unsigned)grid), dim3(NTHREADS), 0, stream,
-                     (const T*)H, (const T*)W, (const T*)bias, mask, mask_dtype, (T*)reps,
-                     argmax, reps_f32, (int)B, (int)S, (int)D, (int)V, (int)n_vt, P);
-  const hipError_t e = hipGetLastError();
-  return e == hipSuccess ? SPARTON_OK : (int)e;
+__global__ __launch_bounds__(256) void fwd_fixup_kernel(int V, const int* __restrict__ count,
+                                                        const int* __restrict__ first,
+                                                        const float2* __restrict__ part,
+                                                        T* __restrict__ reps,
+                                                        int32_t* __restrict__ argmax,
+                                                        float* __restrict__ reps_f32) {
+  const int b = blockIdx.y;
+  const int v = blockIdx.x * 256 + threadIdx.x;
+  const int n = count[b];
+  int ms = 0, me = 0;
+  if (n > 0) {
+    ms = first[b] / MBLK;
+    me = (first[b] + n - 1) / MBLK;
+    if (ms == me) return;  // written by the main kernel
+  }
+  if (v >= V) return;
+  float bv = 0.0f;
+  int bi = 0;
+  if (n > 0) {
+    const float2 p0 = part[((int64_t)ms * 2 + 1) * V + v];
+    bv = p0.x;
+    bi = __float_as_int(p0.y);
+    for (int mm = ms + 1; mm <= me; ++mm) {
+      const float2 p = part[((int64_t)mm * 2 + 0) * V + v];
+      if (p.x > bv) {  // later tiles hold higher s: strict '>' keeps the lower on ties
+        bv = p.x;
+        bi = __float_as_int(p.y);
+      }
+    }
+  }
+  const int64_t o = (int64_t)b * V + v;
+  const float rv = log1pf(bv);
+  reps[o] = from_f32<T>(rv);
+  if (argmax != nullptr) argmax[o] = bi;
+  if (reps_f32 != nullptr) reps_f32[o] = rv;
 }
 
 // Vocab tiles per workgroup: enough workgroups to keep every CU busy for several
-// rounds (the dispatcher balances rows of different length), as few as that allows
-// (each workgroup pays its prologue once). SPARTON_FWD_TILES_PER_GROUP (1..16)
-// overrides the choice, for tests and tuning.
-static int tiles_per_group(int64_t B, int64_t n_vt) {
+// rounds, as few as that allows (each workgroup pays its prologue once).
+// SPARTON_FWD_TILES_PER_GROUP (1..8) overrides the choice, for tests and tuning.
+static int tiles_per_group(int64_t n_mt, int64_t n_vt) {
   if (const char* env = getenv("SPARTON_FWD_TILES_PER_GROUP")) {
     const int p = atoi(env);
     if (p >= 1 && p <= MAX_P) return p;
   }
   const int64_t target = 256 * 6;  // CUs x rounds
   int P = 1;
-  while (P < MAX_P && cdiv(n_vt, 2 * P) * B >= target) P *= 2;
+  while (P < MAX_P && cdiv(n_vt, 2 * P) * n_mt >= target) P *= 2;
   return P;
+}
+
+template <typename T>
+static int launch(const void* H, const void* W, const void* bias, const void* mask,
+                  int mask_dtype, void* reps, int32_t* argmax, float* reps_f32, int64_t B,
+                  int64_t S, int64_t D, int64_t V, const Work& w, hipStream_t stream) {
+  const int64_t nblk = cdiv(S, 32);
+  const int64_t n_vt = cdiv(V, BN);
+  const int64_t n_mt_max = cdiv(B * nblk, MBLK);
+  // The workgroup count is sized for rows about 60% full (the launch does not know the
+  // mask); it affects speed only.
+  const int P = tiles_per_group(cdiv(n_mt_max * 3, 5), n_vt);
+  const int64_t grid = n_mt_max * cdiv(n_vt, P);
+  if (grid > INT32_MAX) return SPARTON_EUNSUPPORTED;
+  hipLaunchKernelGGL(fwd_plan_rows_kernel, dim3((unsigned)cdiv(B, 4)), dim3(256), 0, stream, mask,
+                     mask_dtype, (int)B, (int)S, (int)nblk, w.flag, w.count);
+  hipLaunchKernelGGL(fwd_plan_list_kernel, dim3(1), dim3(PLAN_THREADS), 0, stream, (int)B,
+                     (int)nblk, (const uint8_t*)w.flag, (const int*)w.count, w.first, w.list,
+                     w.meta);
+  if (grid > 0)  // S == 0: no blocks, the fixup writes every row
+    hipLaunchKernelGGL(sparton_fwd_kernel<T>, dim3((unsigned)grid), dim3(NTHREADS), 0, stream,
+                       (const T*)H, (const T*)W, (const T*)bias, mask, mask_dtype, (T*)reps,
+                       argmax, reps_f32, (int)S, (int)D, (int)V, (int)n_vt, P, (int)nblk,
+                       (int)n_mt_max, (const int*)w.meta, (const int*)w.list, w.part);
+  hipLaunchKernelGGL(fwd_fixup_kernel<T>, dim3((unsigned)cdiv(V, 256), (unsigned)B), dim3(256), 0,
+                     stream, (int)V, (const int*)w.count, (const int*)w.first,
+                     (const float2*)w.part, (T*)reps, argmax, reps_f32);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? SPARTON_OK : (int)e;
+}
+
+// Batch rows per launch: byte offsets into H inside a launch stay below 2^31.
+static int64_t rows_per_launch(int64_t B, int64_t S, int64_t D, int64_t esz) {
+  const int64_t per_row = std::max<int64_t>(1, S * D * esz);
+  return std::max<int64_t>(1, std::min<int64_t>(B, ((int64_t)1 << 31) / per_row));
+}
+
+static int64_t mask_elem_bytes(int mask_dtype) {
+  switch (mask_dtype) {
+    case SPARTON_MASK_I64: return 8;
+    case SPARTON_MASK_I32:
+    case SPARTON_MASK_F32: return 4;
+    case SPARTON_MASK_U8: return 1;
+    default: return 2;
+  }
 }
 
 }  // namespace fwd
@@ -568,10 +681,17 @@ static int tiles_per_group(int64_t B, int64_t n_vt) {
 
 using namespace sparton;
 
+extern "C" __attribute__((visibility("default"))) size_t sparton_fwd_workspace_bytes(
+    int64_t B, int64_t S, int64_t D, int64_t V, int dtype) {
+  if (B <= 0 || S < 0 || D < 0 || V <= 0) return 0;
+  const int64_t esz = dtype == SPARTON_F32 ? 4 : 2;
+  return fwd::carve(nullptr, fwd::rows_per_launch(B, S, D, esz), S, V).total;
+}
+
 extern "C" __attribute__((visibility("default"))) int sparton_fwd(
     const void* hidden, const void* weight, const void* bias, const void* mask,
     int mask_dtype, void* reps, int32_t* argmax, float* reps_f32, int64_t B, int64_t S,
-    int64_t D, int64_t V, int dtype, void* stream) {
+    int64_t D, int64_t V, int dtype, void* workspace, size_t workspace_bytes, void* stream) {
   if (B < 0 || S < 0 || D < 0 || V < 0) return SPARTON_EINVAL;
   if (dtype < SPARTON_F32 || dtype > SPARTON_F16) return SPARTON_EINVAL;
   if (mask_dtype < SPARTON_MASK_I64 || mask_dtype > SPARTON_MASK_F16) return SPARTON_EINVAL;
@@ -584,19 +704,35 @@ extern "C" __attribute__((visibility("default"))) int sparton_fwd(
   const int64_t esz = dtype == SPARTON_F32 ? 4 : 2;
   if ((D * esz) % 16 != 0) return SPARTON_EINVAL;
   if (((uintptr_t)hidden | (uintptr_t)weight) % 16 != 0) return SPARTON_EALIGN;
-  // 32-bit sizes inside the kernel; per-tile byte offsets (256 rows) in 32 bits.
-  if (B > INT32_MAX || S > INT32_MAX || V > INT32_MAX) return SPARTON_EUNSUPPORTED;
-  if (S > fwd::MAX_CHUNKS * fwd::BM) return SPARTON_EUNSUPPORTED;
-  if (D * esz * fwd::BM >= ((int64_t)1 << 32)) return SPARTON_EUNSUPPORTED;
-  if (cdiv(V, fwd::BN) * B > INT32_MAX) return SPARTON_EUNSUPPORTED;
+  if (S > fwd::MAX_S || B > INT32_MAX || V > INT32_MAX) return SPARTON_EUNSUPPORTED;
+  if (S * D * esz >= ((int64_t)1 << 31) || (int64_t)fwd::BN * D * esz >= ((int64_t)1 << 31))
+    return SPARTON_EUNSUPPORTED;
+  const size_t need = sparton_fwd_workspace_bytes(B, S, D, V, dtype);
+  if (workspace == nullptr || workspace_bytes < need) return SPARTON_EWORKSPACE;
+  if ((uintptr_t)workspace % 256 != 0) return SPARTON_EALIGN;
   hipStream_t st = (hipStream_t)stream;
-  const int P = fwd::tiles_per_group(B, cdiv(V, fwd::BN));
-  switch (dtype) {
-    case SPARTON_BF16:
-      return fwd::launch<bf16>(hidden, weight, bias, mask, mask_dtype, reps, argmax, reps_f32, B, S, D, V, P, st);
-    case SPARTON_F16:
-      return fwd::launch<f16>(hidden, weight, bias, mask, mask_dtype, reps, argmax, reps_f32, B, S, D, V, P, st);
-    default:
-      return fwd::launch<float>(hidden, weight, bias, mask, mask_dtype, reps, argmax, reps_f32, B, S, D, V, P, st);
+  const int64_t Bc = fwd::rows_per_launch(B, S, D, esz);
+  for (int64_t b0 = 0; b0 < B; b0 += Bc) {
+    const int64_t nb = std::min(Bc, B - b0);
+    const fwd::Work w = fwd::carve(workspace, nb, S, V);
+    const char* h = (const char*)hidden + b0 * S * D * esz;
+    const char* mk = mask == nullptr ? nullptr : (const char*)mask + b0 * S * fwd::mask_elem_bytes(mask_dtype);
+    char* r = (char*)reps + b0 * V * esz;
+    int32_t* am = argmax == nullptr ? nullptr : argmax + b0 * V;
+    float* r32 = reps_f32 == nullptr ? nullptr : reps_f32 + b0 * V;
+    int rc;
+    switch (dtype) {
+      case SPARTON_BF16:
+        rc = fwd::launch<bf16>(h, weight, bias, mk, mask_dtype, r, am, r32, nb, S, D, V, w, st);
+        break;
+      case SPARTON_F16:
+        rc = fwd::launch<f16>(h, weight, bias, mk, mask_dtype, r, am, r32, nb, S, D, V, w, st);
+        break;
+      default:
+        rc = fwd::launch<float>(h, weight, bias, mk, mask_dtype, r, am, r32, nb, S, D, V, w, st);
+        break;
+    }
+    if (rc != SPARTON_OK) return rc;
   }
+  return SPARTON_OK;
 }

@@ -85,10 +85,13 @@ def _fwd_impl(hidden: Tensor, embed: Tensor, bias: Optional[Tensor], mask: Tenso
     idx = torch.empty((B, V), dtype=torch.int32, device=dev) if with_idx else None
     reps32 = torch.empty((B, V), dtype=torch.float32, device=dev) if with_f32 else None
     L = _lib.load()
+    dt = _lib.DTYPE_CODE[hidden.dtype]
+    ws_bytes = int(L.sparton_fwd_workspace_bytes(B, S, D, V, dt))
+    ws = torch.empty((max(ws_bytes, 1),), dtype=torch.uint8, device=dev)
     with torch.cuda.device(dev):
         rc = L.sparton_fwd(hidden.data_ptr(), embed.data_ptr(), _lib.ptr(bias), mask.data_ptr(),
                            _lib.MASK_CODE[mask.dtype], reps.data_ptr(), _lib.ptr(idx),
-                           _lib.ptr(reps32), B, S, D, V, _lib.DTYPE_CODE[hidden.dtype],
+                           _lib.ptr(reps32), B, S, D, V, dt, ws.data_ptr(), ws_bytes,
                            _stream(dev))
     _lib.check(rc, op)
     return reps, idx, reps32

@@ -45,6 +45,10 @@ def test_host_side_entry_points():
     ws = L.sparton_bwd_workspace_bytes(32, 256, 768, 30522)
     assert ws % 256 == 0 and ws >= 32 * 30522 * 8 + 2 * 32 * 256 * 4
     assert L.sparton_bwd_workspace_bytes(0, 256, 768, 30522) == 0
+    fws = L.sparton_fwd_workspace_bytes(32, 256, 768, 30522, 1)
+    # plan (flags, counts, block list) + two partial rows of V (max, argmax) per row tile
+    assert fws % 256 == 0 and fws >= 32 * 2 * 30522 * 8
+    assert L.sparton_fwd_workspace_bytes(0, 256, 768, 30522, 1) == 0
 
 
 # Argument checks that return before any HIP call (fake, never-dereferenced pointers).
@@ -53,7 +57,7 @@ P = 0x10000  # 16-byte aligned dummy address
 
 def fwd(**kw):
     a = dict(hidden=P, weight=P, bias=None, mask=P, mask_dtype=0, reps=P, argmax=P, reps32=None,
-             B=2, S=4, D=64, V=10, dtype=1, stream=None)
+             B=2, S=4, D=64, V=10, dtype=1, ws=P, ws_bytes=1 << 30, stream=None)
     a.update(kw)
     return _lib.load().sparton_fwd(*a.values())
 
@@ -69,7 +73,8 @@ def bwd(**kw):
 @pytest.mark.parametrize("kw,code", [
     (dict(B=-1), -1), (dict(dtype=3), -1), (dict(mask_dtype=6), -1), (dict(hidden=None), -1),
     (dict(D=60), -1), (dict(D=4, dtype=1), -1), (dict(hidden=P + 8), -2), (dict(weight=P + 4), -2),
-    (dict(B=0), 0), (dict(V=0), 0),
+    (dict(B=0), 0), (dict(V=0), 0), (dict(ws=None), -4), (dict(ws_bytes=16), -4),
+    (dict(ws=P + 16), -2), (dict(S=20000), -3),
 ])
 def test_fwd_argument_validation(kw, code):
     assert fwd(**kw) == code

@@ -76,6 +76,7 @@ CASES = [
     ("fp32", 2, 20, 40, 260, False, "holes"),   # K tail: 160-byte rows
     ("fp16", 3, 130, 24, 520, True, "int64"),   # rows shorter than one slab, 3 vocab tiles
     ("bf16", 3, 900, 64, 2100, True, "gaps"),   # fully masked middle chunk, masked row
+    ("bf16", 37, 40, 64, 700, True, "int64"),   # many short rows: several rows per row tile
 ]
 
 # Cases run again with several vocab tiles per workgroup (the unit stream then crosses
@@ -84,7 +85,8 @@ MULTI_TILE_CASES = [
     (("bf16", 3, 900, 64, 2100, True, "gaps"), 3),
     (("fp32", 2, 40, 96, 1300, True, "frac"), 2),
     (("fp16", 2, 300, 24, 1800, False, "bool"), 4),
-    (("bf16", 2, 256, 768, 4099, True, "holes"), 16),
+    (("bf16", 2, 256, 768, 4099, True, "holes"), 8),
+    (("fp16", 37, 40, 64, 700, True, "int64"), 3),
 ]
 
 
