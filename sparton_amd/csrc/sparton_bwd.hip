@@ -8,13 +8,18 @@
 //
 //   dW / dbias  (bwd_dw_kernel)   row v gathers H[b, I[b,v], :] for b ascending.
 //   dH          (count -> scan -> scatter -> bwd_dh_kernel)
-//       1. count:   per (b, wave chunk of CHW vocab ids), active entries per s.
-//       2. scan:    per b, exclusive scan in (s, chunk) order -> each (b,s) segment
-//                   start and each chunk's first slot inside every segment.
+//       1. count:   per (b, wave chunk of CHW vocab ids), active entries per s,
+//                   stored as hist[b][s][chunk].
+//       2. scan:    per b, one exclusive scan of hist[b] in (s, chunk) order -> each
+//                   (b,s) segment start and each chunk's first slot inside it.
 //       3. scatter: per (b, chunk), write (v, g') to its slot. Entries are visited in
 //                   v order and ranked among equal s with ballots, so each segment
 //                   lists its vocab ids in ascending order (a stable counting sort).
-//       4. dh:      one wave per (b,s) row sums g' * W[v,:] over its segment.
+//       4. dh:      one wave per (b,s) row sums g' * W[v,:] over its segment,
+//                   gathering several W rows per batch before accumulating.
+//   dW / dbias for B <= 128 (bwd_dw_staged_kernel): a workgroup stages g' and I of all
+//   batch rows for 64 consecutive vocab ids in LDS (coalesced loads), then each wave
+//   gathers the H rows of one id at a time.
 // The only atomics are integer counts in LDS, which are order-independent.
 //
 // Gradients are written as fp32 (what the reference returns) or in the input dtype
@@ -36,7 +41,7 @@ constexpr int MAX_NP = 16;         // D up to 16 * 256 per register pass
 
 struct Layout {
   int64_t nch;
-  size_t hist, seg_start, seg_cnt, list, total;
+  size_t hist, seg_start, seg_cnt, list, total;  // hist: [B][S][nch] int32
 };
 
 static Layout layout(int64_t B, int64_t S, int64_t V) {
@@ -127,61 +132,62 @@ __global__ __launch_bounds__(256) void bwd_count_kernel(
   }
   __syncthreads();
   if (c < nch) {
-    int* out = hist + ((int64_t)b * nch + c) * S;
-    for (int s = lane; s < S; s += 64) out[s] = h[s];
+    int* out = hist + (int64_t)b * S * nch + c;
+    for (int s = lane; s < S; s += 64) out[(int64_t)s * nch] = h[s];
   }
-}
-
-// Exclusive scan of one int per thread over a 256-thread block.
-__device__ __forceinline__ int block_excl_scan(int x, int* tmp4) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  int v = x;
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const int y = __shfl_up(v, off);
-    if (lane >= off) v += y;
-  }
-  if (lane == 63) tmp4[wave] = v;
-  __syncthreads();
-  int base = 0;
-  for (int w = 0; w < wave; ++w) base += tmp4[w];
-  __syncthreads();
-  return base + v - x;
 }
 
 // ---- 2. scan -----------------------------------------------------------------
-__global__ __launch_bounds__(256) void bwd_scan_kernel(int* __restrict__ hist, int* __restrict__ seg_start,
-                                                       int* __restrict__ seg_cnt, int S, int nch) {
-  int* tot = (int*)sparton_bwd_smem;  // [S]
-  __shared__ int tmp4[4];
-  const int b = blockIdx.x, tid = threadIdx.x;
-  int* hb = hist + (int64_t)b * nch * S;
-  for (int s = tid; s < S; s += 256) {
-    int t = 0;
-    for (int c = 0; c < nch; ++c) t += hb[(int64_t)c * S + s];
-    tot[s] = t;
-  }
+constexpr int SCAN_THREADS = 1024;
+constexpr int SCAN_ITEMS = 4;  // consecutive elements per thread per tile
+
+// One workgroup per batch row: exclusive scan of hist[b] (S * nch ints, (s, chunk)
+// order) in place, in tiles of SCAN_THREADS * SCAN_ITEMS; then the segment of each s.
+__global__ __launch_bounds__(SCAN_THREADS) void bwd_scan_kernel(int* __restrict__ hist,
+                                                                int* __restrict__ seg_start,
+                                                                int* __restrict__ seg_cnt, int S,
+                                                                int nch) {
+  __shared__ int wsum[SCAN_THREADS / 64];
+  __shared__ int carry;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t b = blockIdx.x;
+  const int64_t n = (int64_t)S * nch;
+  int* hb = hist + b * n;
+  if (tid == 0) carry = 0;
   __syncthreads();
-  const int per = (S + 255) / 256, beg = min(S, tid * per), end = min(S, beg + per);
-  int local = 0;
-  for (int s = beg; s < end; ++s) local += tot[s];
-  int run = block_excl_scan(local, tmp4);
-  for (int s = beg; s < end; ++s) {
-    const int t = tot[s];
-    tot[s] = run;
-    seg_start[(int64_t)b * S + s] = run;
-    seg_cnt[(int64_t)b * S + s] = t;
-    run += t;
-  }
-  __syncthreads();
-  for (int s = tid; s < S; s += 256) {
-    int r = tot[s];
-    for (int c = 0; c < nch; ++c) {
-      int* p = hb + (int64_t)c * S + s;
-      const int cnt = *p;
-      *p = r;
-      r += cnt;
+  for (int64_t t0 = 0; t0 < n; t0 += SCAN_THREADS * SCAN_ITEMS) {
+    const int64_t e0 = t0 + (int64_t)tid * SCAN_ITEMS;
+    int x[SCAN_ITEMS], sum = 0;
+#pragma unroll
+    for (int i = 0; i < SCAN_ITEMS; ++i) {
+      x[i] = e0 + i < n ? hb[e0 + i] : 0;
+      sum += x[i];
     }
+    int incl = sum;  // inclusive scan of the per-thread sums: wave, then across waves
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const int y = __shfl_up(incl, d);
+      if (lane >= d) incl += y;
+    }
+    if (lane == 63) wsum[wave] = incl;
+    __syncthreads();
+    int run = carry + incl - sum;
+    for (int w = 0; w < wave; ++w) run += wsum[w];
+#pragma unroll
+    for (int i = 0; i < SCAN_ITEMS; ++i) {
+      if (e0 + i < n) hb[e0 + i] = run;
+      run += x[i];
+    }
+    __syncthreads();
+    if (tid == SCAN_THREADS - 1) carry = run;
+    __syncthreads();
+  }
+  const int total = carry;
+  for (int s = tid; s < S; s += SCAN_THREADS) {
+    const int st = hb[(int64_t)s * nch];
+    const int en = s + 1 < S ? hb[(int64_t)(s + 1) * nch] : total;
+    seg_start[b * S + s] = st;
+    seg_cnt[b * S + s] = en - st;
   }
 }
 
@@ -197,8 +203,8 @@ __global__ __launch_bounds__(256) void bwd_scatter_kernel(
   const int b = blockIdx.y, c = blockIdx.x * wpb + wave;
   stage_mask(maskf, mask, mdt, b, S);
   if (c < nch) {
-    const int* in = hist_base + ((int64_t)b * nch + c) * S;
-    for (int s = lane; s < S; s += 64) cur[s] = in[s];
+    const int* in = hist_base + (int64_t)b * S * nch + c;
+    for (int s = lane; s < S; s += 64) cur[s] = in[(int64_t)s * nch];
   }
   __syncthreads();
   if (c >= nch) return;
@@ -235,18 +241,47 @@ __device__ __forceinline__ void store4(f16* p, const f32x4& a) {
   *(f16x4*)p = f16x4{(f16)a[0], (f16)a[1], (f16)a[2], (f16)a[3]};
 }
 
+// Four consecutive elements of a row, loaded raw (8 bytes for 16-bit types, 16 for
+// fp32) so that a batch of loads is issued before any conversion.
+template <typename T> struct Raw4;
+template <> struct Raw4<float> {
+  f32x4 v;
+  __device__ __forceinline__ void load(const float* p) { v = *(const f32x4*)p; }
+  __device__ __forceinline__ void zero() { v = f32x4{0.f, 0.f, 0.f, 0.f}; }
+  __device__ __forceinline__ f32x4 f() const { return v; }
+};
+template <> struct Raw4<bf16> {
+  bf16x4 v;
+  __device__ __forceinline__ void load(const bf16* p) { v = *(const bf16x4*)p; }
+  __device__ __forceinline__ void zero() { v = bf16x4{(bf16)0.f, (bf16)0.f, (bf16)0.f, (bf16)0.f}; }
+  __device__ __forceinline__ f32x4 f() const { return f32x4{(float)v[0], (float)v[1], (float)v[2], (float)v[3]}; }
+};
+template <> struct Raw4<f16> {
+  f16x4 v;
+  __device__ __forceinline__ void load(const f16* p) { v = *(const f16x4*)p; }
+  __device__ __forceinline__ void zero() { v = f16x4{(f16)0.f, (f16)0.f, (f16)0.f, (f16)0.f}; }
+  __device__ __forceinline__ f32x4 f() const { return f32x4{(float)v[0], (float)v[1], (float)v[2], (float)v[3]}; }
+};
+
+// Rows gathered per batch: all their loads are in flight together (about 24 per lane).
+template <int NP> struct Batch { static constexpr int U = NP <= 3 ? 8 : NP <= 6 ? 4 : NP <= 8 ? 3 : 2; };
+
 // ---- 4. dH ---------------------------------------------------------------------
-// One wave per (b,s) row; lane l owns elements d0 + p*256 + 4l .. +3 for p < NP. The NP
-// loads of two W rows are issued together before they are accumulated.
+// One wave per (b,s) row; lane l owns elements d0 + p*256 + 4l .. +3 for p < NP. The
+// segment's entries sit one per lane; they are taken U at a time (a uniform loop, so
+// the summation order is the segment's v order), all U*NP loads are issued, then the
+// U rows are accumulated.
 template <typename T, typename O, int NP>
 __global__ __launch_bounds__(256) void bwd_dh_kernel(
     const T* __restrict__ W, const int2* __restrict__ list, const int* __restrict__ seg_start,
     const int* __restrict__ seg_cnt, O* __restrict__ dH, int B, int S, int D, int V) {
+  constexpr int U = Batch<NP>::U;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * 4 + wave;
   if (row >= (int64_t)B * S) return;
   const int64_t b = row / S;
-  const int start = seg_start[row], cnt = seg_cnt[row];
+  const int start = __builtin_amdgcn_readfirstlane(seg_start[row]);
+  const int cnt = __builtin_amdgcn_readfirstlane(seg_cnt[row]);
   const int2* seg = list + b * V + start;
   for (int d0 = 0; d0 < D; d0 += NP * 256) {
     f32x4 acc[NP];
@@ -255,30 +290,27 @@ __global__ __launch_bounds__(256) void bwd_dh_kernel(
     for (int e0 = 0; e0 < cnt; e0 += 64) {
       const int2 ent = e0 + lane < cnt ? seg[e0 + lane] : make_int2(0, 0);
       const int n = min(64, cnt - e0);
-      int j = 0;
-      for (; j + 1 < n; j += 2) {
-        const int v0 = __builtin_amdgcn_readlane(ent.x, j);
-        const int v1 = __builtin_amdgcn_readlane(ent.x, j + 1);
-        const float g0 = __int_as_float(__builtin_amdgcn_readlane(ent.y, j));
-        const float g1 = __int_as_float(__builtin_amdgcn_readlane(ent.y, j + 1));
-        f32x4 w0[NP], w1[NP];
+      for (int j = 0; j < n; j += U) {
+        Raw4<T> w[U][NP];
+        float g[U];
 #pragma unroll
-        for (int p = 0; p < NP; ++p) {
-          const int d = d0 + p * 256 + lane * 4;
-          w0[p] = d < D ? load4(W + (int64_t)v0 * D + d) : f32x4{0.f, 0.f, 0.f, 0.f};
-          w1[p] = d < D ? load4(W + (int64_t)v1 * D + d) : f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int u = 0; u < U; ++u) {
+          // past the segment end: reload the last entry's row (a cache hit) with g' = 0,
+          // which keeps the batch free of branches so all its loads issue together
+          const int jj = min(j + u, n - 1);
+          const int v = __builtin_amdgcn_readlane(ent.x, jj);
+          g[u] = j + u < n ? __int_as_float(__builtin_amdgcn_readlane(ent.y, jj)) : 0.0f;
+#pragma unroll
+          for (int p = 0; p < NP; ++p) {
+            const int d = d0 + p * 256 + lane * 4;
+            if (d < D) w[u][p].load(W + (int64_t)v * D + d);
+            else w[u][p].zero();
+          }
         }
 #pragma unroll
-        for (int p = 0; p < NP; ++p) acc[p] += g0 * w0[p] + g1 * w1[p];
-      }
-      if (j < n) {
-        const int v0 = __builtin_amdgcn_readlane(ent.x, j);
-        const float g0 = __int_as_float(__builtin_amdgcn_readlane(ent.y, j));
+        for (int u = 0; u < U; ++u)
 #pragma unroll
-        for (int p = 0; p < NP; ++p) {
-          const int d = d0 + p * 256 + lane * 4;
-          if (d < D) acc[p] += g0 * load4(W + (int64_t)v0 * D + d);
-        }
+          for (int p = 0; p < NP; ++p) acc[p] += g[u] * w[u][p].f();
       }
     }
     O* out = dH + row * D;
@@ -373,6 +405,107 @@ __global__ __launch_bounds__(256) void bwd_dw_kernel(
   }
 }
 
+// ---- 5b. dW and dbias, staged (B <= DW_STAGE_B) ---------------------------------
+constexpr int DW_STAGE_B = 128;
+
+// A workgroup of 16 waves owns 64 consecutive vocab ids. It loads G, reps and I of all
+// batch rows for them (each load instruction reads 64 consecutive elements of one row)
+// and keeps g' (0 = inactive) and I in LDS; then wave w handles ids 4w .. 4w+3, one at
+// a time: lanes scan the batch rows, a ballot lists the active ones, and their H rows
+// are gathered up to U at a time in ascending b and accumulated.
+constexpr int DW_WAVES = 16;
+template <typename T, typename O, int NP>
+__global__ __launch_bounds__(64 * DW_WAVES) void bwd_dw_staged_kernel(
+    const T* __restrict__ grad, const void* __restrict__ reps, int rdt,
+    const int32_t* __restrict__ idx, const void* __restrict__ mask, int mdt,
+    const T* __restrict__ H, O* __restrict__ dW, O* __restrict__ dbias, int B, int S, int D,
+    int V) {
+  constexpr int U = Batch<NP>::U;
+  constexpr int LD = DW_STAGE_B + 1;  // odd row stride: conflict-free column and row access
+  __shared__ float gl[64 * LD];
+  __shared__ uint16_t sl[64 * LD];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int v0 = blockIdx.x * 64;
+  for (int b = wave; b < B; b += DW_WAVES) {
+    const int v = v0 + lane;
+    float g = 0.0f;
+    int s = 0;
+    if (v < V) {
+      const int64_t o = (int64_t)b * V + v;
+      const float r = load_float(reps, rdt, o);
+      s = idx[o];
+      if (r > 0.0f && s >= 0 && s < S) {
+        const float gr = to_f32(grad[o]);
+        if (gr != 0.0f) {
+          const float m = load_mask(mask, mdt, (int64_t)b * S + s);
+          if (m != 0.0f) g = gr * expf(-r) * m;
+        }
+      } else {
+        s = 0;
+      }
+    }
+    gl[lane * LD + b] = g;
+    sl[lane * LD + b] = (uint16_t)s;
+  }
+  __syncthreads();
+  const int dend = max(D, 1);  // one pass even when D == 0, for dbias
+  for (int i = 0; i < 64 / DW_WAVES; ++i) {
+    const int vl = wave * (64 / DW_WAVES) + i, v = v0 + vl;
+    if (v >= V) break;
+    for (int d0 = 0; d0 < dend; d0 += NP * 256) {
+      f32x4 acc[NP];
+#pragma unroll
+      for (int p = 0; p < NP; ++p) acc[p] = f32x4{0.f, 0.f, 0.f, 0.f};
+      float bsum = 0.0f;
+      for (int b0 = 0; b0 < B; b0 += 64) {
+        const int bb = b0 + lane;
+        const float g = bb < B ? gl[vl * LD + bb] : 0.0f;
+        const int s = bb < B ? (int)sl[vl * LD + bb] : 0;
+        uint64_t pending = __ballot(g != 0.0f);
+        while (pending) {
+          const int nb = min(U, __popcll(pending));  // rows in this batch (uniform)
+          Raw4<T> x[U][NP];
+          float gu[U];
+#pragma unroll
+          for (int u = 0; u < U; ++u) {
+            gu[u] = 0.0f;
+            if (u < nb) {
+              const int l = __ffsll((unsigned long long)pending) - 1;
+              pending &= pending - 1;
+              gu[u] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(g), l));
+              const int su = __builtin_amdgcn_readlane(s, l);
+              const T* hr = H + ((int64_t)(b0 + l) * S + su) * D;
+#pragma unroll
+              for (int p = 0; p < NP; ++p) {
+                const int d = d0 + p * 256 + lane * 4;
+                if (d < D) x[u][p].load(hr + d);
+                else x[u][p].zero();
+              }
+            }
+          }
+#pragma unroll
+          for (int u = 0; u < U; ++u) {
+            if (u < nb) {
+              bsum += gu[u];
+#pragma unroll
+              for (int p = 0; p < NP; ++p) acc[p] += gu[u] * x[u][p].f();
+            }
+          }
+        }
+      }
+      if (d0 == 0 && dbias != nullptr && lane == 0) dbias[v] = from_f32<O>(bsum);
+      if (dW != nullptr) {
+        O* out = dW + (int64_t)v * D;
+#pragma unroll
+        for (int p = 0; p < NP; ++p) {
+          const int d = d0 + p * 256 + lane * 4;
+          if (d < D) store4(out + d, acc[p]);
+        }
+      }
+    }
+  }
+}
+
 // Register passes for a row of D elements (4 per lane, 256 per pass), capped at MAX_NP
 // (longer rows loop over D in chunks of MAX_NP * 256).
 static int passes_for(int64_t D) {
@@ -395,7 +528,7 @@ static void launch_rows(const T* g, const void* r, int rdt, const int32_t* idx, 
     if (L.nch > 0)
       hipLaunchKernelGGL(bwd_count_kernel<T>, cgrid, dim3(64 * wpb), cl, st, g, r, rdt, idx,
                          mask, mdt, (int)S, (int)V, (int)L.nch, hist);
-    hipLaunchKernelGGL(bwd_scan_kernel, dim3((unsigned)B), dim3(256), (size_t)S * 4, st, hist,
+    hipLaunchKernelGGL(bwd_scan_kernel, dim3((unsigned)B), dim3(SCAN_THREADS), 0, st, hist,
                        seg_start, seg_cnt, (int)S, (int)L.nch);
     if (L.nch > 0)
       hipLaunchKernelGGL(bwd_scatter_kernel<T>, cgrid, dim3(64 * wpb), cl, st, g, r, rdt, idx,
@@ -404,9 +537,14 @@ static void launch_rows(const T* g, const void* r, int rdt, const int32_t* idx, 
                        st, W, (const int2*)list, (const int*)seg_start, (const int*)seg_cnt, dH,
                        (int)B, (int)S, (int)D, (int)V);
   }
-  if ((dW != nullptr || dbias != nullptr) && V > 0)
-    hipLaunchKernelGGL((bwd_dw_kernel<T, O, NP>), dim3((unsigned)cdiv(V, 4)), dim3(256), 0, st,
-                       g, r, rdt, idx, mask, mdt, H, dW, dbias, (int)B, (int)S, (int)D, (int)V);
+  if ((dW != nullptr || dbias != nullptr) && V > 0) {
+    if (B <= DW_STAGE_B)
+      hipLaunchKernelGGL((bwd_dw_staged_kernel<T, O, NP>), dim3((unsigned)cdiv(V, 64)), dim3(64 * DW_WAVES), 0,
+                         st, g, r, rdt, idx, mask, mdt, H, dW, dbias, (int)B, (int)S, (int)D, (int)V);
+    else
+      hipLaunchKernelGGL((bwd_dw_kernel<T, O, NP>), dim3((unsigned)cdiv(V, 4)), dim3(256), 0, st,
+                         g, r, rdt, idx, mask, mdt, H, dW, dbias, (int)B, (int)S, (int)D, (int)V);
+  }
 }
 
 template <typename T, typename O>

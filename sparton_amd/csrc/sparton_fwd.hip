@@ -63,7 +63,6 @@ constexpr int CHUNKS = SLAB / 16;    // 16-byte chunks per row slab (8)
 constexpr int ROWS_PER_LOAD = 64 / CHUNKS;          // rows one wave-wide load covers (8)
 constexpr int A_LOADS = BM / ROWS_PER_LOAD / NWAVES;  // wave-wide loads per slab for A (4)
 constexpr int B_LOADS = BN / ROWS_PER_LOAD / NWAVES;  // and for B (4)
-constexpr int GROUP_V = 4;           // vocab-tile groups per scheduling group (L2 reuse)
 constexpr int MAX_P = 8;             // vocab tiles per workgroup
 constexpr int MAX_S = 16384;         // positions per batch row (512 blocks)
 constexpr int PLAN_THREADS = 1024;
@@ -105,33 +104,47 @@ static Work carve(void* base, int64_t B, int64_t S, int64_t V) {
 
 // ---- plan -------------------------------------------------------------------------
 
-// One wave per batch row: which 32-row blocks have a nonzero mask entry.
-__global__ __launch_bounds__(256) void fwd_plan_rows_kernel(const void* __restrict__ mask,
-                                                            int mask_dtype, int B, int S, int nblk,
-                                                            uint8_t* __restrict__ flag,
-                                                            int* __restrict__ count) {
-  const int lane = threadIdx.x & 63;
-  const int b = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (b >= B) return;
+// Which 32-row blocks of batch row b have a nonzero mask entry (one wave). Positions
+// are read 8 x 64 at a time, all loads issued before the ballots.
+__device__ __forceinline__ void plan_row(const void* __restrict__ mask, int mask_dtype, int b,
+                                         int S, int nblk, uint8_t* __restrict__ flag,
+                                         int* __restrict__ count, int lane) {
   int n = 0;
-  for (int s0 = 0; s0 < nblk * 32; s0 += 64) {
-    const int s = s0 + lane;
-    const bool nz = s < S && load_mask(mask, mask_dtype, (int64_t)b * S + s) != 0.0f;
-    const uint64_t bal = __ballot(nz);
-    const int j = s0 / 32;
-    const int lo = (bal & 0xffffffffull) != 0 ? 1 : 0;
-    const int hi = (j + 1 < nblk && (bal >> 32) != 0) ? 1 : 0;
-    if (lane == 0) flag[(int64_t)b * nblk + j] = (uint8_t)lo;
-    if (lane == 1 && j + 1 < nblk) flag[(int64_t)b * nblk + j + 1] = (uint8_t)hi;
-    n += lo + hi;
+  for (int t0 = 0; t0 < nblk * 32; t0 += 8 * 64) {
+    bool nz[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int s = t0 + u * 64 + lane;
+      nz[u] = s < S && load_mask(mask, mask_dtype, (int64_t)b * S + s) != 0.0f;
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int j = (t0 + u * 64) / 32;
+      if (j >= nblk) break;
+      const uint64_t bal = __ballot(nz[u]);
+      const int lo = (bal & 0xffffffffull) != 0 ? 1 : 0;
+      const int hi = (j + 1 < nblk && (bal >> 32) != 0) ? 1 : 0;
+      if (lane == 0) flag[(int64_t)b * nblk + j] = (uint8_t)lo;
+      if (lane == 1 && j + 1 < nblk) flag[(int64_t)b * nblk + j + 1] = (uint8_t)hi;
+      n += lo + hi;
+    }
   }
   if (lane == 0) count[b] = n;
 }
 
-// One workgroup: exclusive scan of the per-row counts, then the block list.
-__global__ __launch_bounds__(PLAN_THREADS) void fwd_plan_list_kernel(
-    int B, int nblk, const uint8_t* __restrict__ flag, const int* __restrict__ count,
-    int* __restrict__ first, int* __restrict__ list, int* __restrict__ meta) {
+// One wave per batch row.
+__global__ __launch_bounds__(256) void fwd_plan_rows_kernel(const void* __restrict__ mask,
+                                                            int mask_dtype, int B, int S, int nblk,
+                                                            uint8_t* __restrict__ flag,
+                                                            int* __restrict__ count) {
+  const int b = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (b < B) plan_row(mask, mask_dtype, b, S, nblk, flag, count, threadIdx.x & 63);
+}
+
+// Exclusive scan of the per-row counts, then the block list (one workgroup).
+__device__ __forceinline__ void plan_list(int B, int nblk, const uint8_t* __restrict__ flag,
+                                          const int* __restrict__ count, int* __restrict__ first,
+                                          int* __restrict__ list, int* __restrict__ meta) {
   __shared__ int wsum[PLAN_THREADS / 64];
   __shared__ int carry;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -157,11 +170,99 @@ __global__ __launch_bounds__(PLAN_THREADS) void fwd_plan_list_kernel(
     __syncthreads();
   }
   if (tid == 0) meta[0] = carry;
-  for (int b = tid; b < B; b += PLAN_THREADS) {
+  // One wave per batch row: lane j takes block j (64 at a time); its slot is the row
+  // start plus the active blocks before it (a ballot prefix), so the list stays in
+  // (b, j) order.
+  const int nw = PLAN_THREADS / 64;
+  for (int b = wave; b < B; b += nw) {
     int k = first[b];
     const uint8_t* f = flag + (int64_t)b * nblk;
-    for (int j = 0; j < nblk; ++j)
-      if (f[j]) list[k++] = b * nblk + j;
+    for (int j0 = 0; j0 < nblk; j0 += 64) {
+      const int j = j0 + lane;
+      const bool on = j < nblk && f[j] != 0;
+      const uint64_t bal = __ballot(on);
+      if (on) list[k + __popcll(bal & ((1ull << lane) - 1ull))] = b * nblk + j;
+      k += __popcll(bal);
+    }
+  }
+}
+
+__global__ __launch_bounds__(PLAN_THREADS) void fwd_plan_list_kernel(
+    int B, int nblk, const uint8_t* __restrict__ flag, const int* __restrict__ count,
+    int* __restrict__ first, int* __restrict__ list, int* __restrict__ meta) {
+  plan_list(B, nblk, flag, count, first, list, meta);
+}
+
+// Both plan steps in one workgroup, for small batches (B * nblk <= PLAN_FUSED_MAX):
+// flags and counts stay in LDS, one launch instead of two.
+constexpr int PLAN_FUSED_MAX = 1 << 14;  // blocks (B * nblk); also bounds B
+__global__ __launch_bounds__(PLAN_THREADS) void fwd_plan_small_kernel(
+    const void* __restrict__ mask, int mask_dtype, int B, int S, int nblk, int* __restrict__ count,
+    int* __restrict__ first, int* __restrict__ list, int* __restrict__ meta) {
+  __shared__ uint8_t fl[PLAN_FUSED_MAX];
+  __shared__ int cnt[PLAN_FUSED_MAX];
+  __shared__ int wsum[PLAN_THREADS / 64];
+  __shared__ int carry;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  constexpr int NW = PLAN_THREADS / 64;
+  for (int b = wave; b < B; b += NW) {
+    int n = 0;
+    for (int t0 = 0; t0 < nblk * 32; t0 += 8 * 64) {
+      bool nz[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int s = t0 + u * 64 + lane;
+        nz[u] = s < S && load_mask(mask, mask_dtype, (int64_t)b * S + s) != 0.0f;
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int j = (t0 + u * 64) / 32;
+        if (j >= nblk) break;
+        const uint64_t bal = __ballot(nz[u]);
+        const int lo = (bal & 0xffffffffull) != 0 ? 1 : 0;
+        const int hi = (j + 1 < nblk && (bal >> 32) != 0) ? 1 : 0;
+        if (lane == 0) fl[b * nblk + j] = (uint8_t)lo;
+        if (lane == 1 && j + 1 < nblk) fl[b * nblk + j + 1] = (uint8_t)hi;
+        n += lo + hi;
+      }
+    }
+    if (lane == 0) cnt[b] = n;
+  }
+  if (tid == 0) carry = 0;
+  __syncthreads();
+  for (int b0 = 0; b0 < B; b0 += PLAN_THREADS) {
+    const int b = b0 + tid;
+    const int c = b < B ? cnt[b] : 0;
+    int x = c;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const int y = __shfl_up(x, d);
+      if (lane >= d) x += y;
+    }
+    if (lane == 63) wsum[wave] = x;
+    __syncthreads();
+    int before = carry;
+    for (int w = 0; w < wave; ++w) before += wsum[w];
+    const int start = before + x - c;
+    if (b < B) {
+      first[b] = start;
+      count[b] = c;
+      cnt[b] = start;  // from here on: the row's first slot
+    }
+    __syncthreads();
+    if (tid == PLAN_THREADS - 1) carry = start + c;
+    __syncthreads();
+  }
+  if (tid == 0) meta[0] = carry;
+  for (int b = wave; b < B; b += NW) {
+    int k = cnt[b];
+    for (int j0 = 0; j0 < nblk; j0 += 64) {
+      const int j = j0 + lane;
+      const bool on = j < nblk && fl[b * nblk + j] != 0;
+      const uint64_t bal = __ballot(on);
+      if (on) list[k + __popcll(bal & ((1ull << lane) - 1ull))] = b * nblk + j;
+      k += __popcll(bal);
+    }
   }
 }
 
@@ -219,19 +320,25 @@ template <> struct Mfma<float> {
   }
 };
 
-// Map the hardware workgroup id to (M-tile, vocab-tile group). Workgroups are
-// dispatched round-robin over the 8 XCDs; first make ids that share an XCD
-// consecutive, then walk groups of GROUP_V vocab-tile groups x all M-tiles, so the
-// workgroups resident on one XCD at a time share a few W tiles and a few M-tiles'
-// rows in its L2.
-__device__ __forceinline__ void tile_of(int wg, int grid, int n_mt, int n_vg, int* m, int* vg) {
-  const int xcd = wg & 7, local = wg >> 3, q = grid >> 3, r = grid & 7;
+// Map the hardware workgroup id to (M-tile, vocab-tile group). The launch sizes the
+// grid for every block being active; ids from n_mt * n_vg on (n_mt = the real M-tile
+// count, known on the device) have no tile and exit. Over the real range: workgroups
+// are dispatched round-robin over the 8 XCDs, so ids sharing an XCD are first made
+// consecutive, then groups of GROUP_V vocab-tile groups x all M-tiles are walked (M-tile
+// fastest): the workgroups resident on one XCD share a few decoder tiles and a few
+// M-tiles' rows in its L2.
+constexpr int GROUP_V = 4;
+__device__ __forceinline__ bool tile_of(int wg, int n_mt, int n_vg, int* m, int* vg) {
+  const int n = n_mt * n_vg;
+  if (wg >= n) return false;
+  const int xcd = wg & 7, local = wg >> 3, q = n >> 3, r = n & 7;
   const int lin = (xcd < r ? xcd * (q + 1) : r * (q + 1) + (xcd - r) * q) + local;
   const int group = lin / (GROUP_V * n_mt);
   const int rem = lin - group * GROUP_V * n_mt;
   const int gv = min(GROUP_V, n_vg - group * GROUP_V);
   *m = rem / gv;
   *vg = group * GROUP_V + rem % gv;
+  return true;
 }
 
 struct Geo {
@@ -500,10 +607,9 @@ __global__ __launch_bounds__(NTHREADS, 1) void sparton_fwd_kernel(
   const int wm = wave / WAVES_N, wn = wave % WAVES_N;
 
   const int n_vg = (n_vt + P - 1) / P;
-  int m, vg;
-  tile_of(blockIdx.x, gridDim.x, n_mt_max, n_vg, &m, &vg);
   const int n_blk = __builtin_amdgcn_readfirstlane(meta[0]);
-  if (m * MBLK >= n_blk) return;  // fewer active blocks than the launch allowed for
+  int m, vg;
+  if (!tile_of(blockIdx.x, (n_blk + MBLK - 1) / MBLK, n_vg, &m, &vg)) return;
   const int vt_lo = vg * P, n_tiles = min(P, n_vt - vt_lo);
   const int n_valid = min(MBLK, n_blk - m * MBLK);
 
@@ -578,7 +684,10 @@ __global__ __launch_bounds__(NTHREADS, 1) void sparton_fwd_kernel(
 // ---- fixup ------------------------------------------------------------------------
 
 // Per batch row: no active block -> reps = 0, argmax = 0; blocks spread over several
-// M-tiles -> merge their partials in tile order (= s order).
+// M-tiles -> merge their partials in tile order (= s order). A workgroup covers 1024
+// vocab ids (4 per thread) of one batch row and exits at once if the main kernel
+// completed that row.
+constexpr int FIX_COLS = 1024;
 template <typename T>
 __global__ __launch_bounds__(256) void fwd_fixup_kernel(int V, const int* __restrict__ count,
                                                         const int* __restrict__ first,
@@ -587,7 +696,6 @@ __global__ __launch_bounds__(256) void fwd_fixup_kernel(int V, const int* __rest
                                                         int32_t* __restrict__ argmax,
                                                         float* __restrict__ reps_f32) {
   const int b = blockIdx.y;
-  const int v = blockIdx.x * 256 + threadIdx.x;
   const int n = count[b];
   int ms = 0, me = 0;
   if (n > 0) {
@@ -595,26 +703,30 @@ __global__ __launch_bounds__(256) void fwd_fixup_kernel(int V, const int* __rest
     me = (first[b] + n - 1) / MBLK;
     if (ms == me) return;  // written by the main kernel
   }
-  if (v >= V) return;
-  float bv = 0.0f;
-  int bi = 0;
-  if (n > 0) {
-    const float2 p0 = part[((int64_t)ms * 2 + 1) * V + v];
-    bv = p0.x;
-    bi = __float_as_int(p0.y);
-    for (int mm = ms + 1; mm <= me; ++mm) {
-      const float2 p = part[((int64_t)mm * 2 + 0) * V + v];
-      if (p.x > bv) {  // later tiles hold higher s: strict '>' keeps the lower on ties
-        bv = p.x;
-        bi = __float_as_int(p.y);
+#pragma unroll
+  for (int k = 0; k < FIX_COLS / 256; ++k) {
+    const int v = blockIdx.x * FIX_COLS + k * 256 + threadIdx.x;
+    if (v >= V) break;
+    float bv = 0.0f;
+    int bi = 0;
+    if (n > 0) {
+      const float2 p0 = part[((int64_t)ms * 2 + 1) * V + v];
+      bv = p0.x;
+      bi = __float_as_int(p0.y);
+      for (int mm = ms + 1; mm <= me; ++mm) {
+        const float2 p = part[((int64_t)mm * 2 + 0) * V + v];
+        if (p.x > bv) {  // later tiles hold higher s: strict '>' keeps the lower on ties
+          bv = p.x;
+          bi = __float_as_int(p.y);
+        }
       }
     }
+    const int64_t o = (int64_t)b * V + v;
+    const float rv = log1pf(bv);
+    reps[o] = from_f32<T>(rv);
+    if (argmax != nullptr) argmax[o] = bi;
+    if (reps_f32 != nullptr) reps_f32[o] = rv;
   }
-  const int64_t o = (int64_t)b * V + v;
-  const float rv = log1pf(bv);
-  reps[o] = from_f32<T>(rv);
-  if (argmax != nullptr) argmax[o] = bi;
-  if (reps_f32 != nullptr) reps_f32[o] = rv;
 }
 
 // Vocab tiles per workgroup: enough workgroups to keep every CU busy for several
@@ -643,17 +755,22 @@ static int launch(const void* H, const void* W, const void* bias, const void* ma
   const int P = tiles_per_group(cdiv(n_mt_max * 3, 5), n_vt);
   const int64_t grid = n_mt_max * cdiv(n_vt, P);
   if (grid > INT32_MAX) return SPARTON_EUNSUPPORTED;
-  hipLaunchKernelGGL(fwd_plan_rows_kernel, dim3((unsigned)cdiv(B, 4)), dim3(256), 0, stream, mask,
-                     mask_dtype, (int)B, (int)S, (int)nblk, w.flag, w.count);
-  hipLaunchKernelGGL(fwd_plan_list_kernel, dim3(1), dim3(PLAN_THREADS), 0, stream, (int)B,
-                     (int)nblk, (const uint8_t*)w.flag, (const int*)w.count, w.first, w.list,
-                     w.meta);
+  if (B <= PLAN_FUSED_MAX && B * nblk <= PLAN_FUSED_MAX) {
+    hipLaunchKernelGGL(fwd_plan_small_kernel, dim3(1), dim3(PLAN_THREADS), 0, stream, mask,
+                       mask_dtype, (int)B, (int)S, (int)nblk, w.count, w.first, w.list, w.meta);
+  } else {
+    hipLaunchKernelGGL(fwd_plan_rows_kernel, dim3((unsigned)cdiv(B, 4)), dim3(256), 0, stream,
+                       mask, mask_dtype, (int)B, (int)S, (int)nblk, w.flag, w.count);
+    hipLaunchKernelGGL(fwd_plan_list_kernel, dim3(1), dim3(PLAN_THREADS), 0, stream, (int)B,
+                       (int)nblk, (const uint8_t*)w.flag, (const int*)w.count, w.first, w.list,
+                       w.meta);
+  }
   if (grid > 0)  // S == 0: no blocks, the fixup writes every row
     hipLaunchKernelGGL(sparton_fwd_kernel<T>, dim3((unsigned)grid), dim3(NTHREADS), 0, stream,
                        (const T*)H, (const T*)W, (const T*)bias, mask, mask_dtype, (T*)reps,
                        argmax, reps_f32, (int)S, (int)D, (int)V, (int)n_vt, P, (int)nblk,
                        (int)n_mt_max, (const int*)w.meta, (const int*)w.list, w.part);
-  hipLaunchKernelGGL(fwd_fixup_kernel<T>, dim3((unsigned)cdiv(V, 256), (unsigned)B), dim3(256), 0,
+  hipLaunchKernelGGL(fwd_fixup_kernel<T>, dim3((unsigned)cdiv(V, FIX_COLS), (unsigned)B), dim3(256), 0,
                      stream, (int)V, (const int*)w.count, (const int*)w.first,
                      (const float2*)w.part, (T*)reps, argmax, reps_f32);
   const hipError_t e = hipGetLastError();

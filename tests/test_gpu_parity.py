@@ -77,6 +77,7 @@ CASES = [
     ("fp16", 3, 130, 24, 520, True, "int64"),   # rows shorter than one slab, 3 vocab tiles
     ("bf16", 3, 900, 64, 2100, True, "gaps"),   # fully masked middle chunk, masked row
     ("bf16", 37, 40, 64, 700, True, "int64"),   # many short rows: several rows per row tile
+    ("fp32", 130, 3, 16, 70, True, "int64"),    # B > 128: the unstaged dW path
 ]
 
 # Cases run again with several vocab tiles per workgroup (the unit stream then crosses
