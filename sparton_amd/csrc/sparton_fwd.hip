@@ -272,6 +272,8 @@ struct Smem {
   u32x4 a[2][BM * CHUNKS];   // [stage][row * 8 + (chunk ^ f(row))]
   u32x4 b[2][BN * CHUNKS];
   float maskf[BM];           // mask of the tile's rows (0 past S or past the last block)
+  int maskw[BM];             // the same as an AND mask for 0/1 masks: ~31 (kept) or 0
+  int mask_binary;           // every maskf value is 0 or 1
   float biasf[MAX_P * BN];   // bias of the workgroup's vocab tiles
   float pv[MBLK][BN];        // per block, per column: (max, argmax) of the block's rows
   int pi[MBLK][BN];
@@ -500,54 +502,60 @@ __device__ __forceinline__ int run_unit(Smem& sm, const Geo& g, int v0, int v0_n
     if (own || v0_next >= 0) issue_slab(sm, g, own ? v0 : v0_next, own ? k + 2 : k + 2 - nk, cur, wave, lane);
   }
 
-  // Block epilogue: 32x32 accumulator layout -- lane holds column l32, and for register
-  // i the row 8*(i/4) + 4*h + (i%4) of the block. Rows rise with i, so a strict '>'
-  // keeps the lowest s within the lane; lanes l and l^32 are then merged.
-  // Per-lane bases; the block offsets below are compile-time constants, which keeps
-  // them in the LDS instructions' offset fields instead of in registers.
+  // Block epilogue. 32x32 accumulator layout: lane holds column l32, and register
+  // i = 4q + e the row 8q + 4h + e of the block. Each candidate becomes one integer key:
+  //     key = (bits(x) & ~31) | (31 - row),   x = acc * mask
+  // i.e. x with its 5 lowest mantissa bits replaced by the inverted row. For x > 0 the
+  // float bits order like the values, so the largest key has the largest x and, among
+  // x equal to 2^-18 relative, the lowest row -- the lowest-s rule, applied at the
+  // precision the key keeps (the reference compares bf16-rounded logits, 2^-8). Keys of
+  // x <= 0 are never positive-valued and decode to (0, row 0), the initial max. With a
+  // 0/1 mask, bits(x) & ~31 is one AND with the row's mask word.
+  const int binary = sm.mask_binary;
   const float* mrow = &sm.maskf[wm * 32 + 4 * h];
+  const int* wrow = &sm.maskw[wm * 32 + 4 * h];
   float* pvw = &sm.pv[wm][wn * 64 + l32];
   int* piw = &sm.pi[wm][wn * 64 + l32];
 #pragma unroll
   for (int j = 0; j < JM; ++j) {
     const int s_blk = sm.blk_s[wm + WAVES_M * j];
-    float bv[NB_PER_WAVE];
-    int bi[NB_PER_WAVE];
+    int kmax[NB_PER_WAVE];
 #pragma unroll
-    for (int nb = 0; nb < NB_PER_WAVE; ++nb) {
-      bv[nb] = 0.0f;
-      bi[nb] = 0;
-    }
+    for (int nb = 0; nb < NB_PER_WAVE; ++nb) kmax[nb] = INT32_MIN;
+    if (binary) {
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const f32x4 m4 = *(const f32x4*)(mrow + j * WAVES_M * 32 + 8 * q);
+      for (int q = 0; q < 4; ++q) {
+        const i32x4 w4 = *(const i32x4*)(wrow + j * WAVES_M * 32 + 8 * q);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int s = s_blk + 8 * q + 4 * h + e;
+        for (int e = 0; e < 4; ++e)
 #pragma unroll
-        for (int nb = 0; nb < NB_PER_WAVE; ++nb) {
-          const float x = acc[j][nb][q * 4 + e] * m4[e];
-          if (x > bv[nb]) {
-            bv[nb] = x;
-            bi[nb] = s;
-          }
-        }
+          for (int nb = 0; nb < NB_PER_WAVE; ++nb)
+            kmax[nb] = max(kmax[nb], (__float_as_int(acc[j][nb][q * 4 + e]) & w4[e]) | (31 - 8 * q - e));
+      }
+    } else {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const f32x4 m4 = *(const f32x4*)(mrow + j * WAVES_M * 32 + 8 * q);
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+#pragma unroll
+          for (int nb = 0; nb < NB_PER_WAVE; ++nb)
+            kmax[nb] = max(kmax[nb], (__float_as_int(acc[j][nb][q * 4 + e] * m4[e]) & ~31) | (31 - 8 * q - e));
       }
     }
 #pragma unroll
     for (int nb = 0; nb < NB_PER_WAVE; ++nb) {
-      // v_permlane32_swap exchanges the lane halves: element 1 of the result holds, in
-      // lanes 0..31, the values of lanes 32..63 (the only lanes that store below).
-      const float ov = __uint_as_float(
-          __builtin_amdgcn_permlane32_swap(__float_as_uint(bv[nb]), __float_as_uint(bv[nb]), false, false)[1]);
-      const int oi = (int)__builtin_amdgcn_permlane32_swap((unsigned)bi[nb], (unsigned)bi[nb], false, false)[1];
-      if (ov > bv[nb] || (ov == bv[nb] && oi < bi[nb])) {
-        bv[nb] = ov;
-        bi[nb] = oi;
-      }
+      // The keys above encode rows 8q + e; lanes of half 1 hold rows 4 higher. Then
+      // v_permlane32_swap exchanges the halves: element 1 of the result holds, in lanes
+      // 0..31, the keys of lanes 32..63 (the only lanes that store below).
+      const int k = kmax[nb] - 4 * h;
+      const int ko = (int)__builtin_amdgcn_permlane32_swap((unsigned)k, (unsigned)k, false, false)[1];
+      const int kb = max(k, ko);
+      const float v = __int_as_float(kb & ~31);
       if (h == 0) {
-        pvw[j * WAVES_M * BN + nb * 32] = bv[nb];
-        piw[j * WAVES_M * BN + nb * 32] = bi[nb];
+        const bool pos = v > 0.0f;
+        pvw[j * WAVES_M * BN + nb * 32] = pos ? v : 0.0f;
+        piw[j * WAVES_M * BN + nb * 32] = pos ? s_blk + 31 - (kb & 31) : 0;
       }
     }
   }
@@ -565,13 +573,21 @@ __device__ __forceinline__ void write_unit(Smem& sm, int m, int v0, int V, int n
   if (tid < BN && v0 + tid < V) {
     const int v = v0 + tid;
     const int b_prev = sm.blk_b[MBLK], b_next = sm.blk_b[MBLK + 1];
+    float pvr[MBLK];
+    int pir[MBLK];
+#pragma unroll
+    for (int r = 0; r < MBLK; ++r) {  // all loads first (rows past n_valid are unused)
+      pvr[r] = sm.pv[r][tid];
+      pir[r] = sm.pi[r][tid];
+    }
     float bv = 0.0f;
     int bi = 0;
-    for (int r = 0; r < n_valid; ++r) {
-      const float pv = sm.pv[r][tid];
-      if (pv > bv) {  // earlier blocks hold lower s: strict '>' keeps them on ties
-        bv = pv;
-        bi = sm.pi[r][tid];
+#pragma unroll
+    for (int r = 0; r < MBLK; ++r) {
+      if (r >= n_valid) break;
+      if (pvr[r] > bv) {  // earlier blocks hold lower s: strict '>' keeps them on ties
+        bv = pvr[r];
+        bi = pir[r];
       }
       const int b = sm.blk_b[r];
       if (r + 1 == n_valid || sm.blk_b[r + 1] != b) {  // the segment of batch row b ends
@@ -614,6 +630,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void sparton_fwd_kernel(
   const int n_valid = min(MBLK, n_blk - m * MBLK);
 
   // The tile's blocks, and the batch rows of the blocks just before and after it.
+  if (tid == 0) sm.mask_binary = 1;  // cleared below (after a barrier) by any other value
   if (tid < MBLK + 2) {
     const int e = tid < MBLK ? m * MBLK + tid : (tid == MBLK ? m * MBLK - 1 : m * MBLK + MBLK);
     const bool ok = e >= 0 && e < n_blk && (tid >= MBLK || tid < n_valid);
@@ -650,7 +667,10 @@ __global__ __launch_bounds__(NTHREADS, 1) void sparton_fwd_kernel(
   if (tid < BM) {
     const int r = tid >> 5;
     const int s = sm.blk_s[r] + (tid & 31);
-    sm.maskf[tid] = (r < n_valid && s < S) ? load_mask(mask, mask_dtype, (int64_t)sm.blk_b[r] * S + s) : 0.0f;
+    const float mv = (r < n_valid && s < S) ? load_mask(mask, mask_dtype, (int64_t)sm.blk_b[r] * S + s) : 0.0f;
+    sm.maskf[tid] = mv;
+    sm.maskw[tid] = mv != 0.0f ? ~31 : 0;
+    if (__ballot(mv != 0.0f && mv != 1.0f) != 0 && lane == 0) sm.mask_binary = 0;
   }
 
   const int jm = n_valid <= wm ? 0 : min(4, (n_valid - wm + 1) / WAVES_M);
