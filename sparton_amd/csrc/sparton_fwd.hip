@@ -16,11 +16,12 @@
 // tile except the last is full, so each decoder tile loaded from memory is used for
 // 256 live rows instead of one batch row's (often partly padded) 256 positions.
 //
-// Main kernel. A workgroup owns one M-tile and P consecutive vocab tiles of BN columns
-// (a "unit" per vocab tile). For each unit it computes the 256 x BN logit tile with
-// bf16/fp16 (or fp32) MFMA, K = D streamed through two LDS stages; the K slabs of all
-// its units form one stream, so a unit's first slabs load while the previous unit
-// finishes. The epilogue folds each 32-row block into a per-column (max, argmax),
+// Main kernel. A "unit" is one M-tile x one vocab tile of BN columns. The grid is
+// persistent (one workgroup per CU) and each workgroup walks its units in rounds; for
+// each it computes the 256 x BN logit tile with bf16/fp16 (or fp32) MFMA, K = D
+// streamed through two LDS stages. The K slabs of all its units form one stream, and
+// the next unit's metadata (block list, row mask, row offsets, bias) is fetched during
+// the current unit's first K steps, so a unit starts while the previous one finishes. The epilogue folds each 32-row block into a per-column (max, argmax),
 // merges consecutive blocks of the same batch row in s order (larger value; on ties
 // the lower s, which is the earlier block), and per batch-row segment either writes
 // reps/argmax (segment complete in this tile) or, when the segment continues into a
@@ -63,7 +64,6 @@ constexpr int CHUNKS = SLAB / 16;    // 16-byte chunks per row slab (8)
 constexpr int ROWS_PER_LOAD = 64 / CHUNKS;          // rows one wave-wide load covers (8)
 constexpr int A_LOADS = BM / ROWS_PER_LOAD / NWAVES;  // wave-wide loads per slab for A (4)
 constexpr int B_LOADS = BN / ROWS_PER_LOAD / NWAVES;  // and for B (4)
-constexpr int MAX_P = 8;             // vocab tiles per workgroup
 constexpr int MAX_S = 16384;         // positions per batch row (512 blocks)
 constexpr int PLAN_THREADS = 1024;
 
@@ -78,6 +78,8 @@ struct Work {
   uint8_t* flag;      // [B][nblk] 1 = block has a nonzero mask entry
   int* list;          // [B*nblk] active blocks as b * nblk + j, in (b, j) order
   float2* part;       // [n_mt_max][2][V] partial (max, argmax bits) of edge segments
+  float* rowmask;     // [n_mt_max * 256] mask of each tile row, in list order (0 past S
+                      // and past the last active block of the last tile)
   size_t total;
 };
 
@@ -98,6 +100,7 @@ static Work carve(void* base, int64_t B, int64_t S, int64_t V) {
   w.flag = (uint8_t*)take((size_t)(B * nblk));
   w.list = (int*)take((size_t)(B * nblk) * 4);
   w.part = (float2*)take((size_t)(n_mt_max * 2 * V) * sizeof(float2));
+  w.rowmask = (float*)take((size_t)(n_mt_max * 256) * sizeof(float));
   w.total = off;
   return w;
 }
@@ -193,12 +196,38 @@ __global__ __launch_bounds__(PLAN_THREADS) void fwd_plan_list_kernel(
   plan_list(B, nblk, flag, count, first, list, meta);
 }
 
+// Row mask in list order: tile row t = 32 e + r is position 32 j + r of batch row b,
+// where list[e] = b * nblk + j; rows of entries past the last active block are 0.
+__device__ __forceinline__ void fill_rowmask(const void* __restrict__ mask, int mask_dtype, int S,
+                                             int nblk, int n_blk, const int* __restrict__ list,
+                                             float* __restrict__ rowmask, int t) {
+  const int e = t >> 5;
+  float v = 0.0f;
+  if (e < n_blk) {
+    const int code = list[e];
+    const int b = code / nblk;
+    const int s = (code - b * nblk) * 32 + (t & 31);
+    if (s < S) v = load_mask(mask, mask_dtype, (int64_t)b * S + s);
+  }
+  rowmask[t] = v;
+}
+
+__global__ __launch_bounds__(256) void fwd_plan_rowmask_kernel(
+    const void* __restrict__ mask, int mask_dtype, int S, int nblk, const int* __restrict__ meta,
+    const int* __restrict__ list, float* __restrict__ rowmask) {
+  const int n_blk = meta[0];
+  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (t < (int64_t)(n_blk + MBLK - 1) / MBLK * BM)
+    fill_rowmask(mask, mask_dtype, S, nblk, n_blk, list, rowmask, (int)t);
+}
+
 // Both plan steps in one workgroup, for small batches (B * nblk <= PLAN_FUSED_MAX):
 // flags and counts stay in LDS, one launch instead of two.
 constexpr int PLAN_FUSED_MAX = 1 << 14;  // blocks (B * nblk); also bounds B
 __global__ __launch_bounds__(PLAN_THREADS) void fwd_plan_small_kernel(
     const void* __restrict__ mask, int mask_dtype, int B, int S, int nblk, int* __restrict__ count,
-    int* __restrict__ first, int* __restrict__ list, int* __restrict__ meta) {
+    int* __restrict__ first, int* __restrict__ list, int* __restrict__ meta,
+    float* __restrict__ rowmask) {
   __shared__ uint8_t fl[PLAN_FUSED_MAX];
   __shared__ int cnt[PLAN_FUSED_MAX];
   __shared__ int wsum[PLAN_THREADS / 64];
@@ -264,22 +293,32 @@ __global__ __launch_bounds__(PLAN_THREADS) void fwd_plan_small_kernel(
       k += __popcll(bal);
     }
   }
+  __syncthreads();  // the list (global memory, written by this workgroup) is complete
+  const int n_blk = carry;
+  const int n_rows = (n_blk + MBLK - 1) / MBLK * BM;
+  for (int t = tid; t < n_rows; t += PLAN_THREADS)
+    fill_rowmask(mask, mask_dtype, S, nblk, n_blk, list, rowmask, t);
 }
 
 // ---- main kernel ------------------------------------------------------------------
 
-struct Smem {
-  u32x4 a[2][BM * CHUNKS];   // [stage][row * 8 + (chunk ^ f(row))]
-  u32x4 b[2][BN * CHUNKS];
+// Metadata of one unit, double-buffered: the next unit's copy is filled while the
+// current unit computes. 16-byte aligned: the epilogue reads the mask 4 rows at a time.
+struct __align__(16) UnitMeta {
   float maskf[BM];           // mask of the tile's rows (0 past S or past the last block)
   int maskw[BM];             // the same as an AND mask for 0/1 masks: ~31 (kept) or 0
-  int mask_binary;           // every maskf value is 0 or 1
-  float biasf[MAX_P * BN];   // bias of the workgroup's vocab tiles
-  float pv[MBLK][BN];        // per block, per column: (max, argmax) of the block's rows
-  int pi[MBLK][BN];
   int blk_b[MBLK + 2];       // batch row of each block; [MBLK], [MBLK+1]: rows of the
                              // blocks just before / after the tile (-1 if none)
   int blk_s[MBLK];           // first position of each block (32 j)
+  int mask_binary;           // every maskf value is 0 or 1
+};
+
+struct Smem {
+  u32x4 a[2][BM * CHUNKS];   // [stage][row * 8 + (chunk ^ f(row))]
+  u32x4 b[2][BN * CHUNKS];
+  float pv[MBLK][BN];        // per block, per column: (max, argmax) of the block's rows
+  int pi[MBLK][BN];
+  UnitMeta um[2];
 };
 
 typedef __attribute__((address_space(3))) void lds_void;
@@ -322,68 +361,175 @@ template <> struct Mfma<float> {
   }
 };
 
-// Map the hardware workgroup id to (M-tile, vocab-tile group). The launch sizes the
-// grid for every block being active; ids from n_mt * n_vg on (n_mt = the real M-tile
-// count, known on the device) have no tile and exit. Over the real range: workgroups
-// are dispatched round-robin over the 8 XCDs, so ids sharing an XCD are first made
-// consecutive, then groups of GROUP_V vocab-tile groups x all M-tiles are walked (M-tile
-// fastest): the workgroups resident on one XCD share a few decoder tiles and a few
-// M-tiles' rows in its L2.
+// ---- unit schedule ----
+//
+// The grid is persistent (about one workgroup per CU); the units (M-tile, vocab tile)
+// are dealt out in rounds of gridDim.x. Workgroups are dispatched round-robin over the
+// 8 XCDs, so in each round the workgroups of one XCD (w % 8 equal) take a contiguous
+// range of unit numbers; unit numbers walk groups of GROUP_V vocab tiles x all M-tiles
+// (vocab tile fastest), so the units running together on one XCD share a few decoder
+// tiles and a few M-tiles' rows in its L2. In the last, partial round the ranges
+// shrink evenly and workgroups past them stop.
 constexpr int GROUP_V = 4;
-__device__ __forceinline__ bool tile_of(int wg, int n_mt, int n_vg, int* m, int* vg) {
-  const int n = n_mt * n_vg;
-  if (wg >= n) return false;
-  const int xcd = wg & 7, local = wg >> 3, q = n >> 3, r = n & 7;
-  const int lin = (xcd < r ? xcd * (q + 1) : r * (q + 1) + (xcd - r) * q) + local;
-  const int group = lin / (GROUP_V * n_mt);
-  const int rem = lin - group * GROUP_V * n_mt;
-  const int gv = min(GROUP_V, n_vg - group * GROUP_V);
-  *m = rem / gv;
-  *vg = group * GROUP_V + rem % gv;
-  return true;
+
+// Unit number of workgroup w in round r, or -1 when it has none (it is done).
+__device__ __forceinline__ int unit_at(int w, int r, int G, int n_units) {
+  const int base = r * G;
+  const int R = min(G, n_units - base);
+  if (R <= 0) return -1;
+  const int x = w & 7, local = w >> 3, q = R >> 3, rr = R & 7;
+  if (local >= q + (x < rr ? 1 : 0)) return -1;
+  return base + (x < rr ? x * (q + 1) : rr * (q + 1) + (x - rr) * q) + local;
 }
 
-struct Geo {
+__device__ __forceinline__ void unit_tile(int u, int n_mt, int n_vt, int* m, int* vt) {
+  const int per_group = GROUP_V * n_mt;
+  const int group = u / per_group;
+  const int rem = u - group * per_group;
+  const int gv = min(GROUP_V, n_vt - group * GROUP_V);
+  const int mm = rem / gv;
+  *m = mm;
+  *vt = group * GROUP_V + rem - mm * gv;
+}
+
+// Launch-wide, wave-uniform parameters.
+template <typename T>
+struct Args {
   const char* H;      // H[0, 0, :]
   const char* W;
+  const T* bias;
+  const float* rowmask;  // [n_mt * BM] mask of each tile row
+  const int* list;
+  int n_blk;          // active blocks
+  int nblk;           // blocks per batch row
+  int S;
   int row_bytes;      // D * sizeof(T)
   int nk_full;        // slabs lying entirely inside the row
   int V;
-  int n_valid;        // active blocks in this M-tile (1..8)
-  uint32_t a_off[A_LOADS];  // per lane: byte offset from H of its A row and chunk
 };
+
+// Per-lane data of one unit.
+struct Lanes {
+  uint32_t a_off[A_LOADS];    // byte offset from H of the lane's A row and chunk, per load
+  float bias[NB_PER_WAVE];    // bias of the lane's columns
+};
+
+// ---- unit metadata (each step is run by every thread; the ones named take part) ----
+
+// Threads 0..MBLK+1: the tile's list entry (b * nblk + j), or -1.
+__device__ __forceinline__ int block_entry(int m, int tid);
+__device__ __forceinline__ int block_code(const int* list, int n_blk, int m, int n_valid, int tid) {
+  const int e = block_entry(m, tid);
+  const bool ok = e >= 0 && e < n_blk && (tid >= MBLK || tid < n_valid);
+  return ok ? list[e] : -1;
+}
+
+__device__ __forceinline__ void put_blocks(UnitMeta& um, int code, int nblk, int tid) {
+  if (tid < MBLK + 2) {
+    um.blk_b[tid] = code >= 0 ? code / nblk : -1;
+    if (tid < MBLK) um.blk_s[tid] = code >= 0 ? (code % nblk) * 32 : 0;
+  }
+}
+
+// Threads 0..BM-1, given the mask value of tile row tid: the AND word, and clear
+// mask_binary (set to 1 by thread 0 before a barrier) on any value other than 0 / 1.
+__device__ __forceinline__ void put_mask_words(UnitMeta& um, float mv, int tid, int lane) {
+  if (tid < BM) {  // whole waves
+    um.maskw[tid] = mv != 0.0f ? ~31 : 0;
+    if (__ballot(mv != 0.0f && mv != 1.0f) != 0 && lane == 0) um.mask_binary = 0;
+  }
+}
+
+// Per lane (after put_blocks is visible): the byte offsets of its A rows. Rows of
+// blocks past n_valid get some valid row (their loads are skipped); positions past S
+// any valid position of the row.
+__device__ __forceinline__ void row_offsets(const UnitMeta& um, int n_valid, int S, int row_bytes,
+                                            int wave, int lane, uint32_t* a_off) {
+#pragma unroll
+  for (int i = 0; i < A_LOADS; ++i) {
+    const int grp = i * NWAVES + wave;
+    const int row = grp * ROWS_PER_LOAD + (lane >> 3);
+    const int r = min(row >> 5, n_valid - 1);
+    const int s = min(um.blk_s[r] + (row & 31), S - 1);
+    a_off[i] = (uint32_t)(((int64_t)um.blk_b[r] * S + s) * row_bytes) + lane_chunk(row, lane);
+  }
+}
+
+template <typename T>
+__device__ __forceinline__ void load_bias(const Args<T>& a, int v0, int wn, int lane, float* out) {
+#pragma unroll
+  for (int nb = 0; nb < NB_PER_WAVE; ++nb) {
+    const int col = v0 + wn * 64 + nb * 32 + (lane & 31);
+    out[nb] = (a.bias != nullptr && col < a.V) ? to_f32(a.bias[col]) : 0.0f;
+  }
+}
+
+// Raw loads for the in-loop prefetch: the bits are loaded without any conversion or
+// select, so no instruction needs them until they are converted a K step later, after
+// the step's full drain. (Converting right after the load would make the wave wait for
+// every load in flight -- the next slab included.)
+template <typename T> __device__ __forceinline__ uint32_t load_bits(const T* p, int64_t i);
+template <> __device__ __forceinline__ uint32_t load_bits(const bf16* p, int64_t i) {
+  return ((const uint16_t*)p)[i];
+}
+template <> __device__ __forceinline__ uint32_t load_bits(const f16* p, int64_t i) {
+  return ((const uint16_t*)p)[i];
+}
+template <> __device__ __forceinline__ uint32_t load_bits(const float* p, int64_t i) {
+  return ((const uint32_t*)p)[i];
+}
+template <typename T> __device__ __forceinline__ float bits_to_f32(uint32_t x);
+template <> __device__ __forceinline__ float bits_to_f32<bf16>(uint32_t x) { return __uint_as_float(x << 16); }
+template <> __device__ __forceinline__ float bits_to_f32<f16>(uint32_t x) {
+  return (float)__builtin_bit_cast(f16, (uint16_t)x);
+}
+template <> __device__ __forceinline__ float bits_to_f32<float>(uint32_t x) { return __uint_as_float(x); }
+
+// ---- K stream ----
 
 // Issue the direct global -> LDS copies of K slab k of vocab tile v0 into stage buf.
 // Wave w, load i covers the 8-row group g = i * NWAVES + w (rows 8g..8g+7 of the
-// tile, in block g / 4); lane L lands at LDS chunk g*64 + L. Chunks past the row end
-// (tail or padding slabs) re-read slab 0 -- valid, finite data -- and their W copies
-// are zeroed by zero_tail() before use. W rows past V re-read row V-1 (never stored);
-// A loads of blocks past the last active one are skipped.
-__device__ __forceinline__ void issue_slab(Smem& sm, const Geo& g, int v0, int k, int buf,
-                                           int wave, int lane) {
+// tile, in block g / 4); lane L lands at LDS chunk g*64 + L. A chunk past the row end
+// (tail or padding slabs) re-reads the row's first chunk -- valid, finite data inside
+// the row, so nothing outside H or W is read -- and its W copy is zeroed by zero_tail()
+// before use (a zero W times a finite H adds exactly 0). W rows past V re-read row V-1
+// (never stored); A loads of blocks past the last active one (n_valid) are skipped.
+template <typename T>
+__device__ __forceinline__ void issue_slab(Smem& sm, const Args<T>& a, const uint32_t* a_off,
+                                           int n_valid, int v0, int k, int buf, int wave, int lane) {
   const uint32_t kb = (uint32_t)k * SLAB;
-  const bool tail = k >= g.nk_full;
-  const int a_groups = g.n_valid * (32 / ROWS_PER_LOAD);
+  const bool tail = k >= a.nk_full;
+  const int a_groups = n_valid * (32 / ROWS_PER_LOAD);
 #pragma unroll
   for (int i = 0; i < A_LOADS; ++i) {
     const int grp = i * NWAVES + wave;
     const uint32_t c16 = lane_chunk(grp * ROWS_PER_LOAD + (lane >> 3), lane);
-    const uint32_t step = (!tail || kb + c16 < (uint32_t)g.row_bytes) ? kb : 0u;
+    // a_off includes c16: adding 0 - c16 (mod 2^32) lands on the row's first chunk.
+    const uint32_t step = (!tail || kb + c16 < (uint32_t)a.row_bytes) ? kb : 0u - c16;
     if (grp < a_groups)
-      __builtin_amdgcn_global_load_lds((const void*)(g.H + (g.a_off[i] + step)),
+      __builtin_amdgcn_global_load_lds((const void*)(a.H + (a_off[i] + step)),
                                        (lds_void*)&sm.a[buf][grp * 64], 16, 0, 0);
   }
-  const char* bb = g.W + (int64_t)v0 * g.row_bytes;
-  const int b_last = g.V - 1 - v0;
+  const char* bb = a.W + (int64_t)v0 * a.row_bytes;
+  const int b_last = a.V - 1 - v0;
 #pragma unroll
   for (int i = 0; i < B_LOADS; ++i) {
     const int grp = i * NWAVES + wave;
     const int row = grp * ROWS_PER_LOAD + (lane >> 3);
     const uint32_t c16 = lane_chunk(row, lane);
-    const uint32_t step = (!tail || kb + c16 < (uint32_t)g.row_bytes) ? kb : 0u;
-    const uint32_t off = (uint32_t)min(row, b_last) * (uint32_t)g.row_bytes + c16 + step;
+    const uint32_t step = (!tail || kb + c16 < (uint32_t)a.row_bytes) ? kb : 0u - c16;
+    const uint32_t off = (uint32_t)min(row, b_last) * (uint32_t)a.row_bytes + c16 + step;
     __builtin_amdgcn_global_load_lds((const void*)(bb + off), (lds_void*)&sm.b[buf][grp * 64], 16, 0, 0);
   }
+}
+
+// Direct loads one slab issues from this wave.
+__device__ __forceinline__ int slab_loads(int n_valid, int wave) {
+  const int a_groups = n_valid * (32 / ROWS_PER_LOAD);
+  int n = B_LOADS;
+#pragma unroll
+  for (int i = 0; i < A_LOADS; ++i) n += (i * NWAVES + wave < a_groups) ? 1 : 0;
+  return n;
 }
 
 // Zero the W chunks of slab k (in stage buf) that lie past D; run after its copies
@@ -431,30 +577,114 @@ __device__ __forceinline__ void wait_loads_at_most(int n) {
   }
 }
 
+// ---- one unit ----
+
+// The next unit of this workgroup, when its metadata is fetched inside the current
+// unit's K loop (nk >= 4). Each step ends with a full drain and a barrier, which orders
+// the steps across waves:
+//   step 0: the rows' mask copied straight into LDS (direct loads, like the slabs);
+//           raw loads of the tile's list entries and of the bias of its columns;
+//   step 1: blocks and mask words stored to LDS;
+//   step 2: A-row offsets, from the stored blocks.
+// The bias is converted at the hand-over. The next unit's first two slabs are issued
+// during the current unit's last two steps.
+struct Next {
+  bool on;
+  int m, v0, n_valid;
+  int code_bits;          // threads 0..MBLK+1: list entry (clamped index)
+  uint32_t bias_bits[NB_PER_WAVE];
+  uint32_t a_off[A_LOADS];
+};
+
+__device__ __forceinline__ int block_entry(int m, int tid) {
+  return tid < MBLK ? m * MBLK + tid : (tid == MBLK ? m * MBLK - 1 : m * MBLK + MBLK);
+}
+
+template <typename T>
+__device__ __forceinline__ void fetch_step(int k, const Args<T>& a, Next& nx, UnitMeta& um,
+                                           int tid, int wave, int lane, int wn) {
+  if (k == 0) {
+    if (tid == 0) um.mask_binary = 1;
+    if (wave < BM / 64)
+      __builtin_amdgcn_global_load_lds((const void*)(a.rowmask + (int64_t)nx.m * BM + tid),
+                                       (lds_void*)&um.maskf[wave * 64], 4, 0, 0);
+    if (tid < MBLK + 2) nx.code_bits = a.list[min(max(block_entry(nx.m, tid), 0), a.n_blk - 1)];
+    if (a.bias != nullptr) {
+#pragma unroll
+      for (int nb = 0; nb < NB_PER_WAVE; ++nb)
+        nx.bias_bits[nb] = load_bits(a.bias, min(nx.v0 + wn * 64 + nb * 32 + (lane & 31), a.V - 1));
+    }
+  } else if (k == 1) {
+    const int e = block_entry(nx.m, tid);
+    const bool ok = e >= 0 && e < a.n_blk && (tid >= MBLK || tid < nx.n_valid);
+    put_blocks(um, ok ? nx.code_bits : -1, a.nblk, tid);
+    put_mask_words(um, tid < BM ? um.maskf[tid] : 0.0f, tid, lane);
+  } else {
+    row_offsets(um, nx.n_valid, a.S, a.row_bytes, wave, lane, nx.a_off);
+  }
+}
+
+// Hand-over to the prefetched next unit: its lane data.
+template <typename T>
+__device__ __forceinline__ void take_next(const Args<T>& a, const Next& nx, Lanes& L, int wn, int lane) {
+#pragma unroll
+  for (int i = 0; i < A_LOADS; ++i) L.a_off[i] = nx.a_off[i];
+#pragma unroll
+  for (int nb = 0; nb < NB_PER_WAVE; ++nb) {
+    const int col = nx.v0 + wn * 64 + nb * 32 + (lane & 31);
+    L.bias[nb] = (a.bias != nullptr && col < a.V) ? bits_to_f32<T>(nx.bias_bits[nb]) : 0.0f;
+  }
+}
+
+// Fetch a unit's metadata in place and start its first two slabs (into stages buf,
+// buf ^ 1). On return slab 0 has landed and is visible, slab 1 is in flight and the
+// metadata is published.
+template <typename T>
+__device__ __forceinline__ void start_unit(Smem& sm, const Args<T>& a, UnitMeta& um, int m, int v0,
+                                           int n_valid, Lanes& L, int nk, int buf, int tid, int wave,
+                                           int lane, int wn) {
+  const int code = tid < MBLK + 2 ? block_code(a.list, a.n_blk, m, n_valid, tid) : -1;
+  put_blocks(um, code, a.nblk, tid);
+  if (tid == 0) um.mask_binary = 1;
+  const float mv = tid < BM ? a.rowmask[(int64_t)m * BM + tid] : 0.0f;
+  if (tid < BM) um.maskf[tid] = mv;
+  lds_barrier();
+  row_offsets(um, n_valid, a.S, a.row_bytes, wave, lane, L.a_off);
+  load_bias(a, v0, wn, lane, L.bias);
+  if (nk > 0) {
+    issue_slab(sm, a, L.a_off, n_valid, v0, 0, buf, wave, lane);
+    issue_slab(sm, a, L.a_off, n_valid, v0, 1, buf ^ 1, wave, lane);
+  }
+  put_mask_words(um, mv, tid, lane);
+  if (nk > 0) wait_loads_at_most(slab_loads(n_valid, wave));  // slab 0 landed, slab 1 in flight
+  lds_barrier();
+}
+
 // Mainloop + block epilogue of one unit (vocab tile v0), for a wave with JM blocks.
 // On entry slab 0 of the unit has landed in stage `buf` (and is visible) and slab 1 is
-// in flight or landed in the other stage. On exit the next unit's slab 0 (if any) has
-// landed and its slab 1 is in flight, and pv/pi hold this wave's blocks' results.
+// in flight or landed in the other stage. On exit, if nx.on, the next unit's slab 0
+// has landed and its slab 1 is in flight; pv/pi hold this wave's blocks' results.
 // Returns the stage of the next unit's slab 0.
 template <typename T, int JM>
-__device__ __forceinline__ int run_unit(Smem& sm, const Geo& g, int v0, int v0_next, int nk,
-                                        int buf, int btile, int wave, int lane, int wm, int wn) {
+__device__ __forceinline__ int run_unit(Smem& sm, const Args<T>& a, const UnitMeta& um,
+                                        const Lanes& L, int n_valid, int v0, int nk, int buf,
+                                        Next& nx, UnitMeta& um_next, int tid, int wave, int lane,
+                                        int wm, int wn) {
   constexpr int JA = JM > 0 ? JM : 1;
   const int l32 = lane & 31, h = lane >> 5;
   f32x16 acc[JA][NB_PER_WAVE];
 #pragma unroll
-  for (int nb = 0; nb < NB_PER_WAVE; ++nb) {
-    const float bc = sm.biasf[btile * BN + wn * 64 + nb * 32 + l32];
+  for (int nb = 0; nb < NB_PER_WAVE; ++nb)
 #pragma unroll
     for (int j = 0; j < JA; ++j)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) acc[j][nb][i] = bc;
-  }
+      for (int i = 0; i < 16; ++i) acc[j][nb][i] = L.bias[nb];
 
   for (int k = 0; k < nk; ++k) {
     const int cur = buf ^ (k & 1);
-    if (k >= g.nk_full) {  // tail / padding slab: clear W past D before use
-      zero_tail(sm, g.row_bytes, k, cur, wave, lane);
+    if (nx.on && k < 3) fetch_step(k, a, nx, um_next, tid, wave, lane, wn);
+    if (k >= a.nk_full) {  // tail / padding slab: clear W past D before use
+      zero_tail(sm, a.row_bytes, k, cur, wave, lane);
       lds_barrier();
     }
     if (JM > 0) {
@@ -497,9 +727,16 @@ __device__ __forceinline__ int run_unit(Smem& sm, const Geo& g, int v0, int v0_n
       }
     }
     drain_and_sync();
-    // Stage `cur` is free: refill it with the slab two ahead in the stream.
+    // Stage `cur` is free: refill it with the slab two ahead in the stream (this
+    // unit's, or the next unit's first two).
     const bool own = k + 2 < nk;
-    if (own || v0_next >= 0) issue_slab(sm, g, own ? v0 : v0_next, own ? k + 2 : k + 2 - nk, cur, wave, lane);
+    if (own || nx.on) {
+      uint32_t off[A_LOADS];
+#pragma unroll
+      for (int i = 0; i < A_LOADS; ++i) off[i] = own ? L.a_off[i] : nx.a_off[i];
+      issue_slab(sm, a, off, own ? n_valid : nx.n_valid, own ? v0 : nx.v0, own ? k + 2 : k + 2 - nk,
+                 cur, wave, lane);
+    }
   }
 
   // Block epilogue. 32x32 accumulator layout: lane holds column l32, and register
@@ -511,14 +748,14 @@ __device__ __forceinline__ int run_unit(Smem& sm, const Geo& g, int v0, int v0_n
   // precision the key keeps (the reference compares bf16-rounded logits, 2^-8). Keys of
   // x <= 0 are never positive-valued and decode to (0, row 0), the initial max. With a
   // 0/1 mask, bits(x) & ~31 is one AND with the row's mask word.
-  const int binary = sm.mask_binary;
-  const float* mrow = &sm.maskf[wm * 32 + 4 * h];
-  const int* wrow = &sm.maskw[wm * 32 + 4 * h];
+  const int binary = um.mask_binary;
+  const float* mrow = &um.maskf[wm * 32 + 4 * h];
+  const int* wrow = &um.maskw[wm * 32 + 4 * h];
   float* pvw = &sm.pv[wm][wn * 64 + l32];
   int* piw = &sm.pi[wm][wn * 64 + l32];
 #pragma unroll
   for (int j = 0; j < JM; ++j) {
-    const int s_blk = sm.blk_s[wm + WAVES_M * j];
+    const int s_blk = um.blk_s[wm + WAVES_M * j];
     int kmax[NB_PER_WAVE];
 #pragma unroll
     for (int nb = 0; nb < NB_PER_WAVE; ++nb) kmax[nb] = INT32_MIN;
@@ -566,13 +803,14 @@ __device__ __forceinline__ int run_unit(Smem& sm, const Geo& g, int v0, int v0_n
 // reps/argmax for complete segments, or the partial for a segment that continues into
 // the previous M-tile (slot 0) or the next one (slot 1).
 template <typename T>
-__device__ __forceinline__ void write_unit(Smem& sm, int m, int v0, int V, int n_valid, T* reps,
-                                           int32_t* argmax, float* reps_f32, float2* part) {
+__device__ __forceinline__ void write_unit(Smem& sm, const UnitMeta& um, int m, int v0, int V,
+                                           int n_valid, T* reps, int32_t* argmax, float* reps_f32,
+                                           float2* part) {
   const int tid = threadIdx.x;
   lds_barrier();  // every block's pv/pi are written
   if (tid < BN && v0 + tid < V) {
     const int v = v0 + tid;
-    const int b_prev = sm.blk_b[MBLK], b_next = sm.blk_b[MBLK + 1];
+    const int b_prev = um.blk_b[MBLK], b_next = um.blk_b[MBLK + 1];
     float pvr[MBLK];
     int pir[MBLK];
 #pragma unroll
@@ -589,9 +827,9 @@ __device__ __forceinline__ void write_unit(Smem& sm, int m, int v0, int V, int n
         bv = pvr[r];
         bi = pir[r];
       }
-      const int b = sm.blk_b[r];
-      if (r + 1 == n_valid || sm.blk_b[r + 1] != b) {  // the segment of batch row b ends
-        const bool cont_prev = b == sm.blk_b[0] && b == b_prev;
+      const int b = um.blk_b[r];
+      if (r + 1 == n_valid || um.blk_b[r + 1] != b) {  // the segment of batch row b ends
+        const bool cont_prev = b == um.blk_b[0] && b == b_prev;
         const bool cont_next = r + 1 == n_valid && b == b_next;
         if (cont_prev || cont_next) {
           part[((int64_t)m * 2 + (cont_prev ? 0 : 1)) * V + v] = make_float2(bv, __int_as_float(bi));
@@ -613,91 +851,76 @@ __device__ __forceinline__ void write_unit(Smem& sm, int m, int v0, int V, int n
 template <typename T>
 __global__ __launch_bounds__(NTHREADS, 1) void sparton_fwd_kernel(
     const T* __restrict__ H, const T* __restrict__ W, const T* __restrict__ bias,
-    const void* __restrict__ mask, int mask_dtype, T* __restrict__ reps,
-    int32_t* __restrict__ argmax, float* __restrict__ reps_f32, int S, int D, int V,
-    int n_vt, int P, int nblk, int n_mt_max, const int* __restrict__ meta,
-    const int* __restrict__ list, float2* __restrict__ part) {
+    const float* __restrict__ rowmask, T* __restrict__ reps, int32_t* __restrict__ argmax,
+    float* __restrict__ reps_f32, int S, int D, int V, int n_vt, int nblk,
+    const int* __restrict__ meta, const int* __restrict__ list, float2* __restrict__ part) {
   __shared__ Smem sm;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: keep it scalar
   const int wm = wave / WAVES_N, wn = wave % WAVES_N;
 
-  const int n_vg = (n_vt + P - 1) / P;
-  const int n_blk = __builtin_amdgcn_readfirstlane(meta[0]);
-  int m, vg;
-  if (!tile_of(blockIdx.x, (n_blk + MBLK - 1) / MBLK, n_vg, &m, &vg)) return;
-  const int vt_lo = vg * P, n_tiles = min(P, n_vt - vt_lo);
-  const int n_valid = min(MBLK, n_blk - m * MBLK);
-
-  // The tile's blocks, and the batch rows of the blocks just before and after it.
-  if (tid == 0) sm.mask_binary = 1;  // cleared below (after a barrier) by any other value
-  if (tid < MBLK + 2) {
-    const int e = tid < MBLK ? m * MBLK + tid : (tid == MBLK ? m * MBLK - 1 : m * MBLK + MBLK);
-    const bool ok = e >= 0 && e < n_blk && (tid >= MBLK || tid < n_valid);
-    const int code = ok ? list[e] : -1;
-    sm.blk_b[tid] = ok ? code / nblk : -1;
-    if (tid < MBLK) sm.blk_s[tid] = ok ? (code % nblk) * 32 : 0;
-  }
-  for (int i = tid; i < n_tiles * BN; i += NTHREADS) {
-    const int col = vt_lo * BN + i;
-    sm.biasf[i] = (bias != nullptr && col < V) ? to_f32(bias[col]) : 0.0f;
-  }
-  lds_barrier();
-
-  Geo g;
-  g.row_bytes = D * (int)sizeof(T);
-  g.H = (const char*)H;
-  g.W = (const char*)W;
+  Args<T> a;
+  a.H = (const char*)H;
+  a.W = (const char*)W;
+  a.bias = bias;
+  a.rowmask = rowmask;
+  a.list = list;
+  a.n_blk = __builtin_amdgcn_readfirstlane(meta[0]);
+  a.nblk = nblk;
+  a.S = S;
+  a.row_bytes = D * (int)sizeof(T);
   const int slab_elems = SLAB / (int)sizeof(T);
-  g.nk_full = D / slab_elems;
-  g.V = V;
-  g.n_valid = n_valid;
+  a.nk_full = D / slab_elems;
+  a.V = V;
   // At least two slabs per unit (a padding slab contributes zero); none when D == 0,
   // where x = bias * mask and nothing is loaded.
   const int nk = D == 0 ? 0 : max(2, (int)cdiv(D, slab_elems));
-#pragma unroll
-  for (int i = 0; i < A_LOADS; ++i) {
-    const int grp = i * NWAVES + wave;
-    const int row = grp * ROWS_PER_LOAD + (lane >> 3);  // row of the tile
-    const int r = min(row >> 5, n_valid - 1);            // its block (loads past n_valid are skipped)
-    const int s = min(sm.blk_s[r] + (row & 31), S - 1);  // positions past S: any valid row
-    g.a_off[i] = (uint32_t)(((int64_t)sm.blk_b[r] * S + s) * g.row_bytes) + lane_chunk(row, lane);
-  }
-  // Row mask of the tile (0 past S and past the last active block).
-  if (tid < BM) {
-    const int r = tid >> 5;
-    const int s = sm.blk_s[r] + (tid & 31);
-    const float mv = (r < n_valid && s < S) ? load_mask(mask, mask_dtype, (int64_t)sm.blk_b[r] * S + s) : 0.0f;
-    sm.maskf[tid] = mv;
-    sm.maskw[tid] = mv != 0.0f ? ~31 : 0;
-    if (__ballot(mv != 0.0f && mv != 1.0f) != 0 && lane == 0) sm.mask_binary = 0;
-  }
 
-  const int jm = n_valid <= wm ? 0 : min(4, (n_valid - wm + 1) / WAVES_M);
-  if (nk > 0) {
-    issue_slab(sm, g, vt_lo * BN, 0, 0, wave, lane);
-    issue_slab(sm, g, vt_lo * BN, 1, 1, wave, lane);
-    // Slab 0 must have landed everywhere; slab 1 stays in flight.
-    const int a_groups = n_valid * (32 / ROWS_PER_LOAD);
-    int n1 = B_LOADS;
-#pragma unroll
-    for (int i = 0; i < A_LOADS; ++i) n1 += (i * NWAVES + wave < a_groups) ? 1 : 0;
-    wait_loads_at_most(n1);
-  }
-  lds_barrier();  // also publishes maskf
+  const int n_mt = (a.n_blk + MBLK - 1) / MBLK;
+  const int n_units = n_mt * n_vt;
+  const int G = gridDim.x, w = blockIdx.x;
+  int u = unit_at(w, 0, G, n_units);
+  if (u < 0) return;
+  int m, vt;
+  unit_tile(u, n_mt, n_vt, &m, &vt);
+  int n_valid = min(MBLK, a.n_blk - m * MBLK);
+  Lanes L;
+  int par = 0, buf = 0;
+  start_unit(sm, a, sm.um[0], m, vt * BN, n_valid, L, nk, buf, tid, wave, lane, wn);
 
-  int buf = 0;
-  for (int t = 0; t < n_tiles; ++t) {
-    const int v0 = (vt_lo + t) * BN;
-    const int v0_next = t + 1 < n_tiles ? v0 + BN : -1;
-    switch (jm) {
-      case 0: buf = run_unit<T, 0>(sm, g, v0, v0_next, nk, buf, t, wave, lane, wm, wn); break;
-      case 1: buf = run_unit<T, 1>(sm, g, v0, v0_next, nk, buf, t, wave, lane, wm, wn); break;
-      case 2: buf = run_unit<T, 2>(sm, g, v0, v0_next, nk, buf, t, wave, lane, wm, wn); break;
-      case 3: buf = run_unit<T, 3>(sm, g, v0, v0_next, nk, buf, t, wave, lane, wm, wn); break;
-      default: buf = run_unit<T, 4>(sm, g, v0, v0_next, nk, buf, t, wave, lane, wm, wn); break;
+  for (int r = 1;; ++r) {
+    const int u_next = unit_at(w, r, G, n_units);
+    Next nx;
+    nx.on = false;
+    int vt_next = 0;
+    if (u_next >= 0) {
+      unit_tile(u_next, n_mt, n_vt, &nx.m, &vt_next);
+      nx.v0 = vt_next * BN;
+      nx.n_valid = min(MBLK, a.n_blk - nx.m * MBLK);
+      nx.on = nk >= 4;
     }
-    write_unit<T>(sm, m, v0, V, n_valid, reps, argmax, reps_f32, part);
+    const int v0 = vt * BN;
+    UnitMeta& um = sm.um[par];
+    UnitMeta& um_next = sm.um[par ^ 1];
+    const int jm = n_valid <= wm ? 0 : min(4, (n_valid - wm + 1) / WAVES_M);
+    switch (jm) {
+      case 0: buf = run_unit<T, 0>(sm, a, um, L, n_valid, v0, nk, buf, nx, um_next, tid, wave, lane, wm, wn); break;
+      case 1: buf = run_unit<T, 1>(sm, a, um, L, n_valid, v0, nk, buf, nx, um_next, tid, wave, lane, wm, wn); break;
+      case 2: buf = run_unit<T, 2>(sm, a, um, L, n_valid, v0, nk, buf, nx, um_next, tid, wave, lane, wm, wn); break;
+      case 3: buf = run_unit<T, 3>(sm, a, um, L, n_valid, v0, nk, buf, nx, um_next, tid, wave, lane, wm, wn); break;
+      default: buf = run_unit<T, 4>(sm, a, um, L, n_valid, v0, nk, buf, nx, um_next, tid, wave, lane, wm, wn); break;
+    }
+    write_unit<T>(sm, um, m, v0, V, n_valid, reps, argmax, reps_f32, part);
+    if (u_next < 0) break;
+    m = nx.m;
+    vt = vt_next;
+    n_valid = nx.n_valid;
+    par ^= 1;
+    if (nx.on) {
+      take_next(a, nx, L, wn, lane);
+    } else {
+      start_unit(sm, a, sm.um[par], m, vt * BN, n_valid, L, nk, buf, tid, wave, lane, wn);
+    }
   }
 }
 
@@ -749,18 +972,24 @@ __global__ __launch_bounds__(256) void fwd_fixup_kernel(int V, const int* __rest
   }
 }
 
-// Vocab tiles per workgroup: enough workgroups to keep every CU busy for several
-// rounds, as few as that allows (each workgroup pays its prologue once).
-// SPARTON_FWD_TILES_PER_GROUP (1..8) overrides the choice, for tests and tuning.
-static int tiles_per_group(int64_t n_mt, int64_t n_vt) {
-  if (const char* env = getenv("SPARTON_FWD_TILES_PER_GROUP")) {
-    const int p = atoi(env);
-    if (p >= 1 && p <= MAX_P) return p;
+// Persistent grid: one workgroup per CU (the kernel's LDS allows one per CU), or
+// fewer when there are fewer units. SPARTON_FWD_GRID overrides the workgroup count
+// (tests use it to give each workgroup many units).
+static int64_t persistent_grid(int64_t n_units_max) {
+  int64_t g = 0;
+  if (const char* env = getenv("SPARTON_FWD_GRID")) g = atoll(env);
+  if (g <= 0) {
+    int dev = 0, n_cu = 0;
+    if (hipGetDevice(&dev) == hipSuccess &&
+        hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
+        n_cu > 0) {
+      g = n_cu;
+    } else {
+      (void)hipGetLastError();  // clear the failed query; size for MI355X
+      g = 256;
+    }
   }
-  const int64_t target = 256 * 6;  // CUs x rounds
-  int P = 1;
-  while (P < MAX_P && cdiv(n_vt, 2 * P) * n_mt >= target) P *= 2;
-  return P;
+  return std::min<int64_t>(g, n_units_max);
 }
 
 template <typename T>
@@ -770,26 +999,28 @@ static int launch(const void* H, const void* W, const void* bias, const void* ma
   const int64_t nblk = cdiv(S, 32);
   const int64_t n_vt = cdiv(V, BN);
   const int64_t n_mt_max = cdiv(B * nblk, MBLK);
-  // The workgroup count is sized for rows about 60% full (the launch does not know the
-  // mask); it affects speed only.
-  const int P = tiles_per_group(cdiv(n_mt_max * 3, 5), n_vt);
-  const int64_t grid = n_mt_max * cdiv(n_vt, P);
-  if (grid > INT32_MAX) return SPARTON_EUNSUPPORTED;
+  // Unit numbers (and one round past them) must fit in int.
+  if (n_mt_max * n_vt > INT32_MAX / 2) return SPARTON_EUNSUPPORTED;
+  const int64_t grid = persistent_grid(n_mt_max * n_vt);
   if (B <= PLAN_FUSED_MAX && B * nblk <= PLAN_FUSED_MAX) {
     hipLaunchKernelGGL(fwd_plan_small_kernel, dim3(1), dim3(PLAN_THREADS), 0, stream, mask,
-                       mask_dtype, (int)B, (int)S, (int)nblk, w.count, w.first, w.list, w.meta);
+                       mask_dtype, (int)B, (int)S, (int)nblk, w.count, w.first, w.list, w.meta,
+                       w.rowmask);
   } else {
     hipLaunchKernelGGL(fwd_plan_rows_kernel, dim3((unsigned)cdiv(B, 4)), dim3(256), 0, stream,
                        mask, mask_dtype, (int)B, (int)S, (int)nblk, w.flag, w.count);
     hipLaunchKernelGGL(fwd_plan_list_kernel, dim3(1), dim3(PLAN_THREADS), 0, stream, (int)B,
                        (int)nblk, (const uint8_t*)w.flag, (const int*)w.count, w.first, w.list,
                        w.meta);
+    hipLaunchKernelGGL(fwd_plan_rowmask_kernel, dim3((unsigned)cdiv(n_mt_max * BM, 256)), dim3(256),
+                       0, stream, mask, mask_dtype, (int)S, (int)nblk, (const int*)w.meta,
+                       (const int*)w.list, w.rowmask);
   }
   if (grid > 0)  // S == 0: no blocks, the fixup writes every row
     hipLaunchKernelGGL(sparton_fwd_kernel<T>, dim3((unsigned)grid), dim3(NTHREADS), 0, stream,
-                       (const T*)H, (const T*)W, (const T*)bias, mask, mask_dtype, (T*)reps,
-                       argmax, reps_f32, (int)S, (int)D, (int)V, (int)n_vt, P, (int)nblk,
-                       (int)n_mt_max, (const int*)w.meta, (const int*)w.list, w.part);
+                       (const T*)H, (const T*)W, (const T*)bias, (const float*)w.rowmask, (T*)reps,
+                       argmax, reps_f32, (int)S, (int)D, (int)V, (int)n_vt, (int)nblk,
+                       (const int*)w.meta, (const int*)w.list, w.part);
   hipLaunchKernelGGL(fwd_fixup_kernel<T>, dim3((unsigned)cdiv(V, FIX_COLS), (unsigned)B), dim3(256), 0,
                      stream, (int)V, (const int*)w.count, (const int*)w.first,
                      (const float2*)w.part, (T*)reps, argmax, reps_f32);

@@ -82,12 +82,18 @@ CASES = [
 
 # Cases run again with several vocab tiles per workgroup (the unit stream then crosses
 # vocab tiles and chunks inside one workgroup, including a partial last group).
-MULTI_TILE_CASES = [
-    (("bf16", 3, 900, 64, 2100, True, "gaps"), 3),
-    (("fp32", 2, 40, 96, 1300, True, "frac"), 2),
-    (("fp16", 2, 300, 24, 1800, False, "bool"), 4),
-    (("bf16", 2, 256, 768, 4099, True, "holes"), 8),
-    (("fp16", 37, 40, 64, 700, True, "int64"), 3),
+# (case, grid): the persistent forward kernel run with `grid` workgroups, so each
+# walks many units. nk = K slabs per unit; nk >= 4 fetches the next unit's metadata
+# inside the K loop, nk < 4 hands over synchronously.
+PERSISTENT_CASES = [
+    (("bf16", 3, 900, 64, 2100, True, "gaps"), 1),      # nk 2, one workgroup for all units
+    (("fp32", 2, 40, 96, 1300, True, "frac"), 2),       # nk 3
+    (("fp16", 2, 300, 24, 1800, False, "bool"), 4),     # nk 2 (K tail)
+    (("bf16", 2, 256, 768, 4099, True, "holes"), 3),    # nk 12
+    (("fp16", 37, 40, 64, 700, True, "int64"), 9),
+    (("fp32", 3, 70, 132, 900, True, "frac"), 5),       # nk 5 (K tail), fractional mask
+    (("fp16", 5, 100, 200, 1500, False, "gaps"), 7),    # nk 4 (K tail)
+    (("bf16", 37, 40, 256, 700, True, "int64"), 13),    # nk 4, tiles spanning batch rows
 ]
 
 
@@ -129,10 +135,11 @@ def test_random_shapes(case, device):
     check_bwd_isolated(H, W, b, m, G, reps32, idx, dH, dW, db)
 
 
-@pytest.mark.parametrize("case,P", MULTI_TILE_CASES, ids=[f"{'-'.join(map(str, c))}-P{p}" for c, p in MULTI_TILE_CASES])
-def test_multi_tile_workgroups(case, P, device, monkeypatch):
-    say(f"random case {case} with {P} vocab tiles per workgroup")
-    monkeypatch.setenv("SPARTON_FWD_TILES_PER_GROUP", str(P))
+@pytest.mark.parametrize("case,grid", PERSISTENT_CASES,
+                         ids=[f"{'-'.join(map(str, c))}-G{g}" for c, g in PERSISTENT_CASES])
+def test_persistent_schedules(case, grid, device, monkeypatch):
+    say(f"random case {case} with {grid} forward workgroups")
+    monkeypatch.setenv("SPARTON_FWD_GRID", str(grid))
     H, W, b, m, G = make_case(*case)
     reps, idx, reps32, dH, dW, db = run_fwd_bwd(H, W, b, m, G, device)
     n, bad = check_fwd(H, W, b, m, reps, idx)
@@ -324,6 +331,37 @@ def test_edge_cases(device):
     r2, i2 = torch.ops.sparton.fused_sparton_fwd(H2, W2, None, m2)
     M, I, ref2 = oracle.fused_fwd_ref(H2.cpu(), W2.cpu(), None, m2.cpu())
     torch.testing.assert_close(r2.cpu().to(F64), ref2, **FWD_TOL)
+
+
+@pytest.mark.parametrize("dt,D", [("bf16", 24), ("fp16", 8), ("fp32", 12), ("bf16", 72)])
+def test_reads_stay_inside_rows(dt, D, device):
+    """Rows shorter than (or not a multiple of) one 128-byte K slab: the bytes right
+    after H and W are NaN, so a load past a row end -- which would poison a logit with
+    NaN * 0 -- shows up as a wrong max. The last position of each batch row is made
+    the argmax of many columns, so its row (the one next to the NaNs) must be used."""
+    say(f"NaN-fenced H and W, {dt} D={D}")
+    dtype = DTYPES[dt]
+    B, S, V = 3, 9, 300
+    g = torch.Generator().manual_seed(7)
+    H = torch.randn(B, S, D, generator=g)
+    H[:, -1] *= 4.0
+    W = (torch.randn(V, D, generator=g) * 0.3).to(dtype)
+    H = H.to(dtype)
+    b = (torch.randn(V, generator=g) * 0.1).to(dtype)
+    m = torch.ones(B, S, dtype=torch.long)
+    m[1, 5:] = 0
+    pad = 256
+    Hbuf = torch.full((B * S * D + pad,), float("nan"), dtype=dtype, device=device)
+    Wbuf = torch.full((V * D + pad,), float("nan"), dtype=dtype, device=device)
+    Hd = Hbuf[: B * S * D].view(B, S, D)
+    Wd = Wbuf[: V * D].view(V, D)
+    Hd.copy_(H)
+    Wd.copy_(W)
+    reps, idx = torch.ops.sparton.fused_sparton_fwd(Hd, Wd, b.to(device), m.to(device))
+    torch.cuda.synchronize()
+    assert torch.isnan(Hbuf[B * S * D:]).all() and torch.isnan(Wbuf[V * D:]).all()
+    n, bad = check_fwd(H, W, b, m, reps, idx)
+    say(f"  checked {n} entries, {bad} near-tie argmax differences")
 
 
 def test_autocast_policy(device):
