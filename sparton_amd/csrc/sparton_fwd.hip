@@ -62,8 +62,12 @@ constexpr int NB_PER_WAVE = BN / WAVES_N / 32;     // 2
 constexpr int SLAB = 128;            // bytes of K per row per pipeline stage
 constexpr int CHUNKS = SLAB / 16;    // 16-byte chunks per row slab (8)
 constexpr int ROWS_PER_LOAD = 64 / CHUNKS;          // rows one wave-wide load covers (8)
-constexpr int A_LOADS = BM / ROWS_PER_LOAD / NWAVES;  // wave-wide loads per slab for A (4)
-constexpr int B_LOADS = BN / ROWS_PER_LOAD / NWAVES;  // and for B (4)
+// Only the first LOAD_WAVES waves (one per SIMD) issue the slab copies: a wave waits
+// while the address unit takes its copies, and its SIMD partner (wave + 4, which issues
+// none) keeps the matrix pipe busy meanwhile.
+constexpr int LOAD_WAVES = 4;
+constexpr int A_LOADS = BM / ROWS_PER_LOAD / LOAD_WAVES;  // wave-wide copies per slab for A (8)
+constexpr int B_LOADS = BN / ROWS_PER_LOAD / LOAD_WAVES;  // and for B (8)
 constexpr int MAX_S = 16384;         // positions per batch row (512 blocks)
 constexpr int PLAN_THREADS = 1024;
 
@@ -447,7 +451,7 @@ __device__ __forceinline__ void row_offsets(const UnitMeta& um, int n_valid, int
                                             int wave, int lane, uint32_t* a_off) {
 #pragma unroll
   for (int i = 0; i < A_LOADS; ++i) {
-    const int grp = i * NWAVES + wave;
+    const int grp = i * LOAD_WAVES + (wave & (LOAD_WAVES - 1));
     const int row = grp * ROWS_PER_LOAD + (lane >> 3);
     const int r = min(row >> 5, n_valid - 1);
     const int s = min(um.blk_s[r] + (row & 31), S - 1);
@@ -488,8 +492,9 @@ template <> __device__ __forceinline__ float bits_to_f32<float>(uint32_t x) { re
 // ---- K stream ----
 
 // Issue the direct global -> LDS copies of K slab k of vocab tile v0 into stage buf.
-// Wave w, load i covers the 8-row group g = i * NWAVES + w (rows 8g..8g+7 of the
-// tile, in block g / 4); lane L lands at LDS chunk g*64 + L. A chunk past the row end
+// Loading wave w (< LOAD_WAVES), copy i covers the 8-row group g = i * LOAD_WAVES + w
+// (rows 8g..8g+7 of the tile, in block g / 4); lane L lands at LDS chunk g*64 + L.
+// Other waves issue nothing. A chunk past the row end
 // (tail or padding slabs) re-reads the row's first chunk -- valid, finite data inside
 // the row, so nothing outside H or W is read -- and its W copy is zeroed by zero_tail()
 // before use (a zero W times a finite H adds exactly 0). W rows past V re-read row V-1
@@ -497,12 +502,13 @@ template <> __device__ __forceinline__ float bits_to_f32<float>(uint32_t x) { re
 template <typename T>
 __device__ __forceinline__ void issue_slab(Smem& sm, const Args<T>& a, const uint32_t* a_off,
                                            int n_valid, int v0, int k, int buf, int wave, int lane) {
+  if (wave >= LOAD_WAVES) return;
   const uint32_t kb = (uint32_t)k * SLAB;
   const bool tail = k >= a.nk_full;
   const int a_groups = n_valid * (32 / ROWS_PER_LOAD);
 #pragma unroll
   for (int i = 0; i < A_LOADS; ++i) {
-    const int grp = i * NWAVES + wave;
+    const int grp = i * LOAD_WAVES + wave;
     const uint32_t c16 = lane_chunk(grp * ROWS_PER_LOAD + (lane >> 3), lane);
     // a_off includes c16: adding 0 - c16 (mod 2^32) lands on the row's first chunk.
     const uint32_t step = (!tail || kb + c16 < (uint32_t)a.row_bytes) ? kb : 0u - c16;
@@ -514,7 +520,7 @@ __device__ __forceinline__ void issue_slab(Smem& sm, const Args<T>& a, const uin
   const int b_last = a.V - 1 - v0;
 #pragma unroll
   for (int i = 0; i < B_LOADS; ++i) {
-    const int grp = i * NWAVES + wave;
+    const int grp = i * LOAD_WAVES + wave;
     const int row = grp * ROWS_PER_LOAD + (lane >> 3);
     const uint32_t c16 = lane_chunk(row, lane);
     const uint32_t step = (!tail || kb + c16 < (uint32_t)a.row_bytes) ? kb : 0u - c16;
@@ -525,10 +531,11 @@ __device__ __forceinline__ void issue_slab(Smem& sm, const Args<T>& a, const uin
 
 // Direct loads one slab issues from this wave.
 __device__ __forceinline__ int slab_loads(int n_valid, int wave) {
+  if (wave >= LOAD_WAVES) return 0;
   const int a_groups = n_valid * (32 / ROWS_PER_LOAD);
   int n = B_LOADS;
 #pragma unroll
-  for (int i = 0; i < A_LOADS; ++i) n += (i * NWAVES + wave < a_groups) ? 1 : 0;
+  for (int i = 0; i < A_LOADS; ++i) n += (i * LOAD_WAVES + wave < a_groups) ? 1 : 0;
   return n;
 }
 
@@ -537,7 +544,7 @@ __device__ __forceinline__ int slab_loads(int n_valid, int wave) {
 __device__ __forceinline__ void zero_tail(Smem& sm, int row_bytes, int k, int buf, int wave, int lane) {
   const uint32_t kb = (uint32_t)k * SLAB;
 #pragma unroll
-  for (int i = 0; i < B_LOADS; ++i) {
+  for (int i = 0; i < BN / ROWS_PER_LOAD / NWAVES; ++i) {
     const int grp = i * NWAVES + wave;
     if (kb + lane_chunk(grp * ROWS_PER_LOAD + (lane >> 3), lane) >= (uint32_t)row_bytes)
       sm.b[buf][grp * 64 + lane] = u32x4{0, 0, 0, 0};
@@ -560,22 +567,32 @@ __device__ __forceinline__ void lds_barrier() {
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
-// Wait until at most n (0..8, wave-uniform) direct loads of this wave are in flight.
-// s_waitcnt takes an immediate: simm16 = vmcnt[15:14,3:0] | lgkmcnt[11:8] | expcnt[6:4];
-// 0x0F70 | n is vmcnt(n) with lgkmcnt and expcnt at their no-wait maxima.
+// Wait until at most n (0..16, wave-uniform) direct loads of this wave are in flight.
+// s_waitcnt takes an immediate: simm16 = vmcnt[5:4] << 14 | lgkmcnt[11:8] | expcnt[6:4]
+// | vmcnt[3:0]; VMCNT(n) is vmcnt(n) with lgkmcnt and expcnt at their no-wait maxima.
+#define VMCNT(n) ((((n) >> 4) & 3) << 14 | 0x0F70 | ((n) & 15))
 __device__ __forceinline__ void wait_loads_at_most(int n) {
   switch (n) {
-    case 0: __builtin_amdgcn_s_waitcnt(0x0F70 | 0); break;
-    case 1: __builtin_amdgcn_s_waitcnt(0x0F70 | 1); break;
-    case 2: __builtin_amdgcn_s_waitcnt(0x0F70 | 2); break;
-    case 3: __builtin_amdgcn_s_waitcnt(0x0F70 | 3); break;
-    case 4: __builtin_amdgcn_s_waitcnt(0x0F70 | 4); break;
-    case 5: __builtin_amdgcn_s_waitcnt(0x0F70 | 5); break;
-    case 6: __builtin_amdgcn_s_waitcnt(0x0F70 | 6); break;
-    case 7: __builtin_amdgcn_s_waitcnt(0x0F70 | 7); break;
-    default: __builtin_amdgcn_s_waitcnt(0x0F70 | 8); break;
+    case 0: __builtin_amdgcn_s_waitcnt(VMCNT(0)); break;
+    case 1: __builtin_amdgcn_s_waitcnt(VMCNT(1)); break;
+    case 2: __builtin_amdgcn_s_waitcnt(VMCNT(2)); break;
+    case 3: __builtin_amdgcn_s_waitcnt(VMCNT(3)); break;
+    case 4: __builtin_amdgcn_s_waitcnt(VMCNT(4)); break;
+    case 5: __builtin_amdgcn_s_waitcnt(VMCNT(5)); break;
+    case 6: __builtin_amdgcn_s_waitcnt(VMCNT(6)); break;
+    case 7: __builtin_amdgcn_s_waitcnt(VMCNT(7)); break;
+    case 8: __builtin_amdgcn_s_waitcnt(VMCNT(8)); break;
+    case 9: __builtin_amdgcn_s_waitcnt(VMCNT(9)); break;
+    case 10: __builtin_amdgcn_s_waitcnt(VMCNT(10)); break;
+    case 11: __builtin_amdgcn_s_waitcnt(VMCNT(11)); break;
+    case 12: __builtin_amdgcn_s_waitcnt(VMCNT(12)); break;
+    case 13: __builtin_amdgcn_s_waitcnt(VMCNT(13)); break;
+    case 14: __builtin_amdgcn_s_waitcnt(VMCNT(14)); break;
+    case 15: __builtin_amdgcn_s_waitcnt(VMCNT(15)); break;
+    default: __builtin_amdgcn_s_waitcnt(VMCNT(16)); break;
   }
 }
+#undef VMCNT
 
 // ---- one unit ----
 
