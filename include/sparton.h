@@ -99,7 +99,8 @@ size_t sparton_bwd_workspace_bytes(int64_t B, int64_t S, int64_t D, int64_t V);
 /*
  * Backward: d_hidden, d_weight, d_bias from grad_reps [B,V] (`dtype`).
  * `reps` is the forward's reps in `reps_dtype` (enum sparton_dtype): the rounded
- * `dtype` output, as the reference saves it, or the fp32 `reps_f32` output.
+ * `dtype` output, as the reference saves it, or the fp32 `reps_f32` output (any other
+ * `reps_dtype` is SPARTON_EINVAL).
  * `grad_dtype` is SPARTON_F32 (the reference's fp32 gradients) or `dtype` (the
  * gradients rounded once to the parameters' dtype, as autograd would cast them).
  * Every element of each non-NULL output is written (no zero-fill needed); a NULL

@@ -9,12 +9,14 @@
 //   dW / dbias  (bwd_dw_kernel)   row v gathers H[b, I[b,v], :] for b ascending.
 //   dH          (count -> scan -> scatter -> bwd_dh_kernel)
 //       1. count:   per (b, wave chunk of CHW vocab ids), active entries per s,
-//                   stored as hist[b][s][chunk].
-//       2. scan:    per b, one exclusive scan of hist[b] in (s, chunk) order -> each
-//                   (b,s) segment start and each chunk's first slot inside it.
-//       3. scatter: per (b, chunk), write (v, g') to its slot. Entries are visited in
-//                   v order and ranked among equal s with ballots, so each segment
-//                   lists its vocab ids in ascending order (a stable counting sort).
+//                   stored as hist[b][chunk][s]; the active entries (v, g') are also
+//                   compacted, in v order, into the chunk's slice of the workspace.
+//       2. scan:    per b, the exclusive scan of hist[b] in (s, chunk) order -> each
+//                   (b,s) segment start and each chunk's first slot inside it (one
+//                   thread per s sums its chunks; a block scan over s gives the bases).
+//       3. scatter: per (b, chunk), write its compacted entries to their slots, ranked
+//                   among equal s with one ballot per bit of s, so each segment lists
+//                   its vocab ids in ascending order (a stable counting sort).
 //       4. dh:      one wave per (b,s) row sums g' * W[v,:] over its segment,
 //                   gathering several W rows per batch before accumulating.
 //   dW / dbias for B <= 128 (bwd_dw_staged_kernel): a workgroup stages g' and I of all
@@ -41,7 +43,7 @@ constexpr int MAX_NP = 16;         // D up to 16 * 256 per register pass
 
 struct Layout {
   int64_t nch;
-  size_t hist, seg_start, seg_cnt, list, total;  // hist: [B][S][nch] int32
+  size_t hist, seg_start, seg_cnt, list, comp, ccount, total;  // hist: [B][nch][S] int32
 };
 
 static Layout layout(int64_t B, int64_t S, int64_t V) {
@@ -53,6 +55,8 @@ static Layout layout(int64_t B, int64_t S, int64_t V) {
   L.seg_start = take((size_t)(B * S) * 4);
   L.seg_cnt = take((size_t)(B * S) * 4);
   L.list = take((size_t)(B * V) * 8);
+  L.comp = take((size_t)(B * L.nch * CHW) * 8);  // [B][nch][CHW] active (v, g') per chunk
+  L.ccount = take((size_t)(B * L.nch) * 4);      // [B][nch] their number
   L.total = off;
   return L;
 }
@@ -73,10 +77,11 @@ __device__ __forceinline__ void stage_mask(float* maskf, const void* mask, int m
 // [0, S) makes the entry inactive, so it can never turn into an out-of-bounds access.
 // g' = G * exp(-reps) (src/sparton/sparton_kernel.py:531) times mask[b, I], the torch
 // head's d x / d logits (training/model.py:60); 1 for a 0/1 mask.
-template <typename T>
-__device__ __forceinline__ bool entry(T g_raw, float r, int s, const float* maskf, int S,
+template <typename T, typename RT>
+__device__ __forceinline__ bool entry(T g_raw, RT r_raw, int s, const float* maskf, int S,
                                       float* g_out) {
   *g_out = 0.0f;
+  const float r = to_f32(r_raw);
   if (!(r > 0.0f) || s < 0 || s >= S) return false;
   const float g = to_f32(g_raw);
   if (g == 0.0f) return false;
@@ -87,33 +92,42 @@ __device__ __forceinline__ bool entry(T g_raw, float r, int s, const float* mask
 }
 
 // This wave's chunk of row b: round j, lane l holds entry v = base + j*64 + l, so every
-// load instruction reads consecutive elements; all 3 * ROUNDS loads are issued up front.
-template <typename T>
+// load instruction reads consecutive elements. All 3 * ROUNDS loads are issued up front
+// and unconditionally (ids past V re-read id V-1 and are marked inactive): no value is
+// converted or tested until every load is in flight, so they overlap instead of each
+// waiting for the previous one.
+template <typename T, typename RT>
 struct ChunkData {
   T g[ROUNDS];
-  float r[ROUNDS];
+  RT r[ROUNDS];
   int s[ROUNDS];
-  __device__ __forceinline__ void load(const T* grad, const void* reps, int rdt,
-                                       const int32_t* idx, int64_t row, int base, int V,
-                                       int lane) {
+  __device__ __forceinline__ void load(const T* grad, const RT* reps, const int32_t* idx,
+                                       int64_t row, int base, int V, int lane) {
 #pragma unroll
     for (int j = 0; j < ROUNDS; ++j) {
-      const int v = base + j * 64 + lane;
-      const bool in = v < V;
-      const int64_t o = row + (in ? v : 0);
-      g[j] = in ? grad[o] : from_f32<T>(0.0f);
-      r[j] = in ? load_float(reps, rdt, o) : 0.0f;
-      s[j] = in ? idx[o] : -1;
+      const int64_t o = row + min(base + j * 64 + lane, V - 1);
+      g[j] = grad[o];
+      r[j] = reps[o];
+      s[j] = idx[o];
     }
+  }
+  // Entry j of this lane (v = base + j*64 + lane): active, with coefficient *g.
+  __device__ __forceinline__ bool get(int j, int base, int V, int lane, const float* maskf,
+                                      int S, float* gout) const {
+    if (base + j * 64 + lane >= V) {
+      *gout = 0.0f;
+      return false;
+    }
+    return entry(g[j], r[j], s[j], maskf, S, gout);
   }
 };
 
 // ---- 1. count ----------------------------------------------------------------
-template <typename T>
+template <typename T, typename RT>
 __global__ __launch_bounds__(256) void bwd_count_kernel(
-    const T* __restrict__ grad, const void* __restrict__ reps, int rdt,
-    const int32_t* __restrict__ idx, const void* __restrict__ mask, int mdt, int S, int V,
-    int nch, int* __restrict__ hist) {
+    const T* __restrict__ grad, const RT* __restrict__ reps, const int32_t* __restrict__ idx,
+    const void* __restrict__ mask, int mdt, int S, int V, int nch, int* __restrict__ hist,
+    int2* __restrict__ comp, int* __restrict__ ccount) {
   float* maskf = (float*)sparton_bwd_smem;
   const int wpb = blockDim.x >> 6, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   int* h = (int*)(maskf + S) + wave * S;
@@ -122,27 +136,39 @@ __global__ __launch_bounds__(256) void bwd_count_kernel(
   for (int s = lane; s < S; s += 64) h[s] = 0;
   __syncthreads();
   if (c < nch) {
-    ChunkData<T> d;
-    d.load(grad, reps, rdt, idx, (int64_t)b * V, c * CHW, V, lane);
+    ChunkData<T, RT> d;
+    d.load(grad, reps, idx, (int64_t)b * V, c * CHW, V, lane);
+    // Active entries are also compacted, in v order, into the chunk's slice of comp.
+    int2* cb = comp + ((int64_t)b * nch + c) * CHW;
+    const uint64_t lt = (1ull << lane) - 1ull;
+    int n = 0;
 #pragma unroll
     for (int j = 0; j < ROUNDS; ++j) {
       float g;
-      if (entry(d.g[j], d.r[j], d.s[j], maskf, S, &g)) atomicAdd(&h[d.s[j]], 1);
+      const bool act = d.get(j, c * CHW, V, lane, maskf, S, &g);
+      const uint64_t am = __ballot(act);
+      if (act) {
+        atomicAdd(&h[d.s[j]], 1);
+        cb[n + __popcll(am & lt)] = make_int2(c * CHW + j * 64 + lane, __float_as_int(g));
+      }
+      n += __popcll(am);
     }
+    if (lane == 0) ccount[(int64_t)b * nch + c] = n;
   }
   __syncthreads();
   if (c < nch) {
-    int* out = hist + (int64_t)b * S * nch + c;
-    for (int s = lane; s < S; s += 64) out[(int64_t)s * nch] = h[s];
+    int* out = hist + ((int64_t)b * nch + c) * S;
+    for (int s = lane; s < S; s += 64) out[s] = h[s];
   }
 }
 
 // ---- 2. scan -----------------------------------------------------------------
 constexpr int SCAN_THREADS = 1024;
-constexpr int SCAN_ITEMS = 4;  // consecutive elements per thread per tile
+constexpr int SCAN_BATCH = 8;  // chunk counts loaded together
 
-// One workgroup per batch row: exclusive scan of hist[b] (S * nch ints, (s, chunk)
-// order) in place, in tiles of SCAN_THREADS * SCAN_ITEMS; then the segment of each s.
+// One workgroup per batch row, threads over s: thread s sums its chunks' counts
+// hist[b][c][s] (coalesced across threads), a block scan over s gives the segment
+// starts, and a second pass rewrites each count as its chunk's first slot.
 __global__ __launch_bounds__(SCAN_THREADS) void bwd_scan_kernel(int* __restrict__ hist,
                                                                 int* __restrict__ seg_start,
                                                                 int* __restrict__ seg_cnt, int S,
@@ -151,19 +177,22 @@ __global__ __launch_bounds__(SCAN_THREADS) void bwd_scan_kernel(int* __restrict_
   __shared__ int carry;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t b = blockIdx.x;
-  const int64_t n = (int64_t)S * nch;
-  int* hb = hist + b * n;
+  int* hb = hist + b * nch * S;
   if (tid == 0) carry = 0;
   __syncthreads();
-  for (int64_t t0 = 0; t0 < n; t0 += SCAN_THREADS * SCAN_ITEMS) {
-    const int64_t e0 = t0 + (int64_t)tid * SCAN_ITEMS;
-    int x[SCAN_ITEMS], sum = 0;
+  for (int s0 = 0; s0 < S; s0 += blockDim.x) {
+    const int s = s0 + tid;
+    const bool in = s < S;
+    int tot = 0;
+    for (int c0 = 0; c0 < nch; c0 += SCAN_BATCH) {
+      int x[SCAN_BATCH];
 #pragma unroll
-    for (int i = 0; i < SCAN_ITEMS; ++i) {
-      x[i] = e0 + i < n ? hb[e0 + i] : 0;
-      sum += x[i];
+      for (int i = 0; i < SCAN_BATCH; ++i)
+        x[i] = (in && c0 + i < nch) ? hb[(int64_t)(c0 + i) * S + s] : 0;
+#pragma unroll
+      for (int i = 0; i < SCAN_BATCH; ++i) tot += x[i];
     }
-    int incl = sum;  // inclusive scan of the per-thread sums: wave, then across waves
+    int incl = tot;  // inclusive scan over s: within the wave, then across waves
 #pragma unroll
     for (int d = 1; d < 64; d <<= 1) {
       const int y = __shfl_up(incl, d);
@@ -171,64 +200,65 @@ __global__ __launch_bounds__(SCAN_THREADS) void bwd_scan_kernel(int* __restrict_
     }
     if (lane == 63) wsum[wave] = incl;
     __syncthreads();
-    int run = carry + incl - sum;
+    int run = carry + incl - tot;
     for (int w = 0; w < wave; ++w) run += wsum[w];
+    if (in) {
+      seg_start[b * S + s] = run;
+      seg_cnt[b * S + s] = tot;
+    }
+    for (int c0 = 0; c0 < nch; c0 += SCAN_BATCH) {
+      int x[SCAN_BATCH];
 #pragma unroll
-    for (int i = 0; i < SCAN_ITEMS; ++i) {
-      if (e0 + i < n) hb[e0 + i] = run;
-      run += x[i];
+      for (int i = 0; i < SCAN_BATCH; ++i)
+        x[i] = (in && c0 + i < nch) ? hb[(int64_t)(c0 + i) * S + s] : 0;
+#pragma unroll
+      for (int i = 0; i < SCAN_BATCH; ++i) {
+        if (in && c0 + i < nch) hb[(int64_t)(c0 + i) * S + s] = run;
+        run += x[i];
+      }
     }
     __syncthreads();
-    if (tid == SCAN_THREADS - 1) carry = run;
+    if (tid == (int)blockDim.x - 1) carry = run;
     __syncthreads();
-  }
-  const int total = carry;
-  for (int s = tid; s < S; s += SCAN_THREADS) {
-    const int st = hb[(int64_t)s * nch];
-    const int en = s + 1 < S ? hb[(int64_t)(s + 1) * nch] : total;
-    seg_start[b * S + s] = st;
-    seg_cnt[b * S + s] = en - st;
   }
 }
 
 // ---- 3. scatter ----------------------------------------------------------------
-template <typename T>
+// One wave per chunk: its compacted entries (in v order) are ranked among equal s and
+// written to their segments. Lanes with equal s are found with one ballot per bit of
+// s: `same` keeps the lanes that agree with this lane on every bit. An entry's slot is
+// the cursor of its s plus the lower lanes of its group; all lanes read the cursor,
+// then each group's lowest lane advances it (one wave's LDS accesses complete in
+// program order), so each segment lists its vocab ids in ascending order.
 __global__ __launch_bounds__(256) void bwd_scatter_kernel(
-    const T* __restrict__ grad, const void* __restrict__ reps, int rdt,
-    const int32_t* __restrict__ idx, const void* __restrict__ mask, int mdt, int S, int V,
-    int nch, const int* __restrict__ hist_base, int2* __restrict__ list) {
-  float* maskf = (float*)sparton_bwd_smem;
+    const int32_t* __restrict__ idx, int S, int V, int nch, const int* __restrict__ hist_base,
+    const int2* __restrict__ comp, const int* __restrict__ ccount, int2* __restrict__ list) {
+  int* cur = (int*)sparton_bwd_smem + (threadIdx.x >> 6) * S;
   const int wpb = blockDim.x >> 6, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  int* cur = (int*)(maskf + S) + wave * S;
   const int b = blockIdx.y, c = blockIdx.x * wpb + wave;
-  stage_mask(maskf, mask, mdt, b, S);
-  if (c < nch) {
-    const int* in = hist_base + (int64_t)b * S * nch + c;
-    for (int s = lane; s < S; s += 64) cur[s] = in[(int64_t)s * nch];
-  }
-  __syncthreads();
-  if (c >= nch) return;
-  ChunkData<T> d;
-  d.load(grad, reps, rdt, idx, (int64_t)b * V, c * CHW, V, lane);
+  if (c >= nch) return;  // no workgroup barrier below: waves are independent
+  const int* in = hist_base + ((int64_t)b * nch + c) * S;
+  for (int s = lane; s < S; s += 64) cur[s] = in[s];
+  const int n = ccount[(int64_t)b * nch + c];
+  const int2* cb = comp + ((int64_t)b * nch + c) * CHW;
   int2* lb = list + (int64_t)b * V;
+  const int32_t* ib = idx + (int64_t)b * V;
   const uint64_t lt = (1ull << lane) - 1ull;
-#pragma unroll
-  for (int j = 0; j < ROUNDS; ++j) {
-    float g;
-    const bool act = entry(d.g[j], d.r[j], d.s[j], maskf, S, &g);
-    const int s = d.s[j];
-    const int v = c * CHW + j * 64 + lane;
-    uint64_t pending = __ballot(act);
-    while (pending) {
-      const int leader = __ffsll((unsigned long long)pending) - 1;
-      const int ls = __builtin_amdgcn_readlane(s, leader);
-      const bool mine = act && s == ls;
-      const uint64_t grp = __ballot(mine);
-      const int base = cur[ls];
-      if (mine) lb[base + __popcll(grp & lt)] = make_int2(v, __float_as_int(g));
-      if (lane == leader) cur[ls] = base + __popcll(grp);
-      pending &= ~grp;
+  const int sbits = S > 1 ? 32 - __builtin_clz((unsigned)(S - 1)) : 0;
+  for (int i0 = 0; i0 < n; i0 += 64) {
+    const bool act = i0 + lane < n;
+    const int2 e = cb[act ? i0 + lane : 0];
+    const int s = act ? ib[e.x] : 0;
+    const uint64_t act_mask = __ballot(act);
+    uint64_t same = act_mask;
+    for (int k = 0; k < sbits; ++k) {
+      const bool bit = ((s >> k) & 1) != 0;
+      const uint64_t ones = __ballot(bit);
+      same &= bit ? ones : ~ones;
     }
+    const int base = act ? cur[s] : 0;
+    if (act) lb[base + __popcll(same & lt)] = e;
+    if (act && (same & lt) == 0) cur[s] = base + __popcll(same);
   }
 }
 
@@ -322,12 +352,69 @@ __global__ __launch_bounds__(256) void bwd_dh_kernel(
   }
 }
 
+// Mask values at N offsets: every load issued before any is converted (one round trip).
+template <typename M, int N>
+__device__ __forceinline__ void mask_vals(const void* mask, const int64_t* off, float* out) {
+  M raw[N];
+#pragma unroll
+  for (int i = 0; i < N; ++i) raw[i] = ((const M*)mask)[off[i]];
+#pragma unroll
+  for (int i = 0; i < N; ++i) out[i] = (float)raw[i];
+}
+template <int N>
+__device__ __forceinline__ void load_mask_n(const void* mask, int mdt, const int64_t* off,
+                                            float* out) {
+  switch (mdt) {  // uniform
+    case SPARTON_MASK_I64: mask_vals<int64_t, N>(mask, off, out); break;
+    case SPARTON_MASK_I32: mask_vals<int32_t, N>(mask, off, out); break;
+    case SPARTON_MASK_U8: mask_vals<uint8_t, N>(mask, off, out); break;
+    case SPARTON_MASK_F32: mask_vals<float, N>(mask, off, out); break;
+    case SPARTON_MASK_BF16: mask_vals<bf16, N>(mask, off, out); break;
+    default: mask_vals<f16, N>(mask, off, out); break;
+  }
+}
+
+// Entries (b_i, v) for N batch rows (b_i >= B or v >= V: inactive): g' (0 if inactive) and
+// s. Three raw loads per row, issued together; then the mask of the candidates, issued
+// together; then the coefficients. Inactive entries get s = 0.
+template <typename T, typename RT, int N>
+__device__ __forceinline__ void entries_n(const T* grad, const RT* reps, const int32_t* idx,
+                                          const void* mask, int mdt, const int* bs, int v, int B,
+                                          int S, int V, float* g, int* s) {
+  T gr[N];
+  RT rr[N];
+  int ss[N];
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    const int64_t o = (int64_t)min(bs[i], B - 1) * V + min(v, V - 1);
+    gr[i] = grad[o];
+    rr[i] = reps[o];
+    ss[i] = idx[o];
+  }
+  bool cand[N];
+  int64_t moff[N];
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    cand[i] = bs[i] < B && v < V && to_f32(rr[i]) > 0.0f && ss[i] >= 0 && ss[i] < S &&
+              to_f32(gr[i]) != 0.0f;
+    moff[i] = cand[i] ? (int64_t)bs[i] * S + ss[i] : 0;
+  }
+  float mv[N];
+  load_mask_n<N>(mask, mdt, moff, mv);
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    const bool act = cand[i] && mv[i] != 0.0f;
+    g[i] = act ? to_f32(gr[i]) * expf(-to_f32(rr[i])) * mv[i] : 0.0f;
+    s[i] = act ? ss[i] : 0;
+  }
+}
+
 // ---- 5. dW and dbias -------------------------------------------------------------
 // One wave per vocab row v: lanes hold batch rows b (64 per pass), a ballot lists the
 // active ones, and their H rows are gathered in ascending b, two at a time.
-template <typename T, typename O, int NP>
+template <typename T, typename O, int NP, typename RT>
 __global__ __launch_bounds__(256) void bwd_dw_kernel(
-    const T* __restrict__ grad, const void* __restrict__ reps, int rdt,
+    const T* __restrict__ grad, const RT* __restrict__ reps,
     const int32_t* __restrict__ idx, const void* __restrict__ mask, int mdt,
     const T* __restrict__ H, O* __restrict__ dW, O* __restrict__ dbias, int B, int S, int D,
     int V) {
@@ -342,25 +429,10 @@ __global__ __launch_bounds__(256) void bwd_dw_kernel(
     float bsum = 0.0f;
     for (int b0 = 0; b0 < B; b0 += 64) {
       const int bb = b0 + lane;
-      float g = 0.0f;
-      int s = 0;
-      bool act = false;
-      if (bb < B) {
-        const int64_t o = (int64_t)bb * V + v;
-        const float r = load_float(reps, rdt, o);
-        s = idx[o];
-        if (r > 0.0f && s >= 0 && s < S) {
-          const float gr = to_f32(grad[o]);
-          if (gr != 0.0f) {
-            const float m = load_mask(mask, mdt, (int64_t)bb * S + s);
-            if (m != 0.0f) {
-              act = true;
-              g = gr * expf(-r) * m;
-            }
-          }
-        }
-      }
-      uint64_t pending = __ballot(act);
+      float g;
+      int s;
+      entries_n<T, RT, 1>(grad, reps, idx, mask, mdt, &bb, v, B, S, V, &g, &s);
+      uint64_t pending = __ballot(g != 0.0f);
       while (pending) {
         const int l0 = __ffsll((unsigned long long)pending) - 1;
         pending &= pending - 1;
@@ -414,9 +486,9 @@ constexpr int DW_STAGE_B = 128;
 // a time: lanes scan the batch rows, a ballot lists the active ones, and their H rows
 // are gathered up to U at a time in ascending b and accumulated.
 constexpr int DW_WAVES = 16;
-template <typename T, typename O, int NP>
+template <typename T, typename O, int NP, typename RT>
 __global__ __launch_bounds__(64 * DW_WAVES) void bwd_dw_staged_kernel(
-    const T* __restrict__ grad, const void* __restrict__ reps, int rdt,
+    const T* __restrict__ grad, const RT* __restrict__ reps,
     const int32_t* __restrict__ idx, const void* __restrict__ mask, int mdt,
     const T* __restrict__ H, O* __restrict__ dW, O* __restrict__ dbias, int B, int S, int D,
     int V) {
@@ -426,26 +498,19 @@ __global__ __launch_bounds__(64 * DW_WAVES) void bwd_dw_staged_kernel(
   __shared__ uint16_t sl[64 * LD];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int v0 = blockIdx.x * 64;
-  for (int b = wave; b < B; b += DW_WAVES) {
-    const int v = v0 + lane;
-    float g = 0.0f;
-    int s = 0;
-    if (v < V) {
-      const int64_t o = (int64_t)b * V + v;
-      const float r = load_float(reps, rdt, o);
-      s = idx[o];
-      if (r > 0.0f && s >= 0 && s < S) {
-        const float gr = to_f32(grad[o]);
-        if (gr != 0.0f) {
-          const float m = load_mask(mask, mdt, (int64_t)b * S + s);
-          if (m != 0.0f) g = gr * expf(-r) * m;
-        }
-      } else {
-        s = 0;
+  // Batch rows b = wave + 16 i, two per batch (their loads in flight together).
+  for (int i0 = 0; wave + i0 * DW_WAVES < B; i0 += 2) {
+    const int bs[2] = {wave + i0 * DW_WAVES, wave + (i0 + 1) * DW_WAVES};
+    float g[2];
+    int s[2];
+    entries_n<T, RT, 2>(grad, reps, idx, mask, mdt, bs, v0 + lane, B, S, V, g, s);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      if (bs[i] < B) {
+        gl[lane * LD + bs[i]] = g[i];
+        sl[lane * LD + bs[i]] = (uint16_t)s[i];
       }
     }
-    gl[lane * LD + b] = g;
-    sl[lane * LD + b] = (uint16_t)s;
   }
   __syncthreads();
   const int dend = max(D, 1);  // one pass even when D == 0, for dbias
@@ -512,8 +577,8 @@ static int passes_for(int64_t D) {
   return (int)std::min<int64_t>(MAX_NP, std::max<int64_t>(1, cdiv(D, 256)));
 }
 
-template <typename T, typename O, int NP>
-static void launch_rows(const T* g, const void* r, int rdt, const int32_t* idx, const void* mask,
+template <typename T, typename O, int NP, typename RT>
+static void launch_rows(const T* g, const RT* r, const int32_t* idx, const void* mask,
                         int mdt, const T* H, const T* W, O* dH, O* dW, O* dbias, void* ws,
                         int64_t B, int64_t S, int64_t D, int64_t V, hipStream_t st) {
   if (dH != nullptr && B * S > 0 && D > 0) {
@@ -522,28 +587,32 @@ static void launch_rows(const T* g, const void* r, int rdt, const int32_t* idx, 
     int* seg_start = (int*)((char*)ws + L.seg_start);
     int* seg_cnt = (int*)((char*)ws + L.seg_cnt);
     int2* list = (int2*)((char*)ws + L.list);
+    int2* comp = (int2*)((char*)ws + L.comp);
+    int* ccount = (int*)((char*)ws + L.ccount);
     const int wpb = waves_for(S);
     const dim3 cgrid((unsigned)cdiv(L.nch, wpb), (unsigned)B);
     const size_t cl = (size_t)S * 4 * (1 + wpb);
     if (L.nch > 0)
-      hipLaunchKernelGGL(bwd_count_kernel<T>, cgrid, dim3(64 * wpb), cl, st, g, r, rdt, idx,
-                         mask, mdt, (int)S, (int)V, (int)L.nch, hist);
-    hipLaunchKernelGGL(bwd_scan_kernel, dim3((unsigned)B), dim3(SCAN_THREADS), 0, st, hist,
+      hipLaunchKernelGGL((bwd_count_kernel<T, RT>), cgrid, dim3(64 * wpb), cl, st, g, r, idx,
+                         mask, mdt, (int)S, (int)V, (int)L.nch, hist, comp, ccount);
+    hipLaunchKernelGGL(bwd_scan_kernel, dim3((unsigned)B),
+                       dim3((unsigned)std::min<int64_t>(SCAN_THREADS, round_up(S, 64))), 0, st, hist,
                        seg_start, seg_cnt, (int)S, (int)L.nch);
     if (L.nch > 0)
-      hipLaunchKernelGGL(bwd_scatter_kernel<T>, cgrid, dim3(64 * wpb), cl, st, g, r, rdt, idx,
-                         mask, mdt, (int)S, (int)V, (int)L.nch, (const int*)hist, list);
+      hipLaunchKernelGGL(bwd_scatter_kernel, cgrid, dim3(64 * wpb), (size_t)S * 4 * wpb, st, idx,
+                         (int)S, (int)V, (int)L.nch, (const int*)hist, (const int2*)comp,
+                         (const int*)ccount, list);
     hipLaunchKernelGGL((bwd_dh_kernel<T, O, NP>), dim3((unsigned)cdiv(B * S, 4)), dim3(256), 0,
                        st, W, (const int2*)list, (const int*)seg_start, (const int*)seg_cnt, dH,
                        (int)B, (int)S, (int)D, (int)V);
   }
   if ((dW != nullptr || dbias != nullptr) && V > 0) {
     if (B <= DW_STAGE_B)
-      hipLaunchKernelGGL((bwd_dw_staged_kernel<T, O, NP>), dim3((unsigned)cdiv(V, 64)), dim3(64 * DW_WAVES), 0,
-                         st, g, r, rdt, idx, mask, mdt, H, dW, dbias, (int)B, (int)S, (int)D, (int)V);
+      hipLaunchKernelGGL((bwd_dw_staged_kernel<T, O, NP, RT>), dim3((unsigned)cdiv(V, 64)), dim3(64 * DW_WAVES), 0,
+                         st, g, r, idx, mask, mdt, H, dW, dbias, (int)B, (int)S, (int)D, (int)V);
     else
-      hipLaunchKernelGGL((bwd_dw_kernel<T, O, NP>), dim3((unsigned)cdiv(V, 4)), dim3(256), 0, st,
-                         g, r, rdt, idx, mask, mdt, H, dW, dbias, (int)B, (int)S, (int)D, (int)V);
+      hipLaunchKernelGGL((bwd_dw_kernel<T, O, NP, RT>), dim3((unsigned)cdiv(V, 4)), dim3(256), 0, st,
+                         g, r, idx, mask, mdt, H, dW, dbias, (int)B, (int)S, (int)D, (int)V);
   }
 }
 
@@ -554,9 +623,12 @@ static int launch(const void* grad, const void* r, int rdt, const int32_t* idx, 
   const T* g = (const T*)grad;
   const T* h = (const T*)H;
   const T* w = (const T*)W;
-#define SPARTON_ROWS(NP)                                                                      \
-  launch_rows<T, O, NP>(g, r, rdt, idx, mask, mdt, h, w, (O*)dH, (O*)dW, (O*)dbias, ws, B, S, \
-                        D, V, st)
+#define SPARTON_ROWS(NP)                                                                        \
+  (rdt == SPARTON_F32                                                                           \
+       ? launch_rows<T, O, NP, float>(g, (const float*)r, idx, mask, mdt, h, w, (O*)dH, (O*)dW, \
+                                      (O*)dbias, ws, B, S, D, V, st)                            \
+       : launch_rows<T, O, NP, T>(g, (const T*)r, idx, mask, mdt, h, w, (O*)dH, (O*)dW,         \
+                                  (O*)dbias, ws, B, S, D, V, st))
   switch (passes_for(D)) {
     case 1: SPARTON_ROWS(1); break;
     case 2: SPARTON_ROWS(2); break;
@@ -590,7 +662,7 @@ extern "C" __attribute__((visibility("default"))) int sparton_bwd(
     int64_t B, int64_t S, int64_t D, int64_t V, int dtype, void* stream) {
   if (B < 0 || S < 0 || D < 0 || V < 0) return SPARTON_EINVAL;
   if (dtype < SPARTON_F32 || dtype > SPARTON_F16) return SPARTON_EINVAL;
-  if (reps_dtype < SPARTON_F32 || reps_dtype > SPARTON_F16) return SPARTON_EINVAL;
+  if (reps_dtype != SPARTON_F32 && reps_dtype != dtype) return SPARTON_EINVAL;
   if (grad_dtype != SPARTON_F32 && grad_dtype != dtype) return SPARTON_EINVAL;
   if (mask_dtype < SPARTON_MASK_I64 || mask_dtype > SPARTON_MASK_F16) return SPARTON_EINVAL;
   if (B * V > 0 && (grad_reps == nullptr || reps == nullptr || argmax == nullptr || mask == nullptr))

@@ -82,6 +82,7 @@ def test_fwd_argument_validation(kw, code):
 
 @pytest.mark.parametrize("kw,code", [
     (dict(S=-2), -1), (dict(dtype=-1), -1), (dict(reps_dtype=3), -1), (dict(grad_dtype=2), -1),
+    (dict(reps_dtype=2), -1),  # reps must be fp32 or the parameters' dtype (bf16 here)
     (dict(grad=None), -1), (dict(dH=P + 4, grad_dtype=1, ws=P, ws_bytes=1 << 30), -2),
     (dict(dW=P + 8, grad_dtype=0, ws=P, ws_bytes=1 << 30), -2),
     (dict(weight=None), -1),
