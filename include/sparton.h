@@ -89,6 +89,19 @@ int sparton_fwd(const void* hidden, const void* weight, const void* bias,
                 int dtype, void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * Profiling variant of sparton_fwd: the same work and results; *main_ms receives the
+ * device time of the main (MFMA) kernel alone, from HIP events recorded on `stream`
+ * just before and after its launch (summed over the row chunks of very large batches).
+ * Blocks the host until that kernel has finished. No counterpart in the reference: it
+ * serves measurement (the kernel's roofline), not the operator path.
+ */
+int sparton_fwd_profile(const void* hidden, const void* weight, const void* bias,
+                        const void* mask, int mask_dtype, void* reps, int32_t* argmax,
+                        float* reps_f32, int64_t B, int64_t S, int64_t D, int64_t V,
+                        int dtype, void* workspace, size_t workspace_bytes, void* stream,
+                        float* main_ms);
+
+/*
  * Bytes of device scratch sparton_bwd needs for these sizes (256-byte aligned
  * sections: per-chunk histograms, segment offsets and the bucketed entry list).
  * No counterpart in the reference: its backward needs no scratch because it

@@ -352,28 +352,6 @@ __global__ __launch_bounds__(256) void bwd_dh_kernel(
   }
 }
 
-// Mask values at N offsets: every load issued before any is converted (one round trip).
-template <typename M, int N>
-__device__ __forceinline__ void mask_vals(const void* mask, const int64_t* off, float* out) {
-  M raw[N];
-#pragma unroll
-  for (int i = 0; i < N; ++i) raw[i] = ((const M*)mask)[off[i]];
-#pragma unroll
-  for (int i = 0; i < N; ++i) out[i] = (float)raw[i];
-}
-template <int N>
-__device__ __forceinline__ void load_mask_n(const void* mask, int mdt, const int64_t* off,
-                                            float* out) {
-  switch (mdt) {  // uniform
-    case SPARTON_MASK_I64: mask_vals<int64_t, N>(mask, off, out); break;
-    case SPARTON_MASK_I32: mask_vals<int32_t, N>(mask, off, out); break;
-    case SPARTON_MASK_U8: mask_vals<uint8_t, N>(mask, off, out); break;
-    case SPARTON_MASK_F32: mask_vals<float, N>(mask, off, out); break;
-    case SPARTON_MASK_BF16: mask_vals<bf16, N>(mask, off, out); break;
-    default: mask_vals<f16, N>(mask, off, out); break;
-  }
-}
-
 // Entries (b_i, v) for N batch rows (b_i >= B or v >= V: inactive): g' (0 if inactive) and
 // s. Three raw loads per row, issued together; then the mask of the candidates, issued
 // together; then the coefficients. Inactive entries get s = 0.

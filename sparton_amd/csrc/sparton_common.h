@@ -45,6 +45,30 @@ __device__ __forceinline__ float load_mask(const void* mask, int mask_dtype, int
   }
 }
 
+// Mask values at N element offsets: every load is issued before any is converted, so
+// they take one round trip together (a conversion right after each load would make
+// each wait for the previous one).
+template <typename M, int N>
+__device__ __forceinline__ void mask_vals(const void* mask, const int64_t* off, float* out) {
+  M raw[N];
+#pragma unroll
+  for (int i = 0; i < N; ++i) raw[i] = ((const M*)mask)[off[i]];
+#pragma unroll
+  for (int i = 0; i < N; ++i) out[i] = (float)raw[i];
+}
+template <int N>
+__device__ __forceinline__ void load_mask_n(const void* mask, int mask_dtype, const int64_t* off,
+                                            float* out) {
+  switch (mask_dtype) {  // uniform
+    case SPARTON_MASK_I64: mask_vals<int64_t, N>(mask, off, out); break;
+    case SPARTON_MASK_I32: mask_vals<int32_t, N>(mask, off, out); break;
+    case SPARTON_MASK_U8: mask_vals<uint8_t, N>(mask, off, out); break;
+    case SPARTON_MASK_F32: mask_vals<float, N>(mask, off, out); break;
+    case SPARTON_MASK_BF16: mask_vals<bf16, N>(mask, off, out); break;
+    default: mask_vals<f16, N>(mask, off, out); break;
+  }
+}
+
 // Element `off` of a float tensor of dtype `dt` (enum sparton_dtype) as float.
 __device__ __forceinline__ float load_float(const void* p, int dt, int64_t off) {
   switch (dt) {

@@ -119,11 +119,13 @@ __device__ __forceinline__ void plan_row(const void* __restrict__ mask, int mask
   int n = 0;
   for (int t0 = 0; t0 < nblk * 32; t0 += 8 * 64) {
     bool nz[8];
+    int64_t off[8];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const int s = t0 + u * 64 + lane;
-      nz[u] = s < S && load_mask(mask, mask_dtype, (int64_t)b * S + s) != 0.0f;
-    }
+    for (int u = 0; u < 8; ++u) off[u] = (int64_t)b * S + min(t0 + u * 64 + lane, S - 1);
+    float mv[8];
+    load_mask_n<8>(mask, mask_dtype, off, mv);
+#pragma unroll
+    for (int u = 0; u < 8; ++u) nz[u] = t0 + u * 64 + lane < S && mv[u] != 0.0f;
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
       const int j = (t0 + u * 64) / 32;
@@ -234,6 +236,7 @@ __global__ __launch_bounds__(PLAN_THREADS) void fwd_plan_small_kernel(
     float* __restrict__ rowmask) {
   __shared__ uint8_t fl[PLAN_FUSED_MAX];
   __shared__ int cnt[PLAN_FUSED_MAX];
+  __shared__ int lst[PLAN_FUSED_MAX];  // the list, also kept here for the row mask
   __shared__ int wsum[PLAN_THREADS / 64];
   __shared__ int carry;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -242,11 +245,13 @@ __global__ __launch_bounds__(PLAN_THREADS) void fwd_plan_small_kernel(
     int n = 0;
     for (int t0 = 0; t0 < nblk * 32; t0 += 8 * 64) {
       bool nz[8];
+      int64_t off[8];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const int s = t0 + u * 64 + lane;
-        nz[u] = s < S && load_mask(mask, mask_dtype, (int64_t)b * S + s) != 0.0f;
-      }
+      for (int u = 0; u < 8; ++u) off[u] = (int64_t)b * S + min(t0 + u * 64 + lane, S - 1);
+      float mv[8];
+      load_mask_n<8>(mask, mask_dtype, off, mv);
+#pragma unroll
+      for (int u = 0; u < 8; ++u) nz[u] = t0 + u * 64 + lane < S && mv[u] != 0.0f;
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
         const int j = (t0 + u * 64) / 32;
@@ -293,15 +298,39 @@ __global__ __launch_bounds__(PLAN_THREADS) void fwd_plan_small_kernel(
       const int j = j0 + lane;
       const bool on = j < nblk && fl[b * nblk + j] != 0;
       const uint64_t bal = __ballot(on);
-      if (on) list[k + __popcll(bal & ((1ull << lane) - 1ull))] = b * nblk + j;
+      if (on) {
+        const int e = k + __popcll(bal & ((1ull << lane) - 1ull));
+        list[e] = b * nblk + j;
+        lst[e] = b * nblk + j;
+      }
       k += __popcll(bal);
     }
   }
-  __syncthreads();  // the list (global memory, written by this workgroup) is complete
+  __syncthreads();  // lst is complete
+  // Row mask in list order, RM rows per thread with their mask loads in flight together.
+  constexpr int RM = 8;
   const int n_blk = carry;
   const int n_rows = (n_blk + MBLK - 1) / MBLK * BM;
-  for (int t = tid; t < n_rows; t += PLAN_THREADS)
-    fill_rowmask(mask, mask_dtype, S, nblk, n_blk, list, rowmask, t);
+  for (int t0 = tid; t0 < n_rows; t0 += RM * PLAN_THREADS) {
+    int64_t off[RM];
+    bool ok[RM];
+#pragma unroll
+    for (int u = 0; u < RM; ++u) {
+      const int t = t0 + u * PLAN_THREADS, e = t >> 5;
+      const int code = (t < n_rows && e < n_blk) ? lst[e] : -1;
+      const int bb = code >= 0 ? code / nblk : 0;
+      const int ss = code >= 0 ? (code - bb * nblk) * 32 + (t & 31) : S;
+      ok[u] = ss < S;
+      off[u] = ok[u] ? (int64_t)bb * S + ss : 0;
+    }
+    float mv[RM];
+    load_mask_n<RM>(mask, mask_dtype, off, mv);
+#pragma unroll
+    for (int u = 0; u < RM; ++u) {
+      const int t = t0 + u * PLAN_THREADS;
+      if (t < n_rows) rowmask[t] = ok[u] ? mv[u] : 0.0f;
+    }
+  }
 }
 
 // ---- main kernel ------------------------------------------------------------------
@@ -1009,10 +1038,13 @@ static int64_t persistent_grid(int64_t n_units_max) {
   return std::min<int64_t>(g, n_units_max);
 }
 
+// ev_main: if non-null, two events recorded on `stream` just before and after the main
+// kernel (profiling).
 template <typename T>
 static int launch(const void* H, const void* W, const void* bias, const void* mask,
                   int mask_dtype, void* reps, int32_t* argmax, float* reps_f32, int64_t B,
-                  int64_t S, int64_t D, int64_t V, const Work& w, hipStream_t stream) {
+                  int64_t S, int64_t D, int64_t V, const Work& w, hipStream_t stream,
+                  hipEvent_t* ev_main) {
   const int64_t nblk = cdiv(S, 32);
   const int64_t n_vt = cdiv(V, BN);
   const int64_t n_mt_max = cdiv(B * nblk, MBLK);
@@ -1033,11 +1065,13 @@ static int launch(const void* H, const void* W, const void* bias, const void* ma
                        0, stream, mask, mask_dtype, (int)S, (int)nblk, (const int*)w.meta,
                        (const int*)w.list, w.rowmask);
   }
+  if (ev_main != nullptr) (void)hipEventRecord(ev_main[0], stream);
   if (grid > 0)  // S == 0: no blocks, the fixup writes every row
     hipLaunchKernelGGL(sparton_fwd_kernel<T>, dim3((unsigned)grid), dim3(NTHREADS), 0, stream,
                        (const T*)H, (const T*)W, (const T*)bias, (const float*)w.rowmask, (T*)reps,
                        argmax, reps_f32, (int)S, (int)D, (int)V, (int)n_vt, (int)nblk,
                        (const int*)w.meta, (const int*)w.list, w.part);
+  if (ev_main != nullptr) (void)hipEventRecord(ev_main[1], stream);
   hipLaunchKernelGGL(fwd_fixup_kernel<T>, dim3((unsigned)cdiv(V, FIX_COLS), (unsigned)B), dim3(256), 0,
                      stream, (int)V, (const int*)w.count, (const int*)w.first,
                      (const float2*)w.part, (T*)reps, argmax, reps_f32);
@@ -1073,10 +1107,12 @@ extern "C" __attribute__((visibility("default"))) size_t sparton_fwd_workspace_b
   return fwd::carve(nullptr, fwd::rows_per_launch(B, S, D, esz), S, V).total;
 }
 
-extern "C" __attribute__((visibility("default"))) int sparton_fwd(
-    const void* hidden, const void* weight, const void* bias, const void* mask,
-    int mask_dtype, void* reps, int32_t* argmax, float* reps_f32, int64_t B, int64_t S,
-    int64_t D, int64_t V, int dtype, void* workspace, size_t workspace_bytes, void* stream) {
+// The forward over row chunks; with main_ms, each chunk's main kernel is bracketed by
+// HIP events and its device time added to *main_ms (synchronizing on each chunk).
+static int fwd_run(const void* hidden, const void* weight, const void* bias, const void* mask,
+                   int mask_dtype, void* reps, int32_t* argmax, float* reps_f32, int64_t B,
+                   int64_t S, int64_t D, int64_t V, int dtype, void* workspace,
+                   size_t workspace_bytes, void* stream, float* main_ms) {
   if (B < 0 || S < 0 || D < 0 || V < 0) return SPARTON_EINVAL;
   if (dtype < SPARTON_F32 || dtype > SPARTON_F16) return SPARTON_EINVAL;
   if (mask_dtype < SPARTON_MASK_I64 || mask_dtype > SPARTON_MASK_F16) return SPARTON_EINVAL;
@@ -1105,19 +1141,55 @@ extern "C" __attribute__((visibility("default"))) int sparton_fwd(
     char* r = (char*)reps + b0 * V * esz;
     int32_t* am = argmax == nullptr ? nullptr : argmax + b0 * V;
     float* r32 = reps_f32 == nullptr ? nullptr : reps_f32 + b0 * V;
+    hipEvent_t ev[2] = {nullptr, nullptr};
+    if (main_ms != nullptr) {
+      if (hipEventCreate(&ev[0]) != hipSuccess || hipEventCreate(&ev[1]) != hipSuccess) {
+        if (ev[0] != nullptr) (void)hipEventDestroy(ev[0]);
+        return (int)hipGetLastError();
+      }
+    }
+    hipEvent_t* evp = main_ms != nullptr ? ev : nullptr;
     int rc;
     switch (dtype) {
       case SPARTON_BF16:
-        rc = fwd::launch<bf16>(h, weight, bias, mk, mask_dtype, r, am, r32, nb, S, D, V, w, st);
+        rc = fwd::launch<bf16>(h, weight, bias, mk, mask_dtype, r, am, r32, nb, S, D, V, w, st, evp);
         break;
       case SPARTON_F16:
-        rc = fwd::launch<f16>(h, weight, bias, mk, mask_dtype, r, am, r32, nb, S, D, V, w, st);
+        rc = fwd::launch<f16>(h, weight, bias, mk, mask_dtype, r, am, r32, nb, S, D, V, w, st, evp);
         break;
       default:
-        rc = fwd::launch<float>(h, weight, bias, mk, mask_dtype, r, am, r32, nb, S, D, V, w, st);
+        rc = fwd::launch<float>(h, weight, bias, mk, mask_dtype, r, am, r32, nb, S, D, V, w, st, evp);
         break;
+    }
+    if (main_ms != nullptr) {
+      float ms = 0.0f;
+      hipError_t e = hipEventSynchronize(ev[1]);
+      if (e == hipSuccess) e = hipEventElapsedTime(&ms, ev[0], ev[1]);
+      (void)hipEventDestroy(ev[0]);
+      (void)hipEventDestroy(ev[1]);
+      if (rc == SPARTON_OK && e != hipSuccess) rc = (int)e;
+      *main_ms += ms;
     }
     if (rc != SPARTON_OK) return rc;
   }
   return SPARTON_OK;
+}
+
+extern "C" __attribute__((visibility("default"))) int sparton_fwd(
+    const void* hidden, const void* weight, const void* bias, const void* mask,
+    int mask_dtype, void* reps, int32_t* argmax, float* reps_f32, int64_t B, int64_t S,
+    int64_t D, int64_t V, int dtype, void* workspace, size_t workspace_bytes, void* stream) {
+  return fwd_run(hidden, weight, bias, mask, mask_dtype, reps, argmax, reps_f32, B, S, D, V,
+                 dtype, workspace, workspace_bytes, stream, nullptr);
+}
+
+extern "C" __attribute__((visibility("default"))) int sparton_fwd_profile(
+    const void* hidden, const void* weight, const void* bias, const void* mask,
+    int mask_dtype, void* reps, int32_t* argmax, float* reps_f32, int64_t B, int64_t S,
+    int64_t D, int64_t V, int dtype, void* workspace, size_t workspace_bytes, void* stream,
+    float* main_ms) {
+  if (main_ms == nullptr) return SPARTON_EINVAL;
+  *main_ms = 0.0f;
+  return fwd_run(hidden, weight, bias, mask, mask_dtype, reps, argmax, reps_f32, B, S, D, V,
+                 dtype, workspace, workspace_bytes, stream, main_ms);
 }

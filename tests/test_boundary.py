@@ -93,6 +93,12 @@ def test_bwd_argument_validation(kw, code):
     assert bwd(**kw) == code
 
 
+def test_fwd_profile_requires_time_output():
+    a = dict(hidden=P, weight=P, bias=None, mask=P, mask_dtype=0, reps=P, argmax=P, reps_f32=None,
+             B=2, S=4, D=64, V=10, dtype=1, ws=P, ws_bytes=1 << 30, stream=None, main_ms=None)
+    assert _lib.load().sparton_fwd_profile(*a.values()) == -1
+
+
 def test_strerror_from_python_check():
     with pytest.raises(RuntimeError, match="invalid argument"):
         _lib.check(-1, "x")

@@ -364,6 +364,34 @@ def test_reads_stay_inside_rows(dt, D, device):
     say(f"  checked {n} entries, {bad} near-tie argmax differences")
 
 
+def test_fwd_profile_entry_point_matches_fwd(device):
+    """sparton_fwd_profile does the same work as sparton_fwd and reports the main
+    kernel's device time."""
+    import ctypes
+    say("sparton_fwd_profile vs sparton_fwd")
+    H, W, b, m, _ = make_case("bf16", 3, 77, 64, 1000, True, "int64")
+    Hd, Wd, bd, md = H.to(device), W.to(device), b.to(device), m.to(device)
+    r_ref, i_ref, r32_ref = torch.ops.sparton.fused_sparton_fwd_train(Hd, Wd, bd, md)
+    L = _lib.load()
+    B, S, D = H.shape
+    V = W.shape[0]
+    dt = _lib.DTYPE_CODE[H.dtype]
+    reps = torch.empty_like(r_ref)
+    idx = torch.empty_like(i_ref)
+    r32 = torch.empty_like(r32_ref)
+    nbytes = int(L.sparton_fwd_workspace_bytes(B, S, D, V, dt))
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=device)
+    ms = ctypes.c_float(-1.0)
+    rc = L.sparton_fwd_profile(Hd.data_ptr(), Wd.data_ptr(), bd.data_ptr(), md.data_ptr(),
+                               _lib.MASK_CODE[md.dtype], reps.data_ptr(), idx.data_ptr(),
+                               r32.data_ptr(), B, S, D, V, dt, ws.data_ptr(), nbytes,
+                               torch.cuda.current_stream().cuda_stream, ctypes.byref(ms))
+    assert rc == 0
+    torch.cuda.synchronize()
+    assert torch.equal(reps, r_ref) and torch.equal(idx, i_ref) and torch.equal(r32, r32_ref)
+    assert 0.0 < ms.value < 1000.0
+
+
 def test_autocast_policy(device):
     say("autocast bf16 with fp32 parameters")
     B, S, D, V = 2, 64, 64, 500
