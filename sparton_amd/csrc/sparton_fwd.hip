@@ -21,7 +21,9 @@
 // each it computes the 256 x BN logit tile with bf16/fp16 (or fp32) MFMA, K = D
 // streamed through two LDS stages. The K slabs of all its units form one stream, and
 // the next unit's metadata (block list, row mask, row offsets, bias) is fetched during
-// the current unit's first K steps, so a unit starts while the previous one finishes. The epilogue folds each 32-row block into a per-column (max, argmax),
+// the current unit's first K steps, so a unit starts while the previous one finishes.
+// Eight compute waves run the MFMAs and the epilogue; four copy waves issue all copies
+// and write the results. The epilogue folds each 32-row block into a per-column (max, argmax),
 // merges consecutive blocks of the same batch row in s order (larger value; on ties
 // the lower s, which is the earlier block), and per batch-row segment either writes
 // reps/argmax (segment complete in this tile) or, when the segment continues into a
@@ -53,21 +55,26 @@ namespace fwd {
 
 constexpr int BM = 256;              // rows per M-tile
 constexpr int BN = 256;              // vocab columns per tile
-constexpr int WAVES_M = 2;           // waves along M
-constexpr int WAVES_N = 4;           // waves along N (vocab)
-constexpr int NWAVES = WAVES_M * WAVES_N;
-constexpr int NTHREADS = 64 * NWAVES;
+constexpr int WAVES_M = 2;           // compute waves along M
+constexpr int WAVES_N = 4;           // compute waves along N (vocab)
+// Roles. Waves 0..7 compute (a 2 x 4 grid of 128 x 64 tiles). Waves 8..11, the copy
+// waves (one per SIMD), move data: they issue every slab copy, fetch the next unit's
+// metadata and write the previous unit's results. A wave waits while the address unit
+// takes its copies; this way no compute wave ever does, and the matrix pipe of each
+// SIMD is fed by its two compute waves. Three waves per SIMD leave 168 VGPRs each.
+constexpr int COMPUTE_WAVES = WAVES_M * WAVES_N;
+constexpr int COPY_WAVES = 4;
+constexpr int COPY_THREADS = 64 * COPY_WAVES;
+constexpr int NTHREADS = 64 * (COMPUTE_WAVES + COPY_WAVES);
 constexpr int MBLK = BM / 32;        // 32-row blocks per M-tile (8)
 constexpr int NB_PER_WAVE = BN / WAVES_N / 32;     // 2
 constexpr int SLAB = 128;            // bytes of K per row per pipeline stage
 constexpr int CHUNKS = SLAB / 16;    // 16-byte chunks per row slab (8)
 constexpr int ROWS_PER_LOAD = 64 / CHUNKS;          // rows one wave-wide load covers (8)
-// Only the first LOAD_WAVES waves (one per SIMD) issue the slab copies: a wave waits
-// while the address unit takes its copies, and its SIMD partner (wave + 4, which issues
-// none) keeps the matrix pipe busy meanwhile.
-constexpr int LOAD_WAVES = 4;
-constexpr int A_LOADS = BM / ROWS_PER_LOAD / LOAD_WAVES;  // wave-wide copies per slab for A (8)
-constexpr int B_LOADS = BN / ROWS_PER_LOAD / LOAD_WAVES;  // and for B (8)
+constexpr int A_LOADS = BM / ROWS_PER_LOAD / COPY_WAVES;  // wave-wide copies per slab for A (8)
+constexpr int B_LOADS = BN / ROWS_PER_LOAD / COPY_WAVES;  // and for B (8)
+// The copy threads handle one tile row / one column each.
+static_assert(BM == COPY_THREADS && BN == COPY_THREADS, "one copy thread per row and column");
 constexpr int MAX_S = 16384;         // positions per batch row (512 blocks)
 constexpr int PLAN_THREADS = 1024;
 
@@ -344,6 +351,7 @@ struct __align__(16) UnitMeta {
                              // blocks just before / after the tile (-1 if none)
   int blk_s[MBLK];           // first position of each block (32 j)
   int mask_binary;           // every maskf value is 0 or 1
+  float bias[BN];            // bias of the tile's columns (0 past V or without bias)
 };
 
 struct Smem {
@@ -438,49 +446,50 @@ struct Args {
   int S;
   int row_bytes;      // D * sizeof(T)
   int nk_full;        // slabs lying entirely inside the row
+  int nk;             // slabs per unit
   int V;
 };
 
-// Per-lane data of one unit.
-struct Lanes {
-  uint32_t a_off[A_LOADS];    // byte offset from H of the lane's A row and chunk, per load
-  float bias[NB_PER_WAVE];    // bias of the lane's columns
+// One unit as the copy waves see it.
+struct CopyUnit {
+  int m, v0, n_valid;
+  uint32_t a_off[A_LOADS];  // byte offset from H of the lane's A row and chunk, per copy
 };
 
-// ---- unit metadata (each step is run by every thread; the ones named take part) ----
+// ---- unit metadata (run by the copy threads, ct = 0..255; the ones named take part) ----
 
-// Threads 0..MBLK+1: the tile's list entry (b * nblk + j), or -1.
-__device__ __forceinline__ int block_entry(int m, int tid);
-__device__ __forceinline__ int block_code(const int* list, int n_blk, int m, int n_valid, int tid) {
-  const int e = block_entry(m, tid);
-  const bool ok = e >= 0 && e < n_blk && (tid >= MBLK || tid < n_valid);
+// Copy threads 0..MBLK+1: the tile's list entry (b * nblk + j), or -1.
+__device__ __forceinline__ int block_entry(int m, int ct) {
+  return ct < MBLK ? m * MBLK + ct : (ct == MBLK ? m * MBLK - 1 : m * MBLK + MBLK);
+}
+__device__ __forceinline__ int block_code(const int* list, int n_blk, int m, int n_valid, int ct) {
+  const int e = block_entry(m, ct);
+  const bool ok = e >= 0 && e < n_blk && (ct >= MBLK || ct < n_valid);
   return ok ? list[e] : -1;
 }
 
-__device__ __forceinline__ void put_blocks(UnitMeta& um, int code, int nblk, int tid) {
-  if (tid < MBLK + 2) {
-    um.blk_b[tid] = code >= 0 ? code / nblk : -1;
-    if (tid < MBLK) um.blk_s[tid] = code >= 0 ? (code % nblk) * 32 : 0;
+__device__ __forceinline__ void put_blocks(UnitMeta& um, int code, int nblk, int ct) {
+  if (ct < MBLK + 2) {
+    um.blk_b[ct] = code >= 0 ? code / nblk : -1;
+    if (ct < MBLK) um.blk_s[ct] = code >= 0 ? (code % nblk) * 32 : 0;
   }
 }
 
-// Threads 0..BM-1, given the mask value of tile row tid: the AND word, and clear
-// mask_binary (set to 1 by thread 0 before a barrier) on any value other than 0 / 1.
-__device__ __forceinline__ void put_mask_words(UnitMeta& um, float mv, int tid, int lane) {
-  if (tid < BM) {  // whole waves
-    um.maskw[tid] = mv != 0.0f ? ~31 : 0;
-    if (__ballot(mv != 0.0f && mv != 1.0f) != 0 && lane == 0) um.mask_binary = 0;
-  }
+// Given the mask value of tile row ct: the AND word, and clear mask_binary (set to 1
+// before a barrier) on any value other than 0 / 1.
+__device__ __forceinline__ void put_mask_words(UnitMeta& um, float mv, int ct, int lane) {
+  um.maskw[ct] = mv != 0.0f ? ~31 : 0;
+  if (__ballot(mv != 0.0f && mv != 1.0f) != 0 && lane == 0) um.mask_binary = 0;
 }
 
-// Per lane (after put_blocks is visible): the byte offsets of its A rows. Rows of
-// blocks past n_valid get some valid row (their loads are skipped); positions past S
+// Per copy lane (after put_blocks is visible): the byte offsets of its A rows. Rows of
+// blocks past n_valid get some valid row (their copies are skipped); positions past S
 // any valid position of the row.
 __device__ __forceinline__ void row_offsets(const UnitMeta& um, int n_valid, int S, int row_bytes,
-                                            int wave, int lane, uint32_t* a_off) {
+                                            int c, int lane, uint32_t* a_off) {
 #pragma unroll
   for (int i = 0; i < A_LOADS; ++i) {
-    const int grp = i * LOAD_WAVES + (wave & (LOAD_WAVES - 1));
+    const int grp = i * COPY_WAVES + c;
     const int row = grp * ROWS_PER_LOAD + (lane >> 3);
     const int r = min(row >> 5, n_valid - 1);
     const int s = min(um.blk_s[r] + (row & 31), S - 1);
@@ -488,19 +497,8 @@ __device__ __forceinline__ void row_offsets(const UnitMeta& um, int n_valid, int
   }
 }
 
-template <typename T>
-__device__ __forceinline__ void load_bias(const Args<T>& a, int v0, int wn, int lane, float* out) {
-#pragma unroll
-  for (int nb = 0; nb < NB_PER_WAVE; ++nb) {
-    const int col = v0 + wn * 64 + nb * 32 + (lane & 31);
-    out[nb] = (a.bias != nullptr && col < a.V) ? to_f32(a.bias[col]) : 0.0f;
-  }
-}
-
 // Raw loads for the in-loop prefetch: the bits are loaded without any conversion or
-// select, so no instruction needs them until they are converted a K step later, after
-// the step's full drain. (Converting right after the load would make the wave wait for
-// every load in flight -- the next slab included.)
+// select, and converted two K steps later, after the steps' drains.
 template <typename T> __device__ __forceinline__ uint32_t load_bits(const T* p, int64_t i);
 template <> __device__ __forceinline__ uint32_t load_bits(const bf16* p, int64_t i) {
   return ((const uint16_t*)p)[i];
@@ -520,36 +518,34 @@ template <> __device__ __forceinline__ float bits_to_f32<float>(uint32_t x) { re
 
 // ---- K stream ----
 
-// Issue the direct global -> LDS copies of K slab k of vocab tile v0 into stage buf.
-// Loading wave w (< LOAD_WAVES), copy i covers the 8-row group g = i * LOAD_WAVES + w
-// (rows 8g..8g+7 of the tile, in block g / 4); lane L lands at LDS chunk g*64 + L.
-// Other waves issue nothing. A chunk past the row end
+// Issue the direct global -> LDS copies of K slab k of a unit into stage buf. Copy
+// wave c, copy i covers the 8-row group g = i * COPY_WAVES + c (rows 8g..8g+7 of the
+// tile, in block g / 4); lane L lands at LDS chunk g*64 + L. A chunk past the row end
 // (tail or padding slabs) re-reads the row's first chunk -- valid, finite data inside
 // the row, so nothing outside H or W is read -- and its W copy is zeroed by zero_tail()
 // before use (a zero W times a finite H adds exactly 0). W rows past V re-read row V-1
-// (never stored); A loads of blocks past the last active one (n_valid) are skipped.
+// (never stored); A copies of blocks past the last active one (n_valid) are skipped.
 template <typename T>
-__device__ __forceinline__ void issue_slab(Smem& sm, const Args<T>& a, const uint32_t* a_off,
-                                           int n_valid, int v0, int k, int buf, int wave, int lane) {
-  if (wave >= LOAD_WAVES) return;
+__device__ __forceinline__ void issue_slab(Smem& sm, const Args<T>& a, const CopyUnit& cu, int k,
+                                           int buf, int c, int lane) {
   const uint32_t kb = (uint32_t)k * SLAB;
   const bool tail = k >= a.nk_full;
-  const int a_groups = n_valid * (32 / ROWS_PER_LOAD);
+  const int a_groups = cu.n_valid * (32 / ROWS_PER_LOAD);
 #pragma unroll
   for (int i = 0; i < A_LOADS; ++i) {
-    const int grp = i * LOAD_WAVES + wave;
+    const int grp = i * COPY_WAVES + c;
     const uint32_t c16 = lane_chunk(grp * ROWS_PER_LOAD + (lane >> 3), lane);
     // a_off includes c16: adding 0 - c16 (mod 2^32) lands on the row's first chunk.
     const uint32_t step = (!tail || kb + c16 < (uint32_t)a.row_bytes) ? kb : 0u - c16;
     if (grp < a_groups)
-      __builtin_amdgcn_global_load_lds((const void*)(a.H + (a_off[i] + step)),
+      __builtin_amdgcn_global_load_lds((const void*)(a.H + (cu.a_off[i] + step)),
                                        (lds_void*)&sm.a[buf][grp * 64], 16, 0, 0);
   }
-  const char* bb = a.W + (int64_t)v0 * a.row_bytes;
-  const int b_last = a.V - 1 - v0;
+  const char* bb = a.W + (int64_t)cu.v0 * a.row_bytes;
+  const int b_last = a.V - 1 - cu.v0;
 #pragma unroll
   for (int i = 0; i < B_LOADS; ++i) {
-    const int grp = i * LOAD_WAVES + wave;
+    const int grp = i * COPY_WAVES + c;
     const int row = grp * ROWS_PER_LOAD + (lane >> 3);
     const uint32_t c16 = lane_chunk(row, lane);
     const uint32_t step = (!tail || kb + c16 < (uint32_t)a.row_bytes) ? kb : 0u - c16;
@@ -558,231 +554,307 @@ __device__ __forceinline__ void issue_slab(Smem& sm, const Args<T>& a, const uin
   }
 }
 
-// Direct loads one slab issues from this wave.
-__device__ __forceinline__ int slab_loads(int n_valid, int wave) {
-  if (wave >= LOAD_WAVES) return 0;
-  const int a_groups = n_valid * (32 / ROWS_PER_LOAD);
-  int n = B_LOADS;
-#pragma unroll
-  for (int i = 0; i < A_LOADS; ++i) n += (i * LOAD_WAVES + wave < a_groups) ? 1 : 0;
-  return n;
-}
-
-// Zero the W chunks of slab k (in stage buf) that lie past D; run after its copies
-// landed and before any wave reads the stage.
-__device__ __forceinline__ void zero_tail(Smem& sm, int row_bytes, int k, int buf, int wave, int lane) {
+// Zero the W chunks of slab k (in stage buf) that lie past D; each copy wave clears the
+// chunks it copied itself, after its copies landed and before the step's barrier.
+__device__ __forceinline__ void zero_tail(Smem& sm, int row_bytes, int k, int buf, int c, int lane) {
   const uint32_t kb = (uint32_t)k * SLAB;
 #pragma unroll
-  for (int i = 0; i < BN / ROWS_PER_LOAD / NWAVES; ++i) {
-    const int grp = i * NWAVES + wave;
+  for (int i = 0; i < B_LOADS; ++i) {
+    const int grp = i * COPY_WAVES + c;
     if (kb + lane_chunk(grp * ROWS_PER_LOAD + (lane >> 3), lane) >= (uint32_t)row_bytes)
       sm.b[buf][grp * 64 + lane] = u32x4{0, 0, 0, 0};
   }
 }
 
-// Wait for all of this thread's outstanding memory operations (the direct-to-LDS
-// loads included), then the workgroup barrier.
-__device__ __forceinline__ void drain_and_sync() {
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-}
-
-// Workgroup barrier for data exchanged through ordinary LDS reads/writes only: waits
-// for this wave's LDS operations, not for its global loads. (__syncthreads() implies a
-// workgroup fence, which on gfx950 also waits for every outstanding direct-to-LDS
-// load -- here the next unit's slabs, which must stay in flight.) The memory clobber
-// keeps the compiler from moving memory accesses across it.
+// Workgroup barrier once this wave's LDS operations are complete; its global loads
+// (direct-to-LDS copies included) may still be in flight. (__syncthreads() would also
+// wait for every outstanding direct-to-LDS copy.) The memory clobber keeps the compiler
+// from moving memory accesses across it.
 __device__ __forceinline__ void lds_barrier() {
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
-// Wait until at most n (0..16, wave-uniform) direct loads of this wave are in flight.
-// s_waitcnt takes an immediate: simm16 = vmcnt[5:4] << 14 | lgkmcnt[11:8] | expcnt[6:4]
-// | vmcnt[3:0]; VMCNT(n) is vmcnt(n) with lgkmcnt and expcnt at their no-wait maxima.
-#define VMCNT(n) ((((n) >> 4) & 3) << 14 | 0x0F70 | ((n) & 15))
-__device__ __forceinline__ void wait_loads_at_most(int n) {
-  switch (n) {
-    case 0: __builtin_amdgcn_s_waitcnt(VMCNT(0)); break;
-    case 1: __builtin_amdgcn_s_waitcnt(VMCNT(1)); break;
-    case 2: __builtin_amdgcn_s_waitcnt(VMCNT(2)); break;
-    case 3: __builtin_amdgcn_s_waitcnt(VMCNT(3)); break;
-    case 4: __builtin_amdgcn_s_waitcnt(VMCNT(4)); break;
-    case 5: __builtin_amdgcn_s_waitcnt(VMCNT(5)); break;
-    case 6: __builtin_amdgcn_s_waitcnt(VMCNT(6)); break;
-    case 7: __builtin_amdgcn_s_waitcnt(VMCNT(7)); break;
-    case 8: __builtin_amdgcn_s_waitcnt(VMCNT(8)); break;
-    case 9: __builtin_amdgcn_s_waitcnt(VMCNT(9)); break;
-    case 10: __builtin_amdgcn_s_waitcnt(VMCNT(10)); break;
-    case 11: __builtin_amdgcn_s_waitcnt(VMCNT(11)); break;
-    case 12: __builtin_amdgcn_s_waitcnt(VMCNT(12)); break;
-    case 13: __builtin_amdgcn_s_waitcnt(VMCNT(13)); break;
-    case 14: __builtin_amdgcn_s_waitcnt(VMCNT(14)); break;
-    case 15: __builtin_amdgcn_s_waitcnt(VMCNT(15)); break;
-    default: __builtin_amdgcn_s_waitcnt(VMCNT(16)); break;
+// Wait for all of this wave's memory operations (copies, loads, stores).
+__device__ __forceinline__ void wait_all() {
+  asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+}
+
+// ---- the workgroup's unit sequence ----
+//
+// Both roles walk the same sequence and pass the same barriers:
+//   start of the first unit, and of every unit when the metadata is not prefetched
+//   (nk < PREFETCH_MIN_NK): 2 barriers;
+//   each K step k = 0..nk-1: 1 barrier (B_k); after the epilogue: 1 barrier (E).
+// Slab j of a unit lives in stage buf ^ (j & 1), where buf is the unit's first stage.
+// The copy waves issue slab k+1 at the start of step k (k >= 1; slab 1 is issued before
+// step 0), into the stage that slab k-1 left at B_(k-1), and wait for it before B_k.
+// With prefetch the next unit's slab 0 is issued at step nk-1 and its slab 1 after
+// B_(nk-1), and its metadata is fetched during steps 0, 2 and 3 (step 1 writes the
+// previous unit's results; they and the metadata share a buffer).
+constexpr int PREFETCH_MIN_NK = 5;
+
+struct Unit {
+  int u, m, v0, n_valid;
+};
+__device__ __forceinline__ Unit unit_of(int w, int r, int G, int n_units, int n_mt, int n_vt,
+                                        int n_blk) {
+  Unit x;
+  x.u = unit_at(w, r, G, n_units);
+  x.m = 0;
+  x.v0 = 0;
+  x.n_valid = 0;
+  if (x.u >= 0) {
+    int vt;
+    unit_tile(x.u, n_mt, n_vt, &x.m, &vt);
+    x.v0 = vt * BN;
+    x.n_valid = min(MBLK, n_blk - x.m * MBLK);
+  }
+  return x;
+}
+
+// ---- copy waves ----
+
+// Merge the blocks of each batch-row segment of the tile (copy thread = column) and
+// write reps/argmax for complete segments, or the partial for a segment that continues
+// into the previous M-tile (slot 0) or the next one (slot 1).
+template <typename T>
+__device__ __forceinline__ void write_unit(const Smem& sm, const UnitMeta& um, int m, int v0, int V,
+                                           int n_valid, int ct, T* reps, int32_t* argmax,
+                                           float* reps_f32, float2* part) {
+  if (v0 + ct >= V) return;
+  const int v = v0 + ct;
+  const int b_prev = um.blk_b[MBLK], b_next = um.blk_b[MBLK + 1];
+  float pvr[MBLK];
+  int pir[MBLK];
+#pragma unroll
+  for (int r = 0; r < MBLK; ++r) {  // all loads first (rows past n_valid are unused)
+    pvr[r] = sm.pv[r][ct];
+    pir[r] = sm.pi[r][ct];
+  }
+  float bv = 0.0f;
+  int bi = 0;
+#pragma unroll
+  for (int r = 0; r < MBLK; ++r) {
+    if (r >= n_valid) break;
+    if (pvr[r] > bv) {  // earlier blocks hold lower s: strict '>' keeps them on ties
+      bv = pvr[r];
+      bi = pir[r];
+    }
+    const int b = um.blk_b[r];
+    if (r + 1 == n_valid || um.blk_b[r + 1] != b) {  // the segment of batch row b ends
+      const bool cont_prev = b == um.blk_b[0] && b == b_prev;
+      const bool cont_next = r + 1 == n_valid && b == b_next;
+      if (cont_prev || cont_next) {
+        part[((int64_t)m * 2 + (cont_prev ? 0 : 1)) * V + v] = make_float2(bv, __int_as_float(bi));
+      } else {
+        const int64_t o = (int64_t)b * V + v;
+        const float rv = log1pf(bv);
+        reps[o] = from_f32<T>(rv);
+        if (argmax != nullptr) argmax[o] = bi;
+        if (reps_f32 != nullptr) reps_f32[o] = rv;
+      }
+      bv = 0.0f;
+      bi = 0;
+    }
   }
 }
-#undef VMCNT
 
-// ---- one unit ----
-
-// The next unit of this workgroup, when its metadata is fetched inside the current
-// unit's K loop (nk >= 4). Each step ends with a full drain and a barrier, which orders
-// the steps across waves:
-//   step 0: the rows' mask copied straight into LDS (direct loads, like the slabs);
-//           raw loads of the tile's list entries and of the bias of its columns;
-//   step 1: blocks and mask words stored to LDS;
-//   step 2: A-row offsets, from the stored blocks.
-// The bias is converted at the hand-over. The next unit's first two slabs are issued
-// during the current unit's last two steps.
-struct Next {
-  bool on;
-  int m, v0, n_valid;
-  int code_bits;          // threads 0..MBLK+1: list entry (clamped index)
-  uint32_t bias_bits[NB_PER_WAVE];
-  uint32_t a_off[A_LOADS];
+template <typename T>
+struct Outputs {
+  T* reps;
+  int32_t* argmax;
+  float* reps_f32;
+  float2* part;
 };
 
-__device__ __forceinline__ int block_entry(int m, int tid) {
-  return tid < MBLK ? m * MBLK + tid : (tid == MBLK ? m * MBLK - 1 : m * MBLK + MBLK);
+// Start a unit without prefetch: fetch its metadata into um, write the previous unit's
+// results (prev.u >= 0, metadata in um_prev), and land its first two slabs. Two barriers.
+template <typename T>
+__device__ __forceinline__ void copy_start(Smem& sm, const Args<T>& a, const Outputs<T>& o,
+                                           UnitMeta& um, CopyUnit& cu, int buf,
+                                           const Unit& prev, const UnitMeta& um_prev, int ct,
+                                           int c, int lane) {
+  const int code = ct < MBLK + 2 ? block_code(a.list, a.n_blk, cu.m, cu.n_valid, ct) : -1;
+  const float mv = a.rowmask[(int64_t)cu.m * BM + ct];
+  const int col = cu.v0 + ct;
+  const float bv = (a.bias != nullptr && col < a.V) ? to_f32(a.bias[col]) : 0.0f;
+  put_blocks(um, code, a.nblk, ct);
+  um.maskf[ct] = mv;
+  um.bias[ct] = bv;
+  if (ct == 0) um.mask_binary = 1;
+  lds_barrier();  // S1
+  row_offsets(um, cu.n_valid, a.S, a.row_bytes, c, lane, cu.a_off);
+  if (a.nk > 0) {
+    issue_slab(sm, a, cu, 0, buf, c, lane);
+    issue_slab(sm, a, cu, 1, buf ^ 1, c, lane);
+  }
+  put_mask_words(um, mv, ct, lane);
+  if (prev.u >= 0)
+    write_unit<T>(sm, um_prev, prev.m, prev.v0, a.V, prev.n_valid, ct, o.reps, o.argmax,
+                  o.reps_f32, o.part);
+  wait_all();
+  if (a.nk > 0) {
+    if (0 >= a.nk_full) zero_tail(sm, a.row_bytes, 0, buf, c, lane);
+    if (1 >= a.nk_full) zero_tail(sm, a.row_bytes, 1, buf ^ 1, c, lane);
+  }
+  lds_barrier();  // S2
 }
 
 template <typename T>
-__device__ __forceinline__ void fetch_step(int k, const Args<T>& a, Next& nx, UnitMeta& um,
-                                           int tid, int wave, int lane, int wn) {
-  if (k == 0) {
-    if (tid == 0) um.mask_binary = 1;
-    if (wave < BM / 64)
-      __builtin_amdgcn_global_load_lds((const void*)(a.rowmask + (int64_t)nx.m * BM + tid),
-                                       (lds_void*)&um.maskf[wave * 64], 4, 0, 0);
-    if (tid < MBLK + 2) nx.code_bits = a.list[min(max(block_entry(nx.m, tid), 0), a.n_blk - 1)];
-    if (a.bias != nullptr) {
-#pragma unroll
-      for (int nb = 0; nb < NB_PER_WAVE; ++nb)
-        nx.bias_bits[nb] = load_bits(a.bias, min(nx.v0 + wn * 64 + nb * 32 + (lane & 31), a.V - 1));
+__device__ void copy_path(Smem& sm, const Args<T>& a, const Outputs<T>& o, int w, int G,
+                          int n_units, int n_mt, int n_vt, int ct, int c, int lane) {
+  const int nk = a.nk;
+  Unit cur = unit_of(w, 0, G, n_units, n_mt, n_vt, a.n_blk);
+  if (cur.u < 0) return;
+  Unit prev;
+  prev.u = -1;
+  int par = 0, buf = 0;
+  CopyUnit cu;
+  cu.m = cur.m;
+  cu.v0 = cur.v0;
+  cu.n_valid = cur.n_valid;
+  copy_start(sm, a, o, sm.um[0], cu, buf, prev, sm.um[1], ct, c, lane);
+
+  for (int r = 1;; ++r) {
+    const Unit next = unit_of(w, r, G, n_units, n_mt, n_vt, a.n_blk);
+    const bool pre = next.u >= 0 && nk >= PREFETCH_MIN_NK;
+    UnitMeta& um_next = sm.um[par ^ 1];
+    const int buf_next = buf ^ (nk & 1);
+    CopyUnit nx;
+    nx.m = next.m;
+    nx.v0 = next.v0;
+    nx.n_valid = next.n_valid;
+    int code_bits = 0;
+    uint32_t bias_bits = 0;
+    float mv = 0.0f;
+    for (int k = 0; k < nk; ++k) {
+      if (k >= 1) {
+        if (k + 1 < nk)
+          issue_slab(sm, a, cu, k + 1, buf ^ ((k + 1) & 1), c, lane);
+        else if (pre)
+          issue_slab(sm, a, nx, 0, buf_next, c, lane);
+      }
+      if (pre) {
+        if (k == 0) {
+          if (ct == 0) um_next.mask_binary = 1;
+          __builtin_amdgcn_global_load_lds((const void*)(a.rowmask + (int64_t)nx.m * BM + ct),
+                                           (lds_void*)&um_next.maskf[c * 64], 4, 0, 0);
+          if (ct < MBLK + 2)
+            code_bits = a.list[min(max(block_entry(nx.m, ct), 0), a.n_blk - 1)];
+          if (a.bias != nullptr) bias_bits = load_bits(a.bias, min(nx.v0 + ct, a.V - 1));
+        } else if (k == 2) {
+          const int e = block_entry(nx.m, ct);
+          const bool ok = e >= 0 && e < a.n_blk && (ct >= MBLK || ct < nx.n_valid);
+          put_blocks(um_next, ok ? code_bits : -1, a.nblk, ct);
+          mv = um_next.maskf[ct];
+          put_mask_words(um_next, mv, ct, lane);
+          const int col = nx.v0 + ct;
+          um_next.bias[ct] = (a.bias != nullptr && col < a.V) ? bits_to_f32<T>(bias_bits) : 0.0f;
+        } else if (k == 3) {
+          row_offsets(um_next, nx.n_valid, a.S, a.row_bytes, c, lane, nx.a_off);
+        }
+      }
+      if (k == 1 && prev.u >= 0) {
+        write_unit<T>(sm, um_next, prev.m, prev.v0, a.V, prev.n_valid, ct, o.reps, o.argmax,
+                      o.reps_f32, o.part);
+        prev.u = -1;
+      }
+      wait_all();
+      if (k + 1 < nk) {
+        if (k + 1 >= a.nk_full) zero_tail(sm, a.row_bytes, k + 1, buf ^ ((k + 1) & 1), c, lane);
+      } else if (pre && 0 >= a.nk_full) {
+        zero_tail(sm, a.row_bytes, 0, buf_next, c, lane);
+      }
+      lds_barrier();  // B_k
     }
-  } else if (k == 1) {
-    const int e = block_entry(nx.m, tid);
-    const bool ok = e >= 0 && e < a.n_blk && (tid >= MBLK || tid < nx.n_valid);
-    put_blocks(um, ok ? nx.code_bits : -1, a.nblk, tid);
-    put_mask_words(um, tid < BM ? um.maskf[tid] : 0.0f, tid, lane);
-  } else {
-    row_offsets(um, nx.n_valid, a.S, a.row_bytes, wave, lane, nx.a_off);
+    if (pre) issue_slab(sm, a, nx, 1, buf_next ^ 1, c, lane);
+    lds_barrier();  // E: the compute waves' pv/pi are written
+    if (next.u < 0) {
+      write_unit<T>(sm, sm.um[par], cur.m, cur.v0, a.V, cur.n_valid, ct, o.reps, o.argmax,
+                    o.reps_f32, o.part);
+      return;
+    }
+    if (pre) {
+      prev = cur;  // written during the next unit's step 1
+    } else {
+      copy_start(sm, a, o, um_next, nx, buf_next, cur, sm.um[par], ct, c, lane);
+    }
+    cur = next;
+    cu = nx;
+    par ^= 1;
+    buf = buf_next;
   }
 }
 
-// Hand-over to the prefetched next unit: its lane data.
-template <typename T>
-__device__ __forceinline__ void take_next(const Args<T>& a, const Next& nx, Lanes& L, int wn, int lane) {
-#pragma unroll
-  for (int i = 0; i < A_LOADS; ++i) L.a_off[i] = nx.a_off[i];
-#pragma unroll
-  for (int nb = 0; nb < NB_PER_WAVE; ++nb) {
-    const int col = nx.v0 + wn * 64 + nb * 32 + (lane & 31);
-    L.bias[nb] = (a.bias != nullptr && col < a.V) ? bits_to_f32<T>(nx.bias_bits[nb]) : 0.0f;
-  }
-}
+// ---- compute waves ----
 
-// Fetch a unit's metadata in place and start its first two slabs (into stages buf,
-// buf ^ 1). On return slab 0 has landed and is visible, slab 1 is in flight and the
-// metadata is published.
-template <typename T>
-__device__ __forceinline__ void start_unit(Smem& sm, const Args<T>& a, UnitMeta& um, int m, int v0,
-                                           int n_valid, Lanes& L, int nk, int buf, int tid, int wave,
-                                           int lane, int wn) {
-  const int code = tid < MBLK + 2 ? block_code(a.list, a.n_blk, m, n_valid, tid) : -1;
-  put_blocks(um, code, a.nblk, tid);
-  if (tid == 0) um.mask_binary = 1;
-  const float mv = tid < BM ? a.rowmask[(int64_t)m * BM + tid] : 0.0f;
-  if (tid < BM) um.maskf[tid] = mv;
-  lds_barrier();
-  row_offsets(um, n_valid, a.S, a.row_bytes, wave, lane, L.a_off);
-  load_bias(a, v0, wn, lane, L.bias);
-  if (nk > 0) {
-    issue_slab(sm, a, L.a_off, n_valid, v0, 0, buf, wave, lane);
-    issue_slab(sm, a, L.a_off, n_valid, v0, 1, buf ^ 1, wave, lane);
-  }
-  put_mask_words(um, mv, tid, lane);
-  if (nk > 0) wait_loads_at_most(slab_loads(n_valid, wave));  // slab 0 landed, slab 1 in flight
-  lds_barrier();
-}
-
-// Mainloop + block epilogue of one unit (vocab tile v0), for a wave with JM blocks.
-// On entry slab 0 of the unit has landed in stage `buf` (and is visible) and slab 1 is
-// in flight or landed in the other stage. On exit, if nx.on, the next unit's slab 0
-// has landed and its slab 1 is in flight; pv/pi hold this wave's blocks' results.
-// Returns the stage of the next unit's slab 0.
+// Mainloop + block epilogue of one unit for a compute wave with JM blocks (JM = 0: the
+// wave only keeps the barrier schedule). Stage buf holds the unit's slab 0.
 template <typename T, int JM>
-__device__ __forceinline__ int run_unit(Smem& sm, const Args<T>& a, const UnitMeta& um,
-                                        const Lanes& L, int n_valid, int v0, int nk, int buf,
-                                        Next& nx, UnitMeta& um_next, int tid, int wave, int lane,
-                                        int wm, int wn) {
+__device__ __forceinline__ void compute_unit(Smem& sm, const UnitMeta& um, int nk, int buf,
+                                             int lane, int wm, int wn) {
   constexpr int JA = JM > 0 ? JM : 1;
   const int l32 = lane & 31, h = lane >> 5;
   f32x16 acc[JA][NB_PER_WAVE];
 #pragma unroll
-  for (int nb = 0; nb < NB_PER_WAVE; ++nb)
+  for (int nb = 0; nb < NB_PER_WAVE; ++nb) {
+    const float bv = um.bias[wn * 64 + nb * 32 + l32];
 #pragma unroll
     for (int j = 0; j < JA; ++j)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) acc[j][nb][i] = L.bias[nb];
+      for (int i = 0; i < 16; ++i) acc[j][nb][i] = bv;
+  }
 
   for (int k = 0; k < nk; ++k) {
     const int cur = buf ^ (k & 1);
-    if (nx.on && k < 3) fetch_step(k, a, nx, um_next, tid, wave, lane, wn);
-    if (k >= a.nk_full) {  // tail / padding slab: clear W past D before use
-      zero_tail(sm, a.row_bytes, k, cur, wave, lane);
-      lds_barrier();
-    }
     if (JM > 0) {
       // Every operand row is (multiple of 32) + l32, so its swizzle key is key(l32):
       // a fragment's LDS index is a per-lane offset plus a compile-time row offset.
       const u32x4* abuf = sm.a[cur] + (wm * 32) * CHUNKS;
       const u32x4* bbuf = sm.b[cur] + (wn * 64) * CHUNKS;
       const int kx = swz_key(l32);
-      // Operand fragments for K step p+1 are read while step p's MFMAs run.
-      u32x4 bf[2][NB_PER_WAVE], af[2][JA];
-      auto read = [&](int p, int slot) {
-        const int off = l32 * CHUNKS + ((h * (CHUNKS / 2) + p) ^ kx);  // lane half h: K chunks 4h..4h+3
+      const int off0 = l32 * CHUNKS;
+      auto chunk = [&](int p) { return off0 + ((h * (CHUNKS / 2) + p) ^ kx); };  // lane half h: K chunks 4h..4h+3
+      // One buffer of operand fragments (the 168-VGPR budget holds the 128 accumulator
+      // registers and 24 more): each fragment for K step p+1 is read right after the
+      // last MFMA of step p that uses it. MFMAs run B-fragment-major, so B fragment 0
+      // frees first, then A fragments 0..JM-1, then B fragment 1.
+      u32x4 bf[NB_PER_WAVE], af[JA];
 #pragma unroll
-        for (int nb = 0; nb < NB_PER_WAVE; ++nb) bf[slot][nb] = bbuf[nb * 32 * CHUNKS + off];
+      for (int nb = 0; nb < NB_PER_WAVE; ++nb) bf[nb] = bbuf[nb * 32 * CHUNKS + chunk(0)];
 #pragma unroll
-        for (int j = 0; j < JM; ++j) af[slot][j] = abuf[j * WAVES_M * 32 * CHUNKS + off];
-      };
-      read(0, 0);
-#pragma unroll
-      for (int p = 0; p < CHUNKS / 2; ++p) {
-        if (p + 1 < CHUNKS / 2) read(p + 1, (p + 1) & 1);
-#pragma unroll
-        for (int j = 0; j < JM; ++j)
-#pragma unroll
-          for (int nb = 0; nb < NB_PER_WAVE; ++nb)
-            Mfma<T>::run(af[p & 1][j], bf[p & 1][nb], acc[j][nb]);
-      }
-      // Schedule: the first step's reads, then each step's MFMAs with the next
-      // step's LDS reads slotted one by one between them.
-      constexpr int NREAD = NB_PER_WAVE + JM;
-      constexpr int NMFMA = NB_PER_WAVE * JM * Mfma<T>::kInsts;
-      __builtin_amdgcn_sched_group_barrier(0x100, NREAD, 0);
+      for (int j = 0; j < JM; ++j) af[j] = abuf[j * WAVES_M * 32 * CHUNKS + chunk(0)];
 #pragma unroll
       for (int p = 0; p < CHUNKS / 2; ++p) {
+        const bool more = p + 1 < CHUNKS / 2;
+        const int cn = chunk(p + 1);
 #pragma unroll
-        for (int i = 0; i < NMFMA; ++i) {
-          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-          if (p + 1 < CHUNKS / 2 && i < NREAD) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        for (int j = 0; j < JM; ++j) Mfma<T>::run(af[j], bf[0], acc[j][0]);
+        if (more) bf[0] = bbuf[cn];
+#pragma unroll
+        for (int j = 0; j < JM; ++j) {
+          Mfma<T>::run(af[j], bf[1], acc[j][1]);
+          if (more) af[j] = abuf[j * WAVES_M * 32 * CHUNKS + cn];
         }
+        if (more) bf[1] = bbuf[32 * CHUNKS + cn];
+      }
+      // Keep that order: reads go right after the MFMA that frees their registers.
+      constexpr int KI = Mfma<T>::kInsts;
+      __builtin_amdgcn_sched_group_barrier(0x100, NB_PER_WAVE + JM, 0);
+#pragma unroll
+      for (int p = 0; p < CHUNKS / 2; ++p) {
+        const bool more = p + 1 < CHUNKS / 2;
+        __builtin_amdgcn_sched_group_barrier(0x008, JM * KI, 0);
+        if (more) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+#pragma unroll
+        for (int j = 0; j < JM; ++j) {
+          __builtin_amdgcn_sched_group_barrier(0x008, KI, 0);
+          if (more) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
+        if (more) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
       }
     }
-    drain_and_sync();
-    // Stage `cur` is free: refill it with the slab two ahead in the stream (this
-    // unit's, or the next unit's first two).
-    const bool own = k + 2 < nk;
-    if (own || nx.on) {
-      uint32_t off[A_LOADS];
-#pragma unroll
-      for (int i = 0; i < A_LOADS; ++i) off[i] = own ? L.a_off[i] : nx.a_off[i];
-      issue_slab(sm, a, off, own ? n_valid : nx.n_valid, own ? v0 : nx.v0, own ? k + 2 : k + 2 - nk,
-                 cur, wave, lane);
-    }
+    lds_barrier();  // B_k: slab k read; slab k+1 landed
   }
 
   // Block epilogue. 32x32 accumulator layout: lane holds column l32, and register
@@ -842,56 +914,40 @@ __device__ __forceinline__ int run_unit(Smem& sm, const Args<T>& a, const UnitMe
       }
     }
   }
-  return buf ^ (nk & 1);
+  lds_barrier();  // E
 }
 
-// Merge the blocks of each batch-row segment of the tile (thread = column) and write
-// reps/argmax for complete segments, or the partial for a segment that continues into
-// the previous M-tile (slot 0) or the next one (slot 1).
 template <typename T>
-__device__ __forceinline__ void write_unit(Smem& sm, const UnitMeta& um, int m, int v0, int V,
-                                           int n_valid, T* reps, int32_t* argmax, float* reps_f32,
-                                           float2* part) {
-  const int tid = threadIdx.x;
-  lds_barrier();  // every block's pv/pi are written
-  if (tid < BN && v0 + tid < V) {
-    const int v = v0 + tid;
-    const int b_prev = um.blk_b[MBLK], b_next = um.blk_b[MBLK + 1];
-    float pvr[MBLK];
-    int pir[MBLK];
-#pragma unroll
-    for (int r = 0; r < MBLK; ++r) {  // all loads first (rows past n_valid are unused)
-      pvr[r] = sm.pv[r][tid];
-      pir[r] = sm.pi[r][tid];
+__device__ void compute_path(Smem& sm, const Args<T>& a, int w, int G, int n_units, int n_mt,
+                             int n_vt, int wave, int lane) {
+  const int nk = a.nk;
+  const int wm = wave / WAVES_N, wn = wave % WAVES_N;
+  Unit cur = unit_of(w, 0, G, n_units, n_mt, n_vt, a.n_blk);
+  if (cur.u < 0) return;
+  lds_barrier();  // S1
+  lds_barrier();  // S2
+  int par = 0, buf = 0;
+  for (int r = 1;; ++r) {
+    const UnitMeta& um = sm.um[par];
+    const int n_valid = cur.n_valid;
+    const int jm = n_valid <= wm ? 0 : min(4, (n_valid - wm + 1) / WAVES_M);
+    switch (jm) {
+      case 0: compute_unit<T, 0>(sm, um, nk, buf, lane, wm, wn); break;
+      case 1: compute_unit<T, 1>(sm, um, nk, buf, lane, wm, wn); break;
+      case 2: compute_unit<T, 2>(sm, um, nk, buf, lane, wm, wn); break;
+      case 3: compute_unit<T, 3>(sm, um, nk, buf, lane, wm, wn); break;
+      default: compute_unit<T, 4>(sm, um, nk, buf, lane, wm, wn); break;
     }
-    float bv = 0.0f;
-    int bi = 0;
-#pragma unroll
-    for (int r = 0; r < MBLK; ++r) {
-      if (r >= n_valid) break;
-      if (pvr[r] > bv) {  // earlier blocks hold lower s: strict '>' keeps them on ties
-        bv = pvr[r];
-        bi = pir[r];
-      }
-      const int b = um.blk_b[r];
-      if (r + 1 == n_valid || um.blk_b[r + 1] != b) {  // the segment of batch row b ends
-        const bool cont_prev = b == um.blk_b[0] && b == b_prev;
-        const bool cont_next = r + 1 == n_valid && b == b_next;
-        if (cont_prev || cont_next) {
-          part[((int64_t)m * 2 + (cont_prev ? 0 : 1)) * V + v] = make_float2(bv, __int_as_float(bi));
-        } else {
-          const int64_t o = (int64_t)b * V + v;
-          const float rv = log1pf(bv);
-          reps[o] = from_f32<T>(rv);
-          if (argmax != nullptr) argmax[o] = bi;
-          if (reps_f32 != nullptr) reps_f32[o] = rv;
-        }
-        bv = 0.0f;
-        bi = 0;
-      }
+    const Unit next = unit_of(w, r, G, n_units, n_mt, n_vt, a.n_blk);
+    if (next.u < 0) return;
+    if (nk < PREFETCH_MIN_NK) {
+      lds_barrier();  // S1
+      lds_barrier();  // S2
     }
+    cur = next;
+    par ^= 1;
+    buf ^= nk & 1;
   }
-  lds_barrier();  // pv/pi are reused by the next unit
 }
 
 template <typename T>
@@ -903,7 +959,6 @@ __global__ __launch_bounds__(NTHREADS, 1) void sparton_fwd_kernel(
   __shared__ Smem sm;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: keep it scalar
-  const int wm = wave / WAVES_N, wn = wave % WAVES_N;
 
   Args<T> a;
   a.H = (const char*)H;
@@ -917,56 +972,19 @@ __global__ __launch_bounds__(NTHREADS, 1) void sparton_fwd_kernel(
   a.row_bytes = D * (int)sizeof(T);
   const int slab_elems = SLAB / (int)sizeof(T);
   a.nk_full = D / slab_elems;
-  a.V = V;
   // At least two slabs per unit (a padding slab contributes zero); none when D == 0,
   // where x = bias * mask and nothing is loaded.
-  const int nk = D == 0 ? 0 : max(2, (int)cdiv(D, slab_elems));
+  a.nk = D == 0 ? 0 : max(2, (int)cdiv(D, slab_elems));
+  a.V = V;
 
   const int n_mt = (a.n_blk + MBLK - 1) / MBLK;
   const int n_units = n_mt * n_vt;
-  const int G = gridDim.x, w = blockIdx.x;
-  int u = unit_at(w, 0, G, n_units);
-  if (u < 0) return;
-  int m, vt;
-  unit_tile(u, n_mt, n_vt, &m, &vt);
-  int n_valid = min(MBLK, a.n_blk - m * MBLK);
-  Lanes L;
-  int par = 0, buf = 0;
-  start_unit(sm, a, sm.um[0], m, vt * BN, n_valid, L, nk, buf, tid, wave, lane, wn);
-
-  for (int r = 1;; ++r) {
-    const int u_next = unit_at(w, r, G, n_units);
-    Next nx;
-    nx.on = false;
-    int vt_next = 0;
-    if (u_next >= 0) {
-      unit_tile(u_next, n_mt, n_vt, &nx.m, &vt_next);
-      nx.v0 = vt_next * BN;
-      nx.n_valid = min(MBLK, a.n_blk - nx.m * MBLK);
-      nx.on = nk >= 4;
-    }
-    const int v0 = vt * BN;
-    UnitMeta& um = sm.um[par];
-    UnitMeta& um_next = sm.um[par ^ 1];
-    const int jm = n_valid <= wm ? 0 : min(4, (n_valid - wm + 1) / WAVES_M);
-    switch (jm) {
-      case 0: buf = run_unit<T, 0>(sm, a, um, L, n_valid, v0, nk, buf, nx, um_next, tid, wave, lane, wm, wn); break;
-      case 1: buf = run_unit<T, 1>(sm, a, um, L, n_valid, v0, nk, buf, nx, um_next, tid, wave, lane, wm, wn); break;
-      case 2: buf = run_unit<T, 2>(sm, a, um, L, n_valid, v0, nk, buf, nx, um_next, tid, wave, lane, wm, wn); break;
-      case 3: buf = run_unit<T, 3>(sm, a, um, L, n_valid, v0, nk, buf, nx, um_next, tid, wave, lane, wm, wn); break;
-      default: buf = run_unit<T, 4>(sm, a, um, L, n_valid, v0, nk, buf, nx, um_next, tid, wave, lane, wm, wn); break;
-    }
-    write_unit<T>(sm, um, m, v0, V, n_valid, reps, argmax, reps_f32, part);
-    if (u_next < 0) break;
-    m = nx.m;
-    vt = vt_next;
-    n_valid = nx.n_valid;
-    par ^= 1;
-    if (nx.on) {
-      take_next(a, nx, L, wn, lane);
-    } else {
-      start_unit(sm, a, sm.um[par], m, vt * BN, n_valid, L, nk, buf, tid, wave, lane, wn);
-    }
+  if (wave < COMPUTE_WAVES) {
+    compute_path<T>(sm, a, blockIdx.x, gridDim.x, n_units, n_mt, n_vt, wave, lane);
+  } else {
+    Outputs<T> o{reps, argmax, reps_f32, part};
+    copy_path<T>(sm, a, o, blockIdx.x, gridDim.x, n_units, n_mt, n_vt, tid - 64 * COMPUTE_WAVES,
+                 wave - COMPUTE_WAVES, lane);
   }
 }
 

@@ -94,6 +94,8 @@ PERSISTENT_CASES = [
     (("fp32", 3, 70, 132, 900, True, "frac"), 5),       # nk 5 (K tail), fractional mask
     (("fp16", 5, 100, 200, 1500, False, "gaps"), 7),    # nk 4 (K tail)
     (("bf16", 37, 40, 256, 700, True, "int64"), 13),    # nk 4, tiles spanning batch rows
+    (("bf16", 6, 200, 296, 3000, True, "gaps"), 5),     # nk 5 (K tail), metadata prefetched
+    (("fp16", 4, 128, 1024, 2000, False, "frac"), 6),   # nk 16, no bias, fractional mask
 ]
 
 
