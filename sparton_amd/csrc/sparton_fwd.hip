@@ -8,30 +8,31 @@
 //     reps     = log1p(M)                                        :159-161 (log(1+x) there)
 // The [B,S,V] logits never reach HBM.
 //
-// Packing. Positions are grouped in 32-row blocks (b, j) = rows 32j..32j+31 of batch
-// row b. A block whose mask is all zero contributes x = 0, which never beats the
-// initial 0, so it is dropped. The plan pass lists the remaining ("active") blocks in
-// (b, j) order, and the main kernel multiplies them eight at a time: M-tile m holds
-// active blocks 8m..8m+7, i.e. 256 rows that may belong to several batch rows. Every
-// tile except the last is full, so each decoder tile loaded from memory is used for
-// 256 live rows instead of one batch row's (often partly padded) 256 positions.
+// Packing. Positions are grouped 16 at a time: group (b, j) = positions 16j..16j+15 of
+// batch row b. A group whose mask is all zero contributes x = 0, which never beats the
+// initial 0, so it is dropped. The plan pass lists the remaining ("active") groups in
+// (b, j) order, and the main kernel multiplies them sixteen at a time: M-tile m holds
+// active groups 16m..16m+15, i.e. 256 rows that may belong to several batch rows.
+// Every tile except the last is full, so each decoder tile loaded from memory is used
+// for 256 live rows instead of one batch row's (often partly padded) 256 positions,
+// and a batch row wastes less than 16 rows of padding.
 //
 // Main kernel. A "unit" is one M-tile x one vocab tile of BN columns. The grid is
 // persistent (one workgroup per CU) and each workgroup walks its units in rounds; for
 // each it computes the 256 x BN logit tile with bf16/fp16 (or fp32) MFMA, K = D
 // streamed through two LDS stages. The K slabs of all its units form one stream, and
-// the next unit's metadata (block list, row mask, row offsets, bias) is fetched during
+// the next unit's metadata (group list, row mask, row offsets, bias) is fetched during
 // the current unit's first K steps, so a unit starts while the previous one finishes.
 // Eight compute waves run the MFMAs and the epilogue; four copy waves issue all copies
-// and write the results. The epilogue folds each 32-row block into a per-column (max, argmax),
-// merges consecutive blocks of the same batch row in s order (larger value; on ties
-// the lower s, which is the earlier block), and per batch-row segment either writes
+// and write the results. The epilogue folds each group into a per-column (max, argmax),
+// merges consecutive groups of the same batch row in s order (larger value; on ties
+// the lower s, which is the earlier group), and per batch-row segment either writes
 // reps/argmax (segment complete in this tile) or, when the segment continues into a
 // neighbouring tile, writes the partial (max, argmax) to the workspace.
 //
-// Fixup kernel. For each batch row whose blocks span several M-tiles it merges those
+// Fixup kernel. For each batch row whose groups span several M-tiles it merges those
 // partials in tile order (= s order) and writes reps/argmax; for a batch row with no
-// active block it writes reps = 0, argmax = 0.
+// active group it writes reps = 0, argmax = 0.
 //
 // Data movement: K slabs of 128 bytes per row go straight from global memory into
 // LDS (global_load_lds_dwordx4, no VGPR staging). LDS rows are 128 bytes with the
@@ -66,7 +67,9 @@ constexpr int COMPUTE_WAVES = WAVES_M * WAVES_N;
 constexpr int COPY_WAVES = 4;
 constexpr int COPY_THREADS = 64 * COPY_WAVES;
 constexpr int NTHREADS = 64 * (COMPUTE_WAVES + COPY_WAVES);
-constexpr int MBLK = BM / 32;        // 32-row blocks per M-tile (8)
+constexpr int MBLK = BM / 32;        // 32-row MFMA blocks per M-tile (8)
+constexpr int GROUP = 16;            // positions are packed into M-tiles 16 at a time
+constexpr int NGRP = BM / GROUP;     // groups per M-tile (16); MFMA block j = groups 2j, 2j+1
 constexpr int NB_PER_WAVE = BN / WAVES_N / 32;     // 2
 constexpr int SLAB = 128;            // bytes of K per row per pipeline stage
 constexpr int CHUNKS = SLAB / 16;    // 16-byte chunks per row slab (8)
@@ -75,28 +78,28 @@ constexpr int A_LOADS = BM / ROWS_PER_LOAD / COPY_WAVES;  // wave-wide copies pe
 constexpr int B_LOADS = BN / ROWS_PER_LOAD / COPY_WAVES;  // and for B (8)
 // The copy threads handle one tile row / one column each.
 static_assert(BM == COPY_THREADS && BN == COPY_THREADS, "one copy thread per row and column");
-constexpr int MAX_S = 16384;         // positions per batch row (512 blocks)
+constexpr int MAX_S = 16384;         // positions per batch row (1024 groups)
 constexpr int PLAN_THREADS = 1024;
 
 // ---- workspace ------------------------------------------------------------------
 
 // Device scratch of one launch, carved from the caller's workspace (256-byte aligned
-// sections). nblk = blocks per batch row, n_mt_max = M-tiles if every block is active.
+// sections). ngrp = groups per batch row, n_mt_max = M-tiles if every group is active.
 struct Work {
-  int* meta;          // [0] active blocks
-  int* count;         // [B] active blocks per batch row
-  int* first;         // [B] index of its first active block in `list`
-  uint8_t* flag;      // [B][nblk] 1 = block has a nonzero mask entry
-  int* list;          // [B*nblk] active blocks as b * nblk + j, in (b, j) order
+  int* meta;          // [0] active groups
+  int* count;         // [B] active groups per batch row
+  int* first;         // [B] index of its first active group in `list`
+  uint8_t* flag;      // [B][ngrp] 1 = group has a nonzero mask entry
+  int* list;          // [B*ngrp] active groups as b * ngrp + j, in (b, j) order
   float2* part;       // [n_mt_max][2][V] partial (max, argmax bits) of edge segments
   float* rowmask;     // [n_mt_max * 256] mask of each tile row, in list order (0 past S
-                      // and past the last active block of the last tile)
+                      // and past the last active group of the last tile)
   size_t total;
 };
 
 static Work carve(void* base, int64_t B, int64_t S, int64_t V) {
-  const int64_t nblk = cdiv(S, 32);
-  const int64_t n_mt_max = cdiv(B * nblk, 8);
+  const int64_t ngrp = cdiv(S, GROUP);
+  const int64_t n_mt_max = cdiv(B * ngrp, NGRP);
   char* p = (char*)base;
   size_t off = 0;
   auto take = [&](size_t bytes) {
@@ -108,8 +111,8 @@ static Work carve(void* base, int64_t B, int64_t S, int64_t V) {
   w.meta = (int*)take(16);
   w.count = (int*)take((size_t)B * 4);
   w.first = (int*)take((size_t)B * 4);
-  w.flag = (uint8_t*)take((size_t)(B * nblk));
-  w.list = (int*)take((size_t)(B * nblk) * 4);
+  w.flag = (uint8_t*)take((size_t)(B * ngrp));
+  w.list = (int*)take((size_t)(B * ngrp) * 4);
   w.part = (float2*)take((size_t)(n_mt_max * 2 * V) * sizeof(float2));
   w.rowmask = (float*)take((size_t)(n_mt_max * 256) * sizeof(float));
   w.total = off;
@@ -118,13 +121,26 @@ static Work carve(void* base, int64_t B, int64_t S, int64_t V) {
 
 // ---- plan -------------------------------------------------------------------------
 
-// Which 32-row blocks of batch row b have a nonzero mask entry (one wave). Positions
-// are read 8 x 64 at a time, all loads issued before the ballots.
+// Flags of the GROUP-position groups j .. j+3 that 64 consecutive positions (ballot
+// `bal`, lane = position) cover: lane q < 4 gets group j + q's flag in *on; returns how
+// many of them are active (the same in every lane).
+__device__ __forceinline__ int group_flags(uint64_t bal, int j, int ngrp, int lane, bool* on) {
+  static_assert(GROUP == 16, "four groups per 64-position ballot");
+  int n = 0;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) n += (j + q < ngrp && ((bal >> (16 * q)) & 0xffffull) != 0) ? 1 : 0;
+  const int q = lane & 3;
+  *on = lane < 4 && j + q < ngrp && ((bal >> (16 * q)) & 0xffffull) != 0;
+  return n;
+}
+
+// Which groups of batch row b have a nonzero mask entry (one wave). Positions are read
+// 8 x 64 at a time, all loads issued before the ballots.
 __device__ __forceinline__ void plan_row(const void* __restrict__ mask, int mask_dtype, int b,
-                                         int S, int nblk, uint8_t* __restrict__ flag,
+                                         int S, int ngrp, uint8_t* __restrict__ flag,
                                          int* __restrict__ count, int lane) {
   int n = 0;
-  for (int t0 = 0; t0 < nblk * 32; t0 += 8 * 64) {
+  for (int t0 = 0; t0 < ngrp * GROUP; t0 += 8 * 64) {
     bool nz[8];
     int64_t off[8];
 #pragma unroll
@@ -135,14 +151,11 @@ __device__ __forceinline__ void plan_row(const void* __restrict__ mask, int mask
     for (int u = 0; u < 8; ++u) nz[u] = t0 + u * 64 + lane < S && mv[u] != 0.0f;
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
-      const int j = (t0 + u * 64) / 32;
-      if (j >= nblk) break;
-      const uint64_t bal = __ballot(nz[u]);
-      const int lo = (bal & 0xffffffffull) != 0 ? 1 : 0;
-      const int hi = (j + 1 < nblk && (bal >> 32) != 0) ? 1 : 0;
-      if (lane == 0) flag[(int64_t)b * nblk + j] = (uint8_t)lo;
-      if (lane == 1 && j + 1 < nblk) flag[(int64_t)b * nblk + j + 1] = (uint8_t)hi;
-      n += lo + hi;
+      const int j = (t0 + u * 64) / GROUP;
+      if (j >= ngrp) break;
+      bool on;
+      n += group_flags(__ballot(nz[u]), j, ngrp, lane, &on);
+      if (lane < 4 && j + lane < ngrp) flag[(int64_t)b * ngrp + j + lane] = (uint8_t)(on ? 1 : 0);
     }
   }
   if (lane == 0) count[b] = n;
@@ -150,15 +163,15 @@ __device__ __forceinline__ void plan_row(const void* __restrict__ mask, int mask
 
 // One wave per batch row.
 __global__ __launch_bounds__(256) void fwd_plan_rows_kernel(const void* __restrict__ mask,
-                                                            int mask_dtype, int B, int S, int nblk,
+                                                            int mask_dtype, int B, int S, int ngrp,
                                                             uint8_t* __restrict__ flag,
                                                             int* __restrict__ count) {
   const int b = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (b < B) plan_row(mask, mask_dtype, b, S, nblk, flag, count, threadIdx.x & 63);
+  if (b < B) plan_row(mask, mask_dtype, b, S, ngrp, flag, count, threadIdx.x & 63);
 }
 
-// Exclusive scan of the per-row counts, then the block list (one workgroup).
-__device__ __forceinline__ void plan_list(int B, int nblk, const uint8_t* __restrict__ flag,
+// Exclusive scan of the per-row counts, then the group list (one workgroup).
+__device__ __forceinline__ void plan_list(int B, int ngrp, const uint8_t* __restrict__ flag,
                                           const int* __restrict__ count, int* __restrict__ first,
                                           int* __restrict__ list, int* __restrict__ meta) {
   __shared__ int wsum[PLAN_THREADS / 64];
@@ -186,59 +199,59 @@ __device__ __forceinline__ void plan_list(int B, int nblk, const uint8_t* __rest
     __syncthreads();
   }
   if (tid == 0) meta[0] = carry;
-  // One wave per batch row: lane j takes block j (64 at a time); its slot is the row
-  // start plus the active blocks before it (a ballot prefix), so the list stays in
+  // One wave per batch row: lane j takes group j (64 at a time); its slot is the row
+  // start plus the active groups before it (a ballot prefix), so the list stays in
   // (b, j) order.
   const int nw = PLAN_THREADS / 64;
   for (int b = wave; b < B; b += nw) {
     int k = first[b];
-    const uint8_t* f = flag + (int64_t)b * nblk;
-    for (int j0 = 0; j0 < nblk; j0 += 64) {
+    const uint8_t* f = flag + (int64_t)b * ngrp;
+    for (int j0 = 0; j0 < ngrp; j0 += 64) {
       const int j = j0 + lane;
-      const bool on = j < nblk && f[j] != 0;
+      const bool on = j < ngrp && f[j] != 0;
       const uint64_t bal = __ballot(on);
-      if (on) list[k + __popcll(bal & ((1ull << lane) - 1ull))] = b * nblk + j;
+      if (on) list[k + __popcll(bal & ((1ull << lane) - 1ull))] = b * ngrp + j;
       k += __popcll(bal);
     }
   }
 }
 
 __global__ __launch_bounds__(PLAN_THREADS) void fwd_plan_list_kernel(
-    int B, int nblk, const uint8_t* __restrict__ flag, const int* __restrict__ count,
+    int B, int ngrp, const uint8_t* __restrict__ flag, const int* __restrict__ count,
     int* __restrict__ first, int* __restrict__ list, int* __restrict__ meta) {
-  plan_list(B, nblk, flag, count, first, list, meta);
+  plan_list(B, ngrp, flag, count, first, list, meta);
 }
 
-// Row mask in list order: tile row t = 32 e + r is position 32 j + r of batch row b,
-// where list[e] = b * nblk + j; rows of entries past the last active block are 0.
+// Row mask in list order: tile row t = 16 e + r is position 16 j + r of batch row b,
+// where list[e] = b * ngrp + j; rows of entries past the last active group are 0.
 __device__ __forceinline__ void fill_rowmask(const void* __restrict__ mask, int mask_dtype, int S,
-                                             int nblk, int n_blk, const int* __restrict__ list,
+                                             int ngrp, int n_grp, const int* __restrict__ list,
                                              float* __restrict__ rowmask, int t) {
-  const int e = t >> 5;
+  const int e = t / GROUP;
   float v = 0.0f;
-  if (e < n_blk) {
+  if (e < n_grp) {
     const int code = list[e];
-    const int b = code / nblk;
-    const int s = (code - b * nblk) * 32 + (t & 31);
+    const int b = code / ngrp;
+    const int s = (code - b * ngrp) * GROUP + (t % GROUP);
     if (s < S) v = load_mask(mask, mask_dtype, (int64_t)b * S + s);
   }
   rowmask[t] = v;
 }
 
 __global__ __launch_bounds__(256) void fwd_plan_rowmask_kernel(
-    const void* __restrict__ mask, int mask_dtype, int S, int nblk, const int* __restrict__ meta,
+    const void* __restrict__ mask, int mask_dtype, int S, int ngrp, const int* __restrict__ meta,
     const int* __restrict__ list, float* __restrict__ rowmask) {
-  const int n_blk = meta[0];
+  const int n_grp = meta[0];
   const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (t < (int64_t)(n_blk + MBLK - 1) / MBLK * BM)
-    fill_rowmask(mask, mask_dtype, S, nblk, n_blk, list, rowmask, (int)t);
+  if (t < (int64_t)(n_grp + NGRP - 1) / NGRP * BM)
+    fill_rowmask(mask, mask_dtype, S, ngrp, n_grp, list, rowmask, (int)t);
 }
 
-// Both plan steps in one workgroup, for small batches (B * nblk <= PLAN_FUSED_MAX):
+// Both plan steps in one workgroup, for small batches (B * ngrp <= PLAN_FUSED_MAX):
 // flags and counts stay in LDS, one launch instead of two.
-constexpr int PLAN_FUSED_MAX = 1 << 14;  // blocks (B * nblk); also bounds B
+constexpr int PLAN_FUSED_MAX = 1 << 14;  // groups (B * ngrp); also bounds B
 __global__ __launch_bounds__(PLAN_THREADS) void fwd_plan_small_kernel(
-    const void* __restrict__ mask, int mask_dtype, int B, int S, int nblk, int* __restrict__ count,
+    const void* __restrict__ mask, int mask_dtype, int B, int S, int ngrp, int* __restrict__ count,
     int* __restrict__ first, int* __restrict__ list, int* __restrict__ meta,
     float* __restrict__ rowmask) {
   __shared__ uint8_t fl[PLAN_FUSED_MAX];
@@ -250,7 +263,7 @@ __global__ __launch_bounds__(PLAN_THREADS) void fwd_plan_small_kernel(
   constexpr int NW = PLAN_THREADS / 64;
   for (int b = wave; b < B; b += NW) {
     int n = 0;
-    for (int t0 = 0; t0 < nblk * 32; t0 += 8 * 64) {
+    for (int t0 = 0; t0 < ngrp * GROUP; t0 += 8 * 64) {
       bool nz[8];
       int64_t off[8];
 #pragma unroll
@@ -261,14 +274,11 @@ __global__ __launch_bounds__(PLAN_THREADS) void fwd_plan_small_kernel(
       for (int u = 0; u < 8; ++u) nz[u] = t0 + u * 64 + lane < S && mv[u] != 0.0f;
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
-        const int j = (t0 + u * 64) / 32;
-        if (j >= nblk) break;
-        const uint64_t bal = __ballot(nz[u]);
-        const int lo = (bal & 0xffffffffull) != 0 ? 1 : 0;
-        const int hi = (j + 1 < nblk && (bal >> 32) != 0) ? 1 : 0;
-        if (lane == 0) fl[b * nblk + j] = (uint8_t)lo;
-        if (lane == 1 && j + 1 < nblk) fl[b * nblk + j + 1] = (uint8_t)hi;
-        n += lo + hi;
+        const int j = (t0 + u * 64) / GROUP;
+        if (j >= ngrp) break;
+        bool on;
+        n += group_flags(__ballot(nz[u]), j, ngrp, lane, &on);
+        if (lane < 4 && j + lane < ngrp) fl[b * ngrp + j + lane] = (uint8_t)(on ? 1 : 0);
       }
     }
     if (lane == 0) cnt[b] = n;
@@ -301,14 +311,14 @@ __global__ __launch_bounds__(PLAN_THREADS) void fwd_plan_small_kernel(
   if (tid == 0) meta[0] = carry;
   for (int b = wave; b < B; b += NW) {
     int k = cnt[b];
-    for (int j0 = 0; j0 < nblk; j0 += 64) {
+    for (int j0 = 0; j0 < ngrp; j0 += 64) {
       const int j = j0 + lane;
-      const bool on = j < nblk && fl[b * nblk + j] != 0;
+      const bool on = j < ngrp && fl[b * ngrp + j] != 0;
       const uint64_t bal = __ballot(on);
       if (on) {
         const int e = k + __popcll(bal & ((1ull << lane) - 1ull));
-        list[e] = b * nblk + j;
-        lst[e] = b * nblk + j;
+        list[e] = b * ngrp + j;
+        lst[e] = b * ngrp + j;
       }
       k += __popcll(bal);
     }
@@ -316,17 +326,17 @@ __global__ __launch_bounds__(PLAN_THREADS) void fwd_plan_small_kernel(
   __syncthreads();  // lst is complete
   // Row mask in list order, RM rows per thread with their mask loads in flight together.
   constexpr int RM = 8;
-  const int n_blk = carry;
-  const int n_rows = (n_blk + MBLK - 1) / MBLK * BM;
+  const int n_grp = carry;
+  const int n_rows = (n_grp + NGRP - 1) / NGRP * BM;
   for (int t0 = tid; t0 < n_rows; t0 += RM * PLAN_THREADS) {
     int64_t off[RM];
     bool ok[RM];
 #pragma unroll
     for (int u = 0; u < RM; ++u) {
-      const int t = t0 + u * PLAN_THREADS, e = t >> 5;
-      const int code = (t < n_rows && e < n_blk) ? lst[e] : -1;
-      const int bb = code >= 0 ? code / nblk : 0;
-      const int ss = code >= 0 ? (code - bb * nblk) * 32 + (t & 31) : S;
+      const int t = t0 + u * PLAN_THREADS, e = t / GROUP;
+      const int code = (t < n_rows && e < n_grp) ? lst[e] : -1;
+      const int bb = code >= 0 ? code / ngrp : 0;
+      const int ss = code >= 0 ? (code - bb * ngrp) * GROUP + (t % GROUP) : S;
       ok[u] = ss < S;
       off[u] = ok[u] ? (int64_t)bb * S + ss : 0;
     }
@@ -347,9 +357,9 @@ __global__ __launch_bounds__(PLAN_THREADS) void fwd_plan_small_kernel(
 struct __align__(16) UnitMeta {
   float maskf[BM];           // mask of the tile's rows (0 past S or past the last block)
   int maskw[BM];             // the same as an AND mask for 0/1 masks: ~31 (kept) or 0
-  int blk_b[MBLK + 2];       // batch row of each block; [MBLK], [MBLK+1]: rows of the
-                             // blocks just before / after the tile (-1 if none)
-  int blk_s[MBLK];           // first position of each block (32 j)
+  int grp_b[NGRP + 2];       // batch row of each group; [NGRP], [NGRP+1]: rows of the
+                             // groups just before / after the tile (-1 if none)
+  int grp_s[NGRP];           // first position of each group (16 j)
   int mask_binary;           // every maskf value is 0 or 1
   float bias[BN];            // bias of the tile's columns (0 past V or without bias)
 };
@@ -357,8 +367,8 @@ struct __align__(16) UnitMeta {
 struct Smem {
   u32x4 a[2][BM * CHUNKS];   // [stage][row * 8 + (chunk ^ f(row))]
   u32x4 b[2][BN * CHUNKS];
-  float pv[MBLK][BN];        // per block, per column: (max, argmax) of the block's rows
-  int pi[MBLK][BN];
+  int key[NGRP][BN];         // per group, per column: the epilogue key of the group's
+                             // maximum (value and row; 0 when no value is positive)
   UnitMeta um[2];
 };
 
@@ -441,8 +451,8 @@ struct Args {
   const T* bias;
   const float* rowmask;  // [n_mt * BM] mask of each tile row
   const int* list;
-  int n_blk;          // active blocks
-  int nblk;           // blocks per batch row
+  int n_grp;          // active groups
+  int ngrp;           // groups per batch row
   int S;
   int row_bytes;      // D * sizeof(T)
   int nk_full;        // slabs lying entirely inside the row
@@ -458,20 +468,21 @@ struct CopyUnit {
 
 // ---- unit metadata (run by the copy threads, ct = 0..255; the ones named take part) ----
 
-// Copy threads 0..MBLK+1: the tile's list entry (b * nblk + j), or -1.
-__device__ __forceinline__ int block_entry(int m, int ct) {
-  return ct < MBLK ? m * MBLK + ct : (ct == MBLK ? m * MBLK - 1 : m * MBLK + MBLK);
+// Copy threads 0..NGRP+1: the tile's list entry (b * ngrp + j), or -1; threads NGRP
+// and NGRP+1 take the entries just before and after the tile.
+__device__ __forceinline__ int group_entry(int m, int ct) {
+  return ct < NGRP ? m * NGRP + ct : (ct == NGRP ? m * NGRP - 1 : m * NGRP + NGRP);
 }
-__device__ __forceinline__ int block_code(const int* list, int n_blk, int m, int n_valid, int ct) {
-  const int e = block_entry(m, ct);
-  const bool ok = e >= 0 && e < n_blk && (ct >= MBLK || ct < n_valid);
+__device__ __forceinline__ int group_code(const int* list, int n_grp, int m, int n_valid, int ct) {
+  const int e = group_entry(m, ct);
+  const bool ok = e >= 0 && e < n_grp && (ct >= NGRP || ct < n_valid);
   return ok ? list[e] : -1;
 }
 
-__device__ __forceinline__ void put_blocks(UnitMeta& um, int code, int nblk, int ct) {
-  if (ct < MBLK + 2) {
-    um.blk_b[ct] = code >= 0 ? code / nblk : -1;
-    if (ct < MBLK) um.blk_s[ct] = code >= 0 ? (code % nblk) * 32 : 0;
+__device__ __forceinline__ void put_groups(UnitMeta& um, int code, int ngrp, int ct) {
+  if (ct < NGRP + 2) {
+    um.grp_b[ct] = code >= 0 ? code / ngrp : -1;
+    if (ct < NGRP) um.grp_s[ct] = code >= 0 ? (code % ngrp) * GROUP : 0;
   }
 }
 
@@ -482,8 +493,8 @@ __device__ __forceinline__ void put_mask_words(UnitMeta& um, float mv, int ct, i
   if (__ballot(mv != 0.0f && mv != 1.0f) != 0 && lane == 0) um.mask_binary = 0;
 }
 
-// Per copy lane (after put_blocks is visible): the byte offsets of its A rows. Rows of
-// blocks past n_valid get some valid row (their copies are skipped); positions past S
+// Per copy lane (after put_groups is visible): the byte offsets of its A rows. Rows of
+// groups past n_valid get some valid row (their copies are skipped); positions past S
 // any valid position of the row.
 __device__ __forceinline__ void row_offsets(const UnitMeta& um, int n_valid, int S, int row_bytes,
                                             int c, int lane, uint32_t* a_off) {
@@ -491,9 +502,9 @@ __device__ __forceinline__ void row_offsets(const UnitMeta& um, int n_valid, int
   for (int i = 0; i < A_LOADS; ++i) {
     const int grp = i * COPY_WAVES + c;
     const int row = grp * ROWS_PER_LOAD + (lane >> 3);
-    const int r = min(row >> 5, n_valid - 1);
-    const int s = min(um.blk_s[r] + (row & 31), S - 1);
-    a_off[i] = (uint32_t)(((int64_t)um.blk_b[r] * S + s) * row_bytes) + lane_chunk(row, lane);
+    const int g = min(row / GROUP, n_valid - 1);
+    const int s = min(um.grp_s[g] + row % GROUP, S - 1);
+    a_off[i] = (uint32_t)(((int64_t)um.grp_b[g] * S + s) * row_bytes) + lane_chunk(row, lane);
   }
 }
 
@@ -520,17 +531,17 @@ template <> __device__ __forceinline__ float bits_to_f32<float>(uint32_t x) { re
 
 // Issue the direct global -> LDS copies of K slab k of a unit into stage buf. Copy
 // wave c, copy i covers the 8-row group g = i * COPY_WAVES + c (rows 8g..8g+7 of the
-// tile, in block g / 4); lane L lands at LDS chunk g*64 + L. A chunk past the row end
+// tile, in group g / 2); lane L lands at LDS chunk g*64 + L. A chunk past the row end
 // (tail or padding slabs) re-reads the row's first chunk -- valid, finite data inside
 // the row, so nothing outside H or W is read -- and its W copy is zeroed by zero_tail()
 // before use (a zero W times a finite H adds exactly 0). W rows past V re-read row V-1
-// (never stored); A copies of blocks past the last active one (n_valid) are skipped.
+// (never stored); A copies of groups past the last active one (n_valid) are skipped.
 template <typename T>
 __device__ __forceinline__ void issue_slab(Smem& sm, const Args<T>& a, const CopyUnit& cu, int k,
                                            int buf, int c, int lane) {
   const uint32_t kb = (uint32_t)k * SLAB;
   const bool tail = k >= a.nk_full;
-  const int a_groups = cu.n_valid * (32 / ROWS_PER_LOAD);
+  const int a_groups = cu.n_valid * (GROUP / ROWS_PER_LOAD);
 #pragma unroll
   for (int i = 0; i < A_LOADS; ++i) {
     const int grp = i * COPY_WAVES + c;
@@ -597,7 +608,7 @@ struct Unit {
   int u, m, v0, n_valid;
 };
 __device__ __forceinline__ Unit unit_of(int w, int r, int G, int n_units, int n_mt, int n_vt,
-                                        int n_blk) {
+                                        int n_grp) {
   Unit x;
   x.u = unit_at(w, r, G, n_units);
   x.m = 0;
@@ -607,43 +618,42 @@ __device__ __forceinline__ Unit unit_of(int w, int r, int G, int n_units, int n_
     int vt;
     unit_tile(x.u, n_mt, n_vt, &x.m, &vt);
     x.v0 = vt * BN;
-    x.n_valid = min(MBLK, n_blk - x.m * MBLK);
+    x.n_valid = min(NGRP, n_grp - x.m * NGRP);
   }
   return x;
 }
 
 // ---- copy waves ----
 
-// Merge the blocks of each batch-row segment of the tile (copy thread = column) and
+// Merge the groups of each batch-row segment of the tile (copy thread = column) and
 // write reps/argmax for complete segments, or the partial for a segment that continues
-// into the previous M-tile (slot 0) or the next one (slot 1).
+// into the previous M-tile (slot 0) or the next one (slot 1). A group's key holds its
+// maximum x (5 low mantissa bits cleared) and its row r in the 32-row block (as
+// 31 - r); the row's position is the group's first position plus r mod 16.
 template <typename T>
 __device__ __forceinline__ void write_unit(const Smem& sm, const UnitMeta& um, int m, int v0, int V,
                                            int n_valid, int ct, T* reps, int32_t* argmax,
                                            float* reps_f32, float2* part) {
   if (v0 + ct >= V) return;
   const int v = v0 + ct;
-  const int b_prev = um.blk_b[MBLK], b_next = um.blk_b[MBLK + 1];
-  float pvr[MBLK];
-  int pir[MBLK];
+  const int b_prev = um.grp_b[NGRP], b_next = um.grp_b[NGRP + 1];
+  int kr[NGRP];
 #pragma unroll
-  for (int r = 0; r < MBLK; ++r) {  // all loads first (rows past n_valid are unused)
-    pvr[r] = sm.pv[r][ct];
-    pir[r] = sm.pi[r][ct];
-  }
+  for (int g = 0; g < NGRP; ++g) kr[g] = sm.key[g][ct];  // all loads first (groups past n_valid are unused)
   float bv = 0.0f;
   int bi = 0;
 #pragma unroll
-  for (int r = 0; r < MBLK; ++r) {
-    if (r >= n_valid) break;
-    if (pvr[r] > bv) {  // earlier blocks hold lower s: strict '>' keeps them on ties
-      bv = pvr[r];
-      bi = pir[r];
+  for (int g = 0; g < NGRP; ++g) {
+    if (g >= n_valid) break;
+    const float x = __int_as_float(kr[g] & ~31);
+    if (x > bv) {  // earlier groups hold lower s: strict '>' keeps them on ties
+      bv = x;
+      bi = um.grp_s[g] + ((31 - (kr[g] & 31)) & (GROUP - 1));
     }
-    const int b = um.blk_b[r];
-    if (r + 1 == n_valid || um.blk_b[r + 1] != b) {  // the segment of batch row b ends
-      const bool cont_prev = b == um.blk_b[0] && b == b_prev;
-      const bool cont_next = r + 1 == n_valid && b == b_next;
+    const int b = um.grp_b[g];
+    if (g + 1 == n_valid || um.grp_b[g + 1] != b) {  // the segment of batch row b ends
+      const bool cont_prev = b == um.grp_b[0] && b == b_prev;
+      const bool cont_next = g + 1 == n_valid && b == b_next;
       if (cont_prev || cont_next) {
         part[((int64_t)m * 2 + (cont_prev ? 0 : 1)) * V + v] = make_float2(bv, __int_as_float(bi));
       } else {
@@ -674,11 +684,11 @@ __device__ __forceinline__ void copy_start(Smem& sm, const Args<T>& a, const Out
                                            UnitMeta& um, CopyUnit& cu, int buf,
                                            const Unit& prev, const UnitMeta& um_prev, int ct,
                                            int c, int lane) {
-  const int code = ct < MBLK + 2 ? block_code(a.list, a.n_blk, cu.m, cu.n_valid, ct) : -1;
+  const int code = ct < NGRP + 2 ? group_code(a.list, a.n_grp, cu.m, cu.n_valid, ct) : -1;
   const float mv = a.rowmask[(int64_t)cu.m * BM + ct];
   const int col = cu.v0 + ct;
   const float bv = (a.bias != nullptr && col < a.V) ? to_f32(a.bias[col]) : 0.0f;
-  put_blocks(um, code, a.nblk, ct);
+  put_groups(um, code, a.ngrp, ct);
   um.maskf[ct] = mv;
   um.bias[ct] = bv;
   if (ct == 0) um.mask_binary = 1;
@@ -704,7 +714,7 @@ template <typename T>
 __device__ void copy_path(Smem& sm, const Args<T>& a, const Outputs<T>& o, int w, int G,
                           int n_units, int n_mt, int n_vt, int ct, int c, int lane) {
   const int nk = a.nk;
-  Unit cur = unit_of(w, 0, G, n_units, n_mt, n_vt, a.n_blk);
+  Unit cur = unit_of(w, 0, G, n_units, n_mt, n_vt, a.n_grp);
   if (cur.u < 0) return;
   Unit prev;
   prev.u = -1;
@@ -716,7 +726,7 @@ __device__ void copy_path(Smem& sm, const Args<T>& a, const Outputs<T>& o, int w
   copy_start(sm, a, o, sm.um[0], cu, buf, prev, sm.um[1], ct, c, lane);
 
   for (int r = 1;; ++r) {
-    const Unit next = unit_of(w, r, G, n_units, n_mt, n_vt, a.n_blk);
+    const Unit next = unit_of(w, r, G, n_units, n_mt, n_vt, a.n_grp);
     const bool pre = next.u >= 0 && nk >= PREFETCH_MIN_NK;
     UnitMeta& um_next = sm.um[par ^ 1];
     const int buf_next = buf ^ (nk & 1);
@@ -739,13 +749,13 @@ __device__ void copy_path(Smem& sm, const Args<T>& a, const Outputs<T>& o, int w
           if (ct == 0) um_next.mask_binary = 1;
           __builtin_amdgcn_global_load_lds((const void*)(a.rowmask + (int64_t)nx.m * BM + ct),
                                            (lds_void*)&um_next.maskf[c * 64], 4, 0, 0);
-          if (ct < MBLK + 2)
-            code_bits = a.list[min(max(block_entry(nx.m, ct), 0), a.n_blk - 1)];
+          if (ct < NGRP + 2)
+            code_bits = a.list[min(max(group_entry(nx.m, ct), 0), a.n_grp - 1)];
           if (a.bias != nullptr) bias_bits = load_bits(a.bias, min(nx.v0 + ct, a.V - 1));
         } else if (k == 2) {
-          const int e = block_entry(nx.m, ct);
-          const bool ok = e >= 0 && e < a.n_blk && (ct >= MBLK || ct < nx.n_valid);
-          put_blocks(um_next, ok ? code_bits : -1, a.nblk, ct);
+          const int e = group_entry(nx.m, ct);
+          const bool ok = e >= 0 && e < a.n_grp && (ct >= NGRP || ct < nx.n_valid);
+          put_groups(um_next, ok ? code_bits : -1, a.ngrp, ct);
           mv = um_next.maskf[ct];
           put_mask_words(um_next, mv, ct, lane);
           const int col = nx.v0 + ct;
@@ -805,56 +815,69 @@ __device__ __forceinline__ void compute_unit(Smem& sm, const UnitMeta& um, int n
       for (int i = 0; i < 16; ++i) acc[j][nb][i] = bv;
   }
 
+  // Every operand row is (multiple of 32) + l32, so its swizzle key is key(l32): a
+  // fragment's LDS index is a per-lane offset plus a compile-time row offset.
+  const u32x4* abase = sm.a[0] + (wm * 32) * CHUNKS;
+  const u32x4* bbase = sm.b[0] + (wn * 64) * CHUNKS;
+  constexpr int A_STAGE = BM * CHUNKS, B_STAGE = BN * CHUNKS;
+  const int kx = swz_key(l32), off0 = l32 * CHUNKS;
+  auto chunk = [&](int p) { return off0 + ((h * (CHUNKS / 2) + p) ^ kx); };  // lane half h: K chunks 4h..4h+3
+  // One buffer of operand fragments (the 168-VGPR budget holds the 128 accumulator
+  // registers and 24 more): each fragment for the next K step is read right after the
+  // last MFMA that uses it. MFMAs run B-fragment-major, so B fragment 0 frees first,
+  // then A fragments 0..JM-1, then B fragment 1.
+  u32x4 bf[NB_PER_WAVE], af[JA];
+  // MFMAs of the fragments at hand; rolling reads of K step p of stage st.
+  auto step = [&](int st, int p) {
+    const u32x4* an = abase + st * A_STAGE;
+    const u32x4* bn = bbase + st * B_STAGE;
+    const int cn = chunk(p);
+#pragma unroll
+    for (int j = 0; j < JM; ++j) Mfma<T>::run(af[j], bf[0], acc[j][0]);
+    bf[0] = bn[cn];
+#pragma unroll
+    for (int j = 0; j < JM; ++j) {
+      Mfma<T>::run(af[j], bf[1], acc[j][1]);
+      af[j] = an[j * WAVES_M * 32 * CHUNKS + cn];
+    }
+    bf[1] = bn[32 * CHUNKS + cn];
+  };
+  // Keep that order: each read right after the MFMA that frees its registers.
+  auto order = [&](int steps) {
+    constexpr int KI = Mfma<T>::kInsts;
+#pragma unroll
+    for (int p = 0; p < steps; ++p) {
+      __builtin_amdgcn_sched_group_barrier(0x008, JM * KI, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+#pragma unroll
+      for (int j = 0; j < JM; ++j) {
+        __builtin_amdgcn_sched_group_barrier(0x008, KI, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      }
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+  };
+  if (JM > 0) {
+#pragma unroll
+    for (int nb = 0; nb < NB_PER_WAVE; ++nb) bf[nb] = bbase[buf * B_STAGE + nb * 32 * CHUNKS + chunk(0)];
+#pragma unroll
+    for (int j = 0; j < JM; ++j) af[j] = abase[buf * A_STAGE + j * WAVES_M * 32 * CHUNKS + chunk(0)];
+  }
+  // Software-pipelined over the step barrier: K steps 0..2 of slab k, then B_k, then
+  // K step 3 of slab k with the reads of slab k+1's first K step, whose latency the
+  // MFMAs hide. (After the last slab those reads fetch stale data, never used.)
   for (int k = 0; k < nk; ++k) {
     const int cur = buf ^ (k & 1);
     if (JM > 0) {
-      // Every operand row is (multiple of 32) + l32, so its swizzle key is key(l32):
-      // a fragment's LDS index is a per-lane offset plus a compile-time row offset.
-      const u32x4* abuf = sm.a[cur] + (wm * 32) * CHUNKS;
-      const u32x4* bbuf = sm.b[cur] + (wn * 64) * CHUNKS;
-      const int kx = swz_key(l32);
-      const int off0 = l32 * CHUNKS;
-      auto chunk = [&](int p) { return off0 + ((h * (CHUNKS / 2) + p) ^ kx); };  // lane half h: K chunks 4h..4h+3
-      // One buffer of operand fragments (the 168-VGPR budget holds the 128 accumulator
-      // registers and 24 more): each fragment for K step p+1 is read right after the
-      // last MFMA of step p that uses it. MFMAs run B-fragment-major, so B fragment 0
-      // frees first, then A fragments 0..JM-1, then B fragment 1.
-      u32x4 bf[NB_PER_WAVE], af[JA];
 #pragma unroll
-      for (int nb = 0; nb < NB_PER_WAVE; ++nb) bf[nb] = bbuf[nb * 32 * CHUNKS + chunk(0)];
-#pragma unroll
-      for (int j = 0; j < JM; ++j) af[j] = abuf[j * WAVES_M * 32 * CHUNKS + chunk(0)];
-#pragma unroll
-      for (int p = 0; p < CHUNKS / 2; ++p) {
-        const bool more = p + 1 < CHUNKS / 2;
-        const int cn = chunk(p + 1);
-#pragma unroll
-        for (int j = 0; j < JM; ++j) Mfma<T>::run(af[j], bf[0], acc[j][0]);
-        if (more) bf[0] = bbuf[cn];
-#pragma unroll
-        for (int j = 0; j < JM; ++j) {
-          Mfma<T>::run(af[j], bf[1], acc[j][1]);
-          if (more) af[j] = abuf[j * WAVES_M * 32 * CHUNKS + cn];
-        }
-        if (more) bf[1] = bbuf[32 * CHUNKS + cn];
-      }
-      // Keep that order: reads go right after the MFMA that frees their registers.
-      constexpr int KI = Mfma<T>::kInsts;
-      __builtin_amdgcn_sched_group_barrier(0x100, NB_PER_WAVE + JM, 0);
-#pragma unroll
-      for (int p = 0; p < CHUNKS / 2; ++p) {
-        const bool more = p + 1 < CHUNKS / 2;
-        __builtin_amdgcn_sched_group_barrier(0x008, JM * KI, 0);
-        if (more) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-#pragma unroll
-        for (int j = 0; j < JM; ++j) {
-          __builtin_amdgcn_sched_group_barrier(0x008, KI, 0);
-          if (more) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-        }
-        if (more) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-      }
+      for (int p = 1; p < CHUNKS / 2; ++p) step(cur, p);
+      order(CHUNKS / 2 - 1);
     }
-    lds_barrier();  // B_k: slab k read; slab k+1 landed
+    lds_barrier();  // B_k: slab k read (the last fragments are in registers); slab k+1 landed
+    if (JM > 0) {
+      step(cur ^ 1, 0);
+      order(1);
+    }
   }
 
   // Block epilogue. 32x32 accumulator layout: lane holds column l32, and register
@@ -864,19 +887,20 @@ __device__ __forceinline__ void compute_unit(Smem& sm, const UnitMeta& um, int n
   // float bits order like the values, so the largest key has the largest x and, among
   // x equal to 2^-18 relative, the lowest row -- the lowest-s rule, applied at the
   // precision the key keeps (the reference compares bf16-rounded logits, 2^-8). Keys of
-  // x <= 0 are never positive-valued and decode to (0, row 0), the initial max. With a
-  // 0/1 mask, bits(x) & ~31 is one AND with the row's mask word.
+  // x <= 0 are never positive-valued. With a 0/1 mask, bits(x) & ~31 is one AND with
+  // the row's mask word. Rows 0..15 of block b are group 2b (registers q = 0, 1) and rows
+  // 16..31 group 2b + 1 (q = 2, 3): one key per group and column.
   const int binary = um.mask_binary;
   const float* mrow = &um.maskf[wm * 32 + 4 * h];
   const int* wrow = &um.maskw[wm * 32 + 4 * h];
-  float* pvw = &sm.pv[wm][wn * 64 + l32];
-  int* piw = &sm.pi[wm][wn * 64 + l32];
+  int* kw = &sm.key[2 * wm][wn * 64 + l32];
 #pragma unroll
   for (int j = 0; j < JM; ++j) {
-    const int s_blk = um.blk_s[wm + WAVES_M * j];
-    int kmax[NB_PER_WAVE];
+    int kmax[2][NB_PER_WAVE];
 #pragma unroll
-    for (int nb = 0; nb < NB_PER_WAVE; ++nb) kmax[nb] = INT32_MIN;
+    for (int g = 0; g < 2; ++g)
+#pragma unroll
+      for (int nb = 0; nb < NB_PER_WAVE; ++nb) kmax[g][nb] = INT32_MIN;
     if (binary) {
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
@@ -885,7 +909,8 @@ __device__ __forceinline__ void compute_unit(Smem& sm, const UnitMeta& um, int n
         for (int e = 0; e < 4; ++e)
 #pragma unroll
           for (int nb = 0; nb < NB_PER_WAVE; ++nb)
-            kmax[nb] = max(kmax[nb], (__float_as_int(acc[j][nb][q * 4 + e]) & w4[e]) | (31 - 8 * q - e));
+            kmax[q >> 1][nb] = max(kmax[q >> 1][nb],
+                                   (__float_as_int(acc[j][nb][q * 4 + e]) & w4[e]) | (31 - 8 * q - e));
       }
     } else {
 #pragma unroll
@@ -895,24 +920,22 @@ __device__ __forceinline__ void compute_unit(Smem& sm, const UnitMeta& um, int n
         for (int e = 0; e < 4; ++e)
 #pragma unroll
           for (int nb = 0; nb < NB_PER_WAVE; ++nb)
-            kmax[nb] = max(kmax[nb], (__float_as_int(acc[j][nb][q * 4 + e] * m4[e]) & ~31) | (31 - 8 * q - e));
+            kmax[q >> 1][nb] = max(kmax[q >> 1][nb],
+                                   (__float_as_int(acc[j][nb][q * 4 + e] * m4[e]) & ~31) | (31 - 8 * q - e));
       }
     }
 #pragma unroll
-    for (int nb = 0; nb < NB_PER_WAVE; ++nb) {
-      // The keys above encode rows 8q + e; lanes of half 1 hold rows 4 higher. Then
-      // v_permlane32_swap exchanges the halves: element 1 of the result holds, in lanes
-      // 0..31, the keys of lanes 32..63 (the only lanes that store below).
-      const int k = kmax[nb] - 4 * h;
-      const int ko = (int)__builtin_amdgcn_permlane32_swap((unsigned)k, (unsigned)k, false, false)[1];
-      const int kb = max(k, ko);
-      const float v = __int_as_float(kb & ~31);
-      if (h == 0) {
-        const bool pos = v > 0.0f;
-        pvw[j * WAVES_M * BN + nb * 32] = pos ? v : 0.0f;
-        piw[j * WAVES_M * BN + nb * 32] = pos ? s_blk + 31 - (kb & 31) : 0;
+    for (int g = 0; g < 2; ++g)
+#pragma unroll
+      for (int nb = 0; nb < NB_PER_WAVE; ++nb) {
+        // The keys above encode rows 8q + e; lanes of half 1 hold rows 4 higher. Then
+        // v_permlane32_swap exchanges the halves: element 1 of the result holds, in
+        // lanes 0..31, the keys of lanes 32..63 (the only lanes that store below).
+        const int k = kmax[g][nb] - 4 * h;
+        const int ko = (int)__builtin_amdgcn_permlane32_swap((unsigned)k, (unsigned)k, false, false)[1];
+        const int kb = max(k, ko);
+        if (h == 0) kw[(j * 2 * WAVES_M + g) * BN + nb * 32] = __int_as_float(kb & ~31) > 0.0f ? kb : 0;
       }
-    }
   }
   lds_barrier();  // E
 }
@@ -922,15 +945,15 @@ __device__ void compute_path(Smem& sm, const Args<T>& a, int w, int G, int n_uni
                              int n_vt, int wave, int lane) {
   const int nk = a.nk;
   const int wm = wave / WAVES_N, wn = wave % WAVES_N;
-  Unit cur = unit_of(w, 0, G, n_units, n_mt, n_vt, a.n_blk);
+  Unit cur = unit_of(w, 0, G, n_units, n_mt, n_vt, a.n_grp);
   if (cur.u < 0) return;
   lds_barrier();  // S1
   lds_barrier();  // S2
   int par = 0, buf = 0;
   for (int r = 1;; ++r) {
     const UnitMeta& um = sm.um[par];
-    const int n_valid = cur.n_valid;
-    const int jm = n_valid <= wm ? 0 : min(4, (n_valid - wm + 1) / WAVES_M);
+    const int n_blocks = (cur.n_valid + 1) / 2;  // 32-row blocks with an active group
+    const int jm = n_blocks <= wm ? 0 : min(4, (n_blocks - wm + 1) / WAVES_M);
     switch (jm) {
       case 0: compute_unit<T, 0>(sm, um, nk, buf, lane, wm, wn); break;
       case 1: compute_unit<T, 1>(sm, um, nk, buf, lane, wm, wn); break;
@@ -938,7 +961,7 @@ __device__ void compute_path(Smem& sm, const Args<T>& a, int w, int G, int n_uni
       case 3: compute_unit<T, 3>(sm, um, nk, buf, lane, wm, wn); break;
       default: compute_unit<T, 4>(sm, um, nk, buf, lane, wm, wn); break;
     }
-    const Unit next = unit_of(w, r, G, n_units, n_mt, n_vt, a.n_blk);
+    const Unit next = unit_of(w, r, G, n_units, n_mt, n_vt, a.n_grp);
     if (next.u < 0) return;
     if (nk < PREFETCH_MIN_NK) {
       lds_barrier();  // S1
@@ -954,7 +977,7 @@ template <typename T>
 __global__ __launch_bounds__(NTHREADS, 1) void sparton_fwd_kernel(
     const T* __restrict__ H, const T* __restrict__ W, const T* __restrict__ bias,
     const float* __restrict__ rowmask, T* __restrict__ reps, int32_t* __restrict__ argmax,
-    float* __restrict__ reps_f32, int S, int D, int V, int n_vt, int nblk,
+    float* __restrict__ reps_f32, int S, int D, int V, int n_vt, int ngrp,
     const int* __restrict__ meta, const int* __restrict__ list, float2* __restrict__ part) {
   __shared__ Smem sm;
   const int tid = threadIdx.x, lane = tid & 63;
@@ -966,8 +989,8 @@ __global__ __launch_bounds__(NTHREADS, 1) void sparton_fwd_kernel(
   a.bias = bias;
   a.rowmask = rowmask;
   a.list = list;
-  a.n_blk = __builtin_amdgcn_readfirstlane(meta[0]);
-  a.nblk = nblk;
+  a.n_grp = __builtin_amdgcn_readfirstlane(meta[0]);
+  a.ngrp = ngrp;
   a.S = S;
   a.row_bytes = D * (int)sizeof(T);
   const int slab_elems = SLAB / (int)sizeof(T);
@@ -977,7 +1000,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void sparton_fwd_kernel(
   a.nk = D == 0 ? 0 : max(2, (int)cdiv(D, slab_elems));
   a.V = V;
 
-  const int n_mt = (a.n_blk + MBLK - 1) / MBLK;
+  const int n_mt = (a.n_grp + NGRP - 1) / NGRP;
   const int n_units = n_mt * n_vt;
   if (wave < COMPUTE_WAVES) {
     compute_path<T>(sm, a, blockIdx.x, gridDim.x, n_units, n_mt, n_vt, wave, lane);
@@ -990,7 +1013,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void sparton_fwd_kernel(
 
 // ---- fixup ------------------------------------------------------------------------
 
-// Per batch row: no active block -> reps = 0, argmax = 0; blocks spread over several
+// Per batch row: no active group -> reps = 0, argmax = 0; groups spread over several
 // M-tiles -> merge their partials in tile order (= s order). A workgroup covers 1024
 // vocab ids (4 per thread) of one batch row and exits at once if the main kernel
 // completed that row.
@@ -1006,8 +1029,8 @@ __global__ __launch_bounds__(256) void fwd_fixup_kernel(int V, const int* __rest
   const int n = count[b];
   int ms = 0, me = 0;
   if (n > 0) {
-    ms = first[b] / MBLK;
-    me = (first[b] + n - 1) / MBLK;
+    ms = first[b] / NGRP;
+    me = (first[b] + n - 1) / NGRP;
     if (ms == me) return;  // written by the main kernel
   }
 #pragma unroll
@@ -1063,31 +1086,31 @@ static int launch(const void* H, const void* W, const void* bias, const void* ma
                   int mask_dtype, void* reps, int32_t* argmax, float* reps_f32, int64_t B,
                   int64_t S, int64_t D, int64_t V, const Work& w, hipStream_t stream,
                   hipEvent_t* ev_main) {
-  const int64_t nblk = cdiv(S, 32);
+  const int64_t ngrp = cdiv(S, GROUP);
   const int64_t n_vt = cdiv(V, BN);
-  const int64_t n_mt_max = cdiv(B * nblk, MBLK);
+  const int64_t n_mt_max = cdiv(B * ngrp, NGRP);
   // Unit numbers (and one round past them) must fit in int.
   if (n_mt_max * n_vt > INT32_MAX / 2) return SPARTON_EUNSUPPORTED;
   const int64_t grid = persistent_grid(n_mt_max * n_vt);
-  if (B <= PLAN_FUSED_MAX && B * nblk <= PLAN_FUSED_MAX) {
+  if (B <= PLAN_FUSED_MAX && B * ngrp <= PLAN_FUSED_MAX) {
     hipLaunchKernelGGL(fwd_plan_small_kernel, dim3(1), dim3(PLAN_THREADS), 0, stream, mask,
-                       mask_dtype, (int)B, (int)S, (int)nblk, w.count, w.first, w.list, w.meta,
+                       mask_dtype, (int)B, (int)S, (int)ngrp, w.count, w.first, w.list, w.meta,
                        w.rowmask);
   } else {
     hipLaunchKernelGGL(fwd_plan_rows_kernel, dim3((unsigned)cdiv(B, 4)), dim3(256), 0, stream,
-                       mask, mask_dtype, (int)B, (int)S, (int)nblk, w.flag, w.count);
+                       mask, mask_dtype, (int)B, (int)S, (int)ngrp, w.flag, w.count);
     hipLaunchKernelGGL(fwd_plan_list_kernel, dim3(1), dim3(PLAN_THREADS), 0, stream, (int)B,
-                       (int)nblk, (const uint8_t*)w.flag, (const int*)w.count, w.first, w.list,
+                       (int)ngrp, (const uint8_t*)w.flag, (const int*)w.count, w.first, w.list,
                        w.meta);
     hipLaunchKernelGGL(fwd_plan_rowmask_kernel, dim3((unsigned)cdiv(n_mt_max * BM, 256)), dim3(256),
-                       0, stream, mask, mask_dtype, (int)S, (int)nblk, (const int*)w.meta,
+                       0, stream, mask, mask_dtype, (int)S, (int)ngrp, (const int*)w.meta,
                        (const int*)w.list, w.rowmask);
   }
   if (ev_main != nullptr) (void)hipEventRecord(ev_main[0], stream);
   if (grid > 0)  // S == 0: no blocks, the fixup writes every row
     hipLaunchKernelGGL(sparton_fwd_kernel<T>, dim3((unsigned)grid), dim3(NTHREADS), 0, stream,
                        (const T*)H, (const T*)W, (const T*)bias, (const float*)w.rowmask, (T*)reps,
-                       argmax, reps_f32, (int)S, (int)D, (int)V, (int)n_vt, (int)nblk,
+                       argmax, reps_f32, (int)S, (int)D, (int)V, (int)n_vt, (int)ngrp,
                        (const int*)w.meta, (const int*)w.list, w.part);
   if (ev_main != nullptr) (void)hipEventRecord(ev_main[1], stream);
   hipLaunchKernelGGL(fwd_fixup_kernel<T>, dim3((unsigned)cdiv(V, FIX_COLS), (unsigned)B), dim3(256), 0,
