@@ -350,6 +350,77 @@ __global__ __launch_bounds__(PLAN_THREADS) void fwd_plan_small_kernel(
   }
 }
 
+// The whole plan in one workgroup with every mask value staged in LDS, for
+// B * S <= PLAN_TINY_POS and B * ngrp <= PLAN_THREADS: one batch of mask loads, one
+// prefix scan over the groups (thread g = group g, in (b, j) order), and the row mask
+// filled from LDS.
+constexpr int PLAN_TINY_POS = 1 << 14;  // positions (B * S)
+__global__ __launch_bounds__(PLAN_THREADS) void fwd_plan_tiny_kernel(
+    const void* __restrict__ mask, int mask_dtype, int B, int S, int ngrp, int* __restrict__ count,
+    int* __restrict__ first, int* __restrict__ list, int* __restrict__ meta,
+    float* __restrict__ rowmask) {
+  __shared__ float mv[PLAN_TINY_POS];
+  __shared__ int lst[PLAN_THREADS];          // the list
+  __shared__ int slot_of[PLAN_THREADS + 1];  // list slot of group g (active or not); [n_g] = total
+  __shared__ int wsum[PLAN_THREADS / 64];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int n_pos = B * S, n_g = B * ngrp;
+  constexpr int PER = PLAN_TINY_POS / PLAN_THREADS;
+  if (n_pos > 0) {
+    int64_t off[PER];
+#pragma unroll
+    for (int u = 0; u < PER; ++u) off[u] = min(tid + u * PLAN_THREADS, n_pos - 1);
+    float v[PER];
+    load_mask_n<PER>(mask, mask_dtype, off, v);
+#pragma unroll
+    for (int u = 0; u < PER; ++u)
+      if (tid + u * PLAN_THREADS < n_pos) mv[tid + u * PLAN_THREADS] = v[u];
+  }
+  __syncthreads();
+  bool on = false;
+  if (tid < n_g) {
+    const int b = tid / ngrp, j = tid - b * ngrp;
+    const int s1 = min(S, (j + 1) * GROUP);
+    for (int s = j * GROUP; s < s1; ++s) on |= mv[b * S + s] != 0.0f;
+  }
+  const uint64_t bal = __ballot(on);
+  if (lane == 0) wsum[wave] = __popcll(bal);
+  __syncthreads();
+  int before = 0, total = 0;
+#pragma unroll
+  for (int w = 0; w < PLAN_THREADS / 64; ++w) {
+    before += w < wave ? wsum[w] : 0;
+    total += wsum[w];
+  }
+  const int slot = before + __popcll(bal & ((1ull << lane) - 1ull));
+  if (tid < n_g) slot_of[tid] = slot;
+  if (on) {
+    list[slot] = tid;  // b * ngrp + j
+    lst[slot] = tid;
+  }
+  if (tid == 0) {
+    slot_of[n_g] = total;
+    meta[0] = total;
+  }
+  __syncthreads();
+  for (int b = tid; b < B; b += PLAN_THREADS) {
+    const int f = slot_of[b * ngrp];
+    first[b] = f;
+    count[b] = slot_of[(b + 1) * ngrp] - f;
+  }
+  const int n_rows = (total + NGRP - 1) / NGRP * BM;
+  for (int t = tid; t < n_rows; t += PLAN_THREADS) {
+    const int e = t / GROUP;
+    float v = 0.0f;
+    if (e < total) {
+      const int code = lst[e], b = code / ngrp;
+      const int s = (code - b * ngrp) * GROUP + t % GROUP;
+      if (s < S) v = mv[b * S + s];
+    }
+    rowmask[t] = v;
+  }
+}
+
 // ---- main kernel ------------------------------------------------------------------
 
 // Metadata of one unit, double-buffered: the next unit's copy is filled while the
@@ -1033,28 +1104,44 @@ __global__ __launch_bounds__(256) void fwd_fixup_kernel(int V, const int* __rest
     me = (first[b] + n - 1) / NGRP;
     if (ms == me) return;  // written by the main kernel
   }
+  constexpr int CPT = FIX_COLS / 256;  // columns per thread; each round's loads go together
+  int col[CPT];
+  float bv[CPT];
+  int bi[CPT];
 #pragma unroll
-  for (int k = 0; k < FIX_COLS / 256; ++k) {
+  for (int k = 0; k < CPT; ++k) {
+    col[k] = min(blockIdx.x * FIX_COLS + k * 256 + (int)threadIdx.x, V - 1);
+    bv[k] = 0.0f;
+    bi[k] = 0;
+  }
+  if (n > 0) {
+    float2 p[CPT];
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) p[k] = part[((int64_t)ms * 2 + 1) * V + col[k]];
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+      bv[k] = p[k].x;
+      bi[k] = __float_as_int(p[k].y);
+    }
+    for (int mm = ms + 1; mm <= me; ++mm) {
+#pragma unroll
+      for (int k = 0; k < CPT; ++k) p[k] = part[((int64_t)mm * 2 + 0) * V + col[k]];
+#pragma unroll
+      for (int k = 0; k < CPT; ++k)
+        if (p[k].x > bv[k]) {  // later tiles hold higher s: strict '>' keeps the lower on ties
+          bv[k] = p[k].x;
+          bi[k] = __float_as_int(p[k].y);
+        }
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < CPT; ++k) {
     const int v = blockIdx.x * FIX_COLS + k * 256 + threadIdx.x;
     if (v >= V) break;
-    float bv = 0.0f;
-    int bi = 0;
-    if (n > 0) {
-      const float2 p0 = part[((int64_t)ms * 2 + 1) * V + v];
-      bv = p0.x;
-      bi = __float_as_int(p0.y);
-      for (int mm = ms + 1; mm <= me; ++mm) {
-        const float2 p = part[((int64_t)mm * 2 + 0) * V + v];
-        if (p.x > bv) {  // later tiles hold higher s: strict '>' keeps the lower on ties
-          bv = p.x;
-          bi = __float_as_int(p.y);
-        }
-      }
-    }
     const int64_t o = (int64_t)b * V + v;
-    const float rv = log1pf(bv);
+    const float rv = log1pf(bv[k]);
     reps[o] = from_f32<T>(rv);
-    if (argmax != nullptr) argmax[o] = bi;
+    if (argmax != nullptr) argmax[o] = bi[k];
     if (reps_f32 != nullptr) reps_f32[o] = rv;
   }
 }
@@ -1092,7 +1179,11 @@ static int launch(const void* H, const void* W, const void* bias, const void* ma
   // Unit numbers (and one round past them) must fit in int.
   if (n_mt_max * n_vt > INT32_MAX / 2) return SPARTON_EUNSUPPORTED;
   const int64_t grid = persistent_grid(n_mt_max * n_vt);
-  if (B <= PLAN_FUSED_MAX && B * ngrp <= PLAN_FUSED_MAX) {
+  if (B * S <= PLAN_TINY_POS && B * ngrp <= PLAN_THREADS) {
+    hipLaunchKernelGGL(fwd_plan_tiny_kernel, dim3(1), dim3(PLAN_THREADS), 0, stream, mask,
+                       mask_dtype, (int)B, (int)S, (int)ngrp, w.count, w.first, w.list, w.meta,
+                       w.rowmask);
+  } else if (B <= PLAN_FUSED_MAX && B * ngrp <= PLAN_FUSED_MAX) {
     hipLaunchKernelGGL(fwd_plan_small_kernel, dim3(1), dim3(PLAN_THREADS), 0, stream, mask,
                        mask_dtype, (int)B, (int)S, (int)ngrp, w.count, w.first, w.list, w.meta,
                        w.rowmask);
