@@ -296,6 +296,19 @@ template <> struct Raw4<f16> {
 // Rows gathered per batch: all their loads are in flight together (about 24 per lane).
 template <int NP> struct Batch { static constexpr int U = NP <= 3 ? 8 : NP <= 6 ? 4 : NP <= 8 ? 3 : 2; };
 
+// The staged dW kernel gathers the rows of IDC of a wave's ids together; their
+// accumulators and U rows of loads fit its 128 VGPRs.
+template <typename T, int NP> struct DwBatch {
+  static constexpr int IDC = NP > 3 ? 1 : sizeof(T) == 2 ? 4 : 2;
+  static constexpr int U = IDC > 1 ? 6 : Batch<NP>::U;
+};
+// Register passes of the staged dW kernel: at most 8 (16-bit) or 4 (fp32), so that one
+// id's accumulators and a batch of rows fit 128 VGPRs; longer rows loop over D.
+template <typename T, int NP> struct DwPasses {
+  static constexpr int CAP = sizeof(T) == 2 ? 8 : 4;
+  static constexpr int value = NP < CAP ? NP : CAP;
+};
+
 // ---- 4. dH ---------------------------------------------------------------------
 // One wave per (b,s) row; lane l owns elements d0 + p*256 + 4l .. +3 for p < NP. The
 // segment's entries sit one per lane; they are taken U at a time (a uniform loop, so
@@ -460,9 +473,9 @@ constexpr int DW_STAGE_B = 128;
 
 // A workgroup of 16 waves owns 64 consecutive vocab ids. It loads G, reps and I of all
 // batch rows for them (each load instruction reads 64 consecutive elements of one row)
-// and keeps g' (0 = inactive) and I in LDS; then wave w handles ids 4w .. 4w+3, one at
-// a time: lanes scan the batch rows, a ballot lists the active ones, and their H rows
-// are gathered up to U at a time in ascending b and accumulated.
+// and keeps g' (0 = inactive) and I in LDS; then wave w handles ids 4w .. 4w+3
+// together: lanes scan the batch rows, ballots list the active ones, and their H rows
+// are gathered up to U at a time and accumulated, each id in ascending b.
 constexpr int DW_WAVES = 16;
 template <typename T, typename O, int NP, typename RT>
 __global__ __launch_bounds__(64 * DW_WAVES) void bwd_dw_staged_kernel(
@@ -470,7 +483,7 @@ __global__ __launch_bounds__(64 * DW_WAVES) void bwd_dw_staged_kernel(
     const int32_t* __restrict__ idx, const void* __restrict__ mask, int mdt,
     const T* __restrict__ H, O* __restrict__ dW, O* __restrict__ dbias, int B, int S, int D,
     int V) {
-  constexpr int U = Batch<NP>::U;
+  
   constexpr int LD = DW_STAGE_B + 1;  // odd row stride: conflict-free column and row access
   __shared__ float gl[64 * LD];
   __shared__ uint16_t sl[64 * LD];
@@ -491,32 +504,66 @@ __global__ __launch_bounds__(64 * DW_WAVES) void bwd_dw_staged_kernel(
     }
   }
   __syncthreads();
+  // IDC of the wave's ids at a time are gathered together: batches of U rows are taken
+  // from their active (id, b) pairs in (id, b) order, so each id still sums its rows in
+  // ascending b.
+  constexpr int IDS = 64 / DW_WAVES;
+  constexpr int IDC = DwBatch<T, NP>::IDC;
+  constexpr int U = DwBatch<T, NP>::U;
+  static_assert(IDS % IDC == 0, "ids per wave");
   const int dend = max(D, 1);  // one pass even when D == 0, for dbias
-  for (int i = 0; i < 64 / DW_WAVES; ++i) {
-    const int vl = wave * (64 / DW_WAVES) + i, v = v0 + vl;
-    if (v >= V) break;
+  for (int i0 = 0; i0 < IDS; i0 += IDC) {
+    if (v0 + wave * IDS + i0 >= V) break;
     for (int d0 = 0; d0 < dend; d0 += NP * 256) {
-      f32x4 acc[NP];
+      f32x4 acc[IDC][NP];
+      float bsum[IDC];
 #pragma unroll
-      for (int p = 0; p < NP; ++p) acc[p] = f32x4{0.f, 0.f, 0.f, 0.f};
-      float bsum = 0.0f;
+      for (int i = 0; i < IDC; ++i) {
+        bsum[i] = 0.0f;
+#pragma unroll
+        for (int p = 0; p < NP; ++p) acc[i][p] = f32x4{0.f, 0.f, 0.f, 0.f};
+      }
       for (int b0 = 0; b0 < B; b0 += 64) {
         const int bb = b0 + lane;
-        const float g = bb < B ? gl[vl * LD + bb] : 0.0f;
-        const int s = bb < B ? (int)sl[vl * LD + bb] : 0;
-        uint64_t pending = __ballot(g != 0.0f);
-        while (pending) {
-          const int nb = min(U, __popcll(pending));  // rows in this batch (uniform)
+        float g[IDC];
+        int s[IDC];
+        uint64_t pend[IDC];
+        int left = 0;
+#pragma unroll
+        for (int i = 0; i < IDC; ++i) {
+          const int vl = wave * IDS + i0 + i;
+          const bool in = bb < B && v0 + vl < V;
+          g[i] = in ? gl[vl * LD + bb] : 0.0f;
+          s[i] = in ? (int)sl[vl * LD + bb] : 0;
+          pend[i] = __ballot(g[i] != 0.0f);
+          left += __popcll(pend[i]);
+        }
+        while (left > 0) {
+          const int nb = min(U, left);  // rows in this batch (uniform)
+          left -= nb;
           Raw4<T> x[U][NP];
           float gu[U];
+          int iu[U];
 #pragma unroll
           for (int u = 0; u < U; ++u) {
             gu[u] = 0.0f;
+            iu[u] = -1;
             if (u < nb) {
-              const int l = __ffsll((unsigned long long)pending) - 1;
-              pending &= pending - 1;
-              gu[u] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(g), l));
-              const int su = __builtin_amdgcn_readlane(s, l);
+              int l = 0, su = 0;
+              float gg = 0.0f;
+              bool taken = false;
+#pragma unroll
+              for (int i = 0; i < IDC; ++i) {  // the first id with rows left (uniform)
+                if (!taken && pend[i] != 0) {
+                  taken = true;
+                  iu[u] = i;
+                  l = __ffsll((unsigned long long)pend[i]) - 1;
+                  pend[i] &= pend[i] - 1;
+                  gg = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(g[i]), l));
+                  su = __builtin_amdgcn_readlane(s[i], l);
+                }
+              }
+              gu[u] = gg;
               const T* hr = H + ((int64_t)(b0 + l) * S + su) * D;
 #pragma unroll
               for (int p = 0; p < NP; ++p) {
@@ -528,21 +575,29 @@ __global__ __launch_bounds__(64 * DW_WAVES) void bwd_dw_staged_kernel(
           }
 #pragma unroll
           for (int u = 0; u < U; ++u) {
-            if (u < nb) {
-              bsum += gu[u];
 #pragma unroll
-              for (int p = 0; p < NP; ++p) acc[p] += gu[u] * x[u][p].f();
+            for (int i = 0; i < IDC; ++i) {
+              if (iu[u] == i) {
+                bsum[i] += gu[u];
+#pragma unroll
+                for (int p = 0; p < NP; ++p) acc[i][p] += gu[u] * x[u][p].f();
+              }
             }
           }
         }
       }
-      if (d0 == 0 && dbias != nullptr && lane == 0) dbias[v] = from_f32<O>(bsum);
-      if (dW != nullptr) {
-        O* out = dW + (int64_t)v * D;
 #pragma unroll
-        for (int p = 0; p < NP; ++p) {
-          const int d = d0 + p * 256 + lane * 4;
-          if (d < D) store4(out + d, acc[p]);
+      for (int i = 0; i < IDC; ++i) {
+        const int v = v0 + wave * IDS + i0 + i;
+        if (v >= V) break;
+        if (d0 == 0 && dbias != nullptr && lane == 0) dbias[v] = from_f32<O>(bsum[i]);
+        if (dW != nullptr) {
+          O* out = dW + (int64_t)v * D;
+#pragma unroll
+          for (int p = 0; p < NP; ++p) {
+            const int d = d0 + p * 256 + lane * 4;
+            if (d < D) store4(out + d, acc[i][p]);
+          }
         }
       }
     }
@@ -586,7 +641,8 @@ static void launch_rows(const T* g, const RT* r, const int32_t* idx, const void*
   }
   if ((dW != nullptr || dbias != nullptr) && V > 0) {
     if (B <= DW_STAGE_B)
-      hipLaunchKernelGGL((bwd_dw_staged_kernel<T, O, NP, RT>), dim3((unsigned)cdiv(V, 64)), dim3(64 * DW_WAVES), 0,
+      hipLaunchKernelGGL((bwd_dw_staged_kernel<T, O, DwPasses<T, NP>::value, RT>),
+                         dim3((unsigned)cdiv(V, 64)), dim3(64 * DW_WAVES), 0,
                          st, g, r, idx, mask, mdt, H, dW, dbias, (int)B, (int)S, (int)D, (int)V);
     else
       hipLaunchKernelGGL((bwd_dw_kernel<T, O, NP, RT>), dim3((unsigned)cdiv(V, 4)), dim3(256), 0, st,

@@ -78,6 +78,7 @@ CASES = [
     ("bf16", 3, 900, 64, 2100, True, "gaps"),   # fully masked middle chunk, masked row
     ("bf16", 37, 40, 64, 700, True, "int64"),   # many short rows: several rows per row tile
     ("fp32", 130, 3, 16, 70, True, "int64"),    # B > 128: the unstaged dW path
+    ("bf16", 100, 24, 64, 900, True, "frac"),   # 64 < B <= 128: staged dW, two batch passes
     ("bf16", 8, 3000, 64, 700, True, "gaps"),   # B*S > 16384: plan with the mask in global memory
     ("fp16", 1100, 8, 16, 200, True, "int64"),  # more groups than plan threads
     ("bf16", 600, 500, 16, 300, True, "holes"),  # > 16384 groups: the three-kernel plan
