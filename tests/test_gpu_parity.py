@@ -205,6 +205,37 @@ def test_deterministic_repeat(device):
         assert torch.equal(a, c)
 
 
+def test_graph_capture_replays(device):
+    """Forward and backward captured into one graph (the backward forks its dW kernel onto a
+    second stream and joins it back) replay to the eager results, bitwise, with eager work
+    and synchronizations between the replays."""
+    say("graph capture of fwd + bwd, config 3, 3 replays")
+    inp = make_inputs(WORKLOADS[3]).to(device)
+    H, W, b, m, G = inp.hidden, inp.weight, inp.bias, inp.mask, inp.grad
+
+    def step():
+        r, i, r32 = torch.ops.sparton.fused_sparton_fwd_train(H, W, b, m)
+        return (r, i, r32) + tuple(torch.ops.sparton.fused_sparton_bwd_train(G, r32, i, H, W, b, m))
+
+    eager = [t.clone() for t in step()]
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            step()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = step()
+    for k in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        _ = (H.float().sum() + W.float().sum()).item()  # eager work between replays
+        for a, e in zip(out, eager):
+            assert torch.equal(a, e), f"replay {k}"
+
+
 @pytest.mark.parametrize("cfg", [2, 3])
 def test_training_backward_is_fp32_rounded_once(cfg, device):
     """fused_sparton_bwd_train writes each gradient in the input dtype, rounded once from
