@@ -43,7 +43,7 @@ constexpr int MAX_NP = 16;         // D up to 16 * 256 per register pass
 
 struct Layout {
   int64_t nch;
-  size_t hist, seg_start, seg_cnt, list, comp, ccount, total;  // hist: [B][nch][S] int32
+  size_t hist, seg_start, seg_cnt, list, comp, ccount, cnt64, off64, total;  // hist: [B][nch][S] int32
 };
 
 static Layout layout(int64_t B, int64_t S, int64_t V) {
@@ -54,9 +54,12 @@ static Layout layout(int64_t B, int64_t S, int64_t V) {
   L.hist = take((size_t)(B * L.nch * S) * 4);
   L.seg_start = take((size_t)(B * S) * 4);
   L.seg_cnt = take((size_t)(B * S) * 4);
-  L.list = take((size_t)(B * V) * 8);
+  // [B][V] segment lists; the fused path keeps [B][V/64][64] compacted entries here
+  L.list = take((size_t)(B * round_up(V, 64)) * 8);
   L.comp = take((size_t)(B * L.nch * CHW) * 8);  // [B][nch][CHW] active (v, g') per chunk
   L.ccount = take((size_t)(B * L.nch) * 4);      // [B][nch] their number
+  L.cnt64 = take((size_t)(B * cdiv(V, 64)) * 4);  // fused path: [B][V/64] entries per block
+  L.off64 = take((size_t)(B * cdiv(V, 64) * cdiv(std::min<int64_t>(S, 1024), 16)) * 4);  // and per row range
   L.total = off;
   return L;
 }
@@ -470,6 +473,13 @@ __global__ __launch_bounds__(256) void bwd_dw_kernel(
 
 // ---- 5b. dW and dbias, staged (B <= DW_STAGE_B) ---------------------------------
 constexpr int DW_STAGE_B = 128;
+// The fused dH path (B <= DW_STAGE_B, S <= FUSE_MAX_S, V <= 2^FUSE_V_BITS, D in one
+// register pass): an entry packs v and s into one int.
+constexpr int FUSE_V_BITS = 18;
+constexpr int FUSE_MAX_S = 1024;
+constexpr int FUSE_MAX_NVB = (1 << FUSE_V_BITS) / 64;  // 64-id blocks
+constexpr int FUSE_ROWS = 16;                          // rows per range (one workgroup)
+constexpr int FUSE_MAX_NR = FUSE_MAX_S / FUSE_ROWS;    // ranges (<= 64: one lane each)
 
 // A workgroup of 16 waves owns 64 consecutive vocab ids. It loads G, reps and I of all
 // batch rows for them (each load instruction reads 64 consecutive elements of one row)
@@ -482,8 +492,7 @@ __global__ __launch_bounds__(64 * DW_WAVES) void bwd_dw_staged_kernel(
     const T* __restrict__ grad, const RT* __restrict__ reps,
     const int32_t* __restrict__ idx, const void* __restrict__ mask, int mdt,
     const T* __restrict__ H, O* __restrict__ dW, O* __restrict__ dbias, int B, int S, int D,
-    int V) {
-  
+    int V, int2* __restrict__ comp, int* __restrict__ cnt, int* __restrict__ offs) {
   constexpr int LD = DW_STAGE_B + 1;  // odd row stride: conflict-free column and row access
   __shared__ float gl[64 * LD];
   __shared__ uint16_t sl[64 * LD];
@@ -504,6 +513,35 @@ __global__ __launch_bounds__(64 * DW_WAVES) void bwd_dw_staged_kernel(
     }
   }
   __syncthreads();
+  if (comp != nullptr) {
+    // For the fused dH kernel: row b's active entries among these 64 ids, sorted by row
+    // range k = s / FUSE_ROWS and then by v, as (v | s << FUSE_V_BITS, g') at
+    // comp[(b * nvb + block) * 64 + rank]; their number, and the first rank of each range
+    // (offs[(b * nvb + block) * nr + k], lane k). Ranks come from one pass over the
+    // active lanes (a handful per block).
+    const int nvb = gridDim.x, nr = (S + FUSE_ROWS - 1) / FUSE_ROWS;
+    for (int b = wave; b < B; b += DW_WAVES) {
+      const float g = gl[lane * LD + b];  // 0 for inactive entries and ids past V
+      const int sv = (int)sl[lane * LD + b];
+      const bool on = g != 0.0f;
+      const int k = sv / FUSE_ROWS;
+      const uint64_t bal = __ballot(on);  // outside any branch: every lane votes
+      uint64_t act = bal;
+      const int64_t base = (int64_t)b * nvb + blockIdx.x;
+      int rank = 0, first = 0;  // this entry's rank; the first rank of range `lane`
+      while (act) {
+        const int j = __ffsll((unsigned long long)act) - 1;
+        act &= act - 1;
+        const int kj = __builtin_amdgcn_readlane(k, j);
+        rank += (kj < k || (kj == k && j < lane)) ? 1 : 0;
+        first += kj < lane ? 1 : 0;
+      }
+      if (on)
+        comp[base * 64 + rank] = make_int2((v0 + lane) | (sv << FUSE_V_BITS), __float_as_int(g));
+      if (lane < nr) offs[base * nr + lane] = first;
+      if (lane == 0) cnt[base] = __popcll(bal);
+    }
+  }
   // IDC of the wave's ids at a time are gathered together: batches of U rows are taken
   // from their active (id, b) pairs in (id, b) order, so each id still sums its rows in
   // ascending b.
@@ -604,6 +642,153 @@ __global__ __launch_bounds__(64 * DW_WAVES) void bwd_dw_staged_kernel(
   }
 }
 
+// ---- 4b. dH from the staged dW kernel's compacted entries (the fused path) -------------
+// Two workgroups per (b, range of FUSE_ROWS consecutive rows); wave w of half h owns row
+// s = FUSE_ROWS * range + FUSE_WAVES * h + w. Each 64-id block of row b lists its active
+// entries sorted by row range, then v, so a range's entries are one contiguous run per
+// block: thread t copies the t-th of them into LDS (its block found by binary search over
+// the runs' prefix sums), 64 * FUSE_WAVES per round, in block (= v) order. Each wave
+// appends the entries of its row to its own list, keeping v order, and gathers their W
+// rows U at a time, summing in v order exactly as bwd_dh_kernel does over its segment.
+// With the compaction in the dW kernel this replaces the count, scan and scatter passes.
+constexpr int FUSE_CAP = 256;  // a wave's list; gathered before it could overflow
+constexpr int FUSE_WAVES = 8;  // rows per workgroup: two workgroups per range, so that three
+                               // fit a CU (24 waves) at the dH gathers' ~80 VGPRs
+static_assert(FUSE_ROWS == 2 * FUSE_WAVES, "two workgroups per row range");
+// Register passes the fused path takes (a batch of rows and the accumulators in ~80 VGPRs).
+template <typename T> struct FuseMaxNp { static constexpr int value = sizeof(T) == 2 ? 6 : 3; };
+
+template <typename T, int NP>
+__device__ __forceinline__ void gather_rows(const T* __restrict__ W, const int2* list, int n,
+                                            int D, int lane, f32x4* acc) {
+  constexpr int U = Batch<NP>::U;
+  constexpr int VMASK = (1 << FUSE_V_BITS) - 1;
+  for (int e0 = 0; e0 < n; e0 += 64) {
+    const int2 ent = e0 + lane < n ? list[e0 + lane] : make_int2(0, 0);
+    const int m = min(64, n - e0);
+    for (int j = 0; j < m; j += U) {
+      Raw4<T> w[U][NP];
+      float g[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        // past the list end: reload the last entry's row (a cache hit) with g' = 0
+        const int jj = min(j + u, m - 1);
+        const int v = __builtin_amdgcn_readlane(ent.x, jj) & VMASK;
+        g[u] = j + u < m ? __int_as_float(__builtin_amdgcn_readlane(ent.y, jj)) : 0.0f;
+#pragma unroll
+        for (int p = 0; p < NP; ++p) {
+          const int d = p * 256 + lane * 4;
+          if (d < D) w[u][p].load(W + (int64_t)v * D + d);
+          else w[u][p].zero();
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+#pragma unroll
+        for (int p = 0; p < NP; ++p) acc[p] += g[u] * w[u][p].f();
+    }
+  }
+}
+
+template <typename T, typename O, int NP>
+__global__ __launch_bounds__(64 * FUSE_WAVES) void bwd_dh_fused_kernel(
+    const T* __restrict__ W, const int2* __restrict__ comp, const int* __restrict__ cnt,
+    const int* __restrict__ offs, O* __restrict__ dH, int S, int D, int nvb) {
+  constexpr int NT = 64 * FUSE_WAVES;
+  constexpr int PER = FUSE_MAX_NVB / NT;  // blocks per thread in the prefix
+  __shared__ int pre[FUSE_MAX_NVB + 1];   // prefix of the runs' lengths
+  __shared__ int lo_of[FUSE_MAX_NVB];     // each run's first rank in its block
+  __shared__ int2 stage[NT];
+  __shared__ int2 lst[FUSE_WAVES][FUSE_CAP];
+  __shared__ int wsum[FUSE_WAVES];
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int64_t b = blockIdx.y;
+  const int k = blockIdx.x >> 1, nr = (S + FUSE_ROWS - 1) / FUSE_ROWS;
+  // >= S: no row (the wave still keeps the barriers)
+  const int s = k * FUSE_ROWS + (blockIdx.x & 1) * FUSE_WAVES + wave;
+  // Run of block `blk`: ranks [offs[k], offs[k+1]) (the last range ends at the count).
+  int c[PER], sum = 0;
+  {
+    int lo[PER], hi[PER];
+#pragma unroll
+    for (int q = 0; q < PER; ++q) {
+      const int blk = min(PER * tid + q, nvb - 1);
+      const int64_t o = (b * nvb + blk) * nr + k;
+      lo[q] = offs[o];
+      hi[q] = k + 1 < nr ? offs[o + 1] : cnt[b * nvb + blk];
+    }
+#pragma unroll
+    for (int q = 0; q < PER; ++q) {
+      const int blk = PER * tid + q;
+      c[q] = blk < nvb ? hi[q] - lo[q] : 0;
+      if (blk < nvb) lo_of[blk] = lo[q];
+      sum += c[q];
+    }
+  }
+  int x = sum;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int y = __shfl_up(x, d);
+    if (lane >= d) x += y;
+  }
+  if (lane == 63) wsum[wave] = x;
+  __syncthreads();
+  int before = 0, total = 0;
+#pragma unroll
+  for (int w = 0; w < FUSE_WAVES; ++w) {
+    before += w < wave ? wsum[w] : 0;
+    total += wsum[w];
+  }
+  int run = before + x - sum;
+#pragma unroll
+  for (int q = 0; q < PER; ++q) {
+    pre[PER * tid + q] = run;
+    run += c[q];
+  }
+  if (tid == 0) pre[FUSE_MAX_NVB] = total;
+  __syncthreads();
+  f32x4 acc[NP];
+#pragma unroll
+  for (int p = 0; p < NP; ++p) acc[p] = f32x4{0.f, 0.f, 0.f, 0.f};
+  int n = 0;  // entries in this wave's list (uniform)
+  for (int t0 = 0; t0 < total; t0 += NT) {
+    const int t = t0 + tid;
+    if (t < total) {
+      int lo = 0, hi = nvb;  // pre[lo] <= t < pre[hi]
+      while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if (pre[mid] <= t) lo = mid;
+        else hi = mid;
+      }
+      stage[tid] = comp[(b * nvb + lo) * 64 + lo_of[lo] + (t - pre[lo])];
+    }
+    __syncthreads();
+    const int here = min(NT, total - t0);
+    for (int i = 0; i * 64 < here; ++i) {
+      const int j = i * 64 + lane;
+      const int2 e = j < here ? stage[j] : make_int2(-1, 0);
+      const bool mine = j < here && (e.x >> FUSE_V_BITS) == s;
+      const uint64_t bal = __ballot(mine);
+      if (mine) lst[wave][n + __popcll(bal & ((1ull << lane) - 1ull))] = e;
+      n += __popcll(bal);
+      if (n > FUSE_CAP - 64) {  // the next 64 could overflow: gather what is listed
+        gather_rows<T, NP>(W, lst[wave], n, D, lane, acc);
+        n = 0;
+      }
+    }
+    __syncthreads();  // stage is refilled next round
+  }
+  gather_rows<T, NP>(W, lst[wave], n, D, lane, acc);
+  if (s < S) {
+    O* out = dH + (b * S + s) * D;
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+      const int d = p * 256 + lane * 4;
+      if (d < D) store4(out + d, acc[p]);
+    }
+  }
+}
+
 // Register passes for a row of D elements (4 per lane, 256 per pass), capped at MAX_NP
 // (longer rows loop over D in chunks of MAX_NP * 256).
 static int passes_for(int64_t D) {
@@ -614,6 +799,25 @@ template <typename T, typename O, int NP, typename RT>
 static void launch_rows(const T* g, const RT* r, const int32_t* idx, const void* mask,
                         int mdt, const T* H, const T* W, O* dH, O* dW, O* dbias, void* ws,
                         int64_t B, int64_t S, int64_t D, int64_t V, hipStream_t st) {
+  constexpr int FNP = NP <= FuseMaxNp<T>::value ? NP : FuseMaxNp<T>::value;
+  const bool fused = dH != nullptr && dW != nullptr && B * S > 0 && D > 0 && V > 0 &&
+                     B <= DW_STAGE_B && S <= FUSE_MAX_S && V <= (1 << FUSE_V_BITS) &&
+                     D <= (int64_t)FNP * 256;
+  if (fused) {
+    const Layout L = layout(B, S, V);
+    int2* comp = (int2*)((char*)ws + L.list);
+    int* cnt = (int*)((char*)ws + L.cnt64);
+    int* offs = (int*)((char*)ws + L.off64);
+    const int nvb = (int)cdiv(V, 64);
+    hipLaunchKernelGGL((bwd_dw_staged_kernel<T, O, DwPasses<T, NP>::value, RT>), dim3((unsigned)nvb),
+                       dim3(64 * DW_WAVES), 0, st, g, r, idx, mask, mdt, H, dW, dbias, (int)B,
+                       (int)S, (int)D, (int)V, comp, cnt, offs);
+    hipLaunchKernelGGL((bwd_dh_fused_kernel<T, O, FNP>),
+                       dim3((unsigned)(2 * cdiv(S, FUSE_ROWS)), (unsigned)B), dim3(64 * FUSE_WAVES), 0, st,
+                       W, (const int2*)comp, (const int*)cnt, (const int*)offs, dH, (int)S, (int)D,
+                       nvb);
+    return;
+  }
   if (dH != nullptr && B * S > 0 && D > 0) {
     const Layout L = layout(B, S, V);
     int* hist = (int*)((char*)ws + L.hist);
@@ -643,7 +847,8 @@ static void launch_rows(const T* g, const RT* r, const int32_t* idx, const void*
     if (B <= DW_STAGE_B)
       hipLaunchKernelGGL((bwd_dw_staged_kernel<T, O, DwPasses<T, NP>::value, RT>),
                          dim3((unsigned)cdiv(V, 64)), dim3(64 * DW_WAVES), 0,
-                         st, g, r, idx, mask, mdt, H, dW, dbias, (int)B, (int)S, (int)D, (int)V);
+                         st, g, r, idx, mask, mdt, H, dW, dbias, (int)B, (int)S, (int)D, (int)V,
+                         (int2*)nullptr, (int*)nullptr, (int*)nullptr);
     else
       hipLaunchKernelGGL((bwd_dw_kernel<T, O, NP, RT>), dim3((unsigned)cdiv(V, 4)), dim3(256), 0, st,
                          g, r, idx, mask, mdt, H, dW, dbias, (int)B, (int)S, (int)D, (int)V);
