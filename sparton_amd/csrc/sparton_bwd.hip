@@ -28,6 +28,9 @@
 // (what autograd would cast them to for bf16/fp16 parameters), rounded once from
 // the fp32 sums.
 
+#include <stdlib.h>
+#include <string.h>
+
 #include "sparton_common.h"
 
 extern __shared__ __attribute__((aligned(16))) unsigned char sparton_bwd_smem[];
@@ -795,12 +798,19 @@ static int passes_for(int64_t D) {
   return (int)std::min<int64_t>(MAX_NP, std::max<int64_t>(1, cdiv(D, 256)));
 }
 
+// SPARTON_BWD_PATH=five forces the five-kernel path (tests compare the two paths).
+static bool fused_path_enabled() {
+  const char* e = getenv("SPARTON_BWD_PATH");
+  return e == nullptr || strcmp(e, "five") != 0;
+}
+
 template <typename T, typename O, int NP, typename RT>
 static void launch_rows(const T* g, const RT* r, const int32_t* idx, const void* mask,
                         int mdt, const T* H, const T* W, O* dH, O* dW, O* dbias, void* ws,
                         int64_t B, int64_t S, int64_t D, int64_t V, hipStream_t st) {
   constexpr int FNP = NP <= FuseMaxNp<T>::value ? NP : FuseMaxNp<T>::value;
-  const bool fused = dH != nullptr && dW != nullptr && B * S > 0 && D > 0 && V > 0 &&
+  const bool fused = fused_path_enabled() && dH != nullptr && dW != nullptr && B * S > 0 &&
+                     D > 0 && V > 0 &&
                      B <= DW_STAGE_B && S <= FUSE_MAX_S && V <= (1 << FUSE_V_BITS) &&
                      D <= (int64_t)FNP * 256;
   if (fused) {

@@ -205,6 +205,28 @@ def test_deterministic_repeat(device):
         assert torch.equal(a, c)
 
 
+@pytest.mark.parametrize("case", [
+    ("bf16", 32, 256, 768, 30522, True, "int64"),   # the headline shape
+    ("fp16", 8, 512, 768, 9000, True, "holes"),
+    ("fp32", 5, 70, 132, 900, False, "frac"),
+    ("bf16", 37, 40, 256, 700, True, "int64"),      # many short rows
+], ids=lambda c: "-".join(map(str, c)))
+def test_backward_paths_agree_bitwise(case, device, monkeypatch):
+    """The fused backward (entries compacted by the dW kernel) and the five-kernel one
+    (count, scan, scatter) sum every gradient in the same order: bitwise equal."""
+    say(f"backward paths, case {case}")
+    H, W, b, m, G = make_case(*case)
+    Hd, Wd, md, Gd = H.to(device), W.to(device), m.to(device), G.to(device)
+    bd = None if b is None else b.to(device)
+    _, idx, reps32 = torch.ops.sparton.fused_sparton_fwd_train(Hd, Wd, bd, md)
+    fused = [t.clone() for t in torch.ops.sparton.fused_sparton_bwd_train(Gd, reps32, idx, Hd, Wd, bd, md)]
+    monkeypatch.setenv("SPARTON_BWD_PATH", "five")
+    five = torch.ops.sparton.fused_sparton_bwd_train(Gd, reps32, idx, Hd, Wd, bd, md)
+    torch.cuda.synchronize()
+    for a, c in zip(fused, five):
+        assert torch.equal(a, c)
+
+
 def test_graph_capture_replays(device):
     """Forward and backward captured into one graph (the backward forks its dW kernel onto a
     second stream and joins it back) replay to the eager results, bitwise, with eager work
