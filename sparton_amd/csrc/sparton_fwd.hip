@@ -606,22 +606,20 @@ template <> __device__ __forceinline__ float bits_to_f32<float>(uint32_t x) { re
 // (tail or padding slabs) re-reads the row's first chunk -- valid, finite data inside
 // the row, so nothing outside H or W is read -- and its W copy is zeroed by zero_tail()
 // before use (a zero W times a finite H adds exactly 0). W rows past V re-read row V-1
-// (never stored); A copies of groups past the last active one (n_valid) are skipped.
-template <typename T>
-__device__ __forceinline__ void issue_slab(Smem& sm, const Args<T>& a, const CopyUnit& cu, int k,
-                                           int buf, int c, int lane) {
+// (never stored). Rows of groups past the last active one (n_valid) re-read a row of the
+// last active group (their keys are never used), so every copy is issued unconditionally.
+template <typename T, bool TAIL>
+__device__ __forceinline__ void issue_slab_k(Smem& sm, const Args<T>& a, const CopyUnit& cu, int k,
+                                             int buf, int c, int lane) {
   const uint32_t kb = (uint32_t)k * SLAB;
-  const bool tail = k >= a.nk_full;
-  const int a_groups = cu.n_valid * (GROUP / ROWS_PER_LOAD);
 #pragma unroll
   for (int i = 0; i < A_LOADS; ++i) {
     const int grp = i * COPY_WAVES + c;
     const uint32_t c16 = lane_chunk(grp * ROWS_PER_LOAD + (lane >> 3), lane);
     // a_off includes c16: adding 0 - c16 (mod 2^32) lands on the row's first chunk.
-    const uint32_t step = (!tail || kb + c16 < (uint32_t)a.row_bytes) ? kb : 0u - c16;
-    if (grp < a_groups)
-      __builtin_amdgcn_global_load_lds((const void*)(a.H + (cu.a_off[i] + step)),
-                                       (lds_void*)&sm.a[buf][grp * 64], 16, 0, 0);
+    const uint32_t step = (!TAIL || kb + c16 < (uint32_t)a.row_bytes) ? kb : 0u - c16;
+    __builtin_amdgcn_global_load_lds((const void*)(a.H + (cu.a_off[i] + step)),
+                                     (lds_void*)&sm.a[buf][grp * 64], 16, 0, 0);
   }
   const char* bb = a.W + (int64_t)cu.v0 * a.row_bytes;
   const int b_last = a.V - 1 - cu.v0;
@@ -630,10 +628,16 @@ __device__ __forceinline__ void issue_slab(Smem& sm, const Args<T>& a, const Cop
     const int grp = i * COPY_WAVES + c;
     const int row = grp * ROWS_PER_LOAD + (lane >> 3);
     const uint32_t c16 = lane_chunk(row, lane);
-    const uint32_t step = (!tail || kb + c16 < (uint32_t)a.row_bytes) ? kb : 0u - c16;
+    const uint32_t step = (!TAIL || kb + c16 < (uint32_t)a.row_bytes) ? kb : 0u - c16;
     const uint32_t off = (uint32_t)min(row, b_last) * (uint32_t)a.row_bytes + c16 + step;
     __builtin_amdgcn_global_load_lds((const void*)(bb + off), (lds_void*)&sm.b[buf][grp * 64], 16, 0, 0);
   }
+}
+template <typename T>
+__device__ __forceinline__ void issue_slab(Smem& sm, const Args<T>& a, const CopyUnit& cu, int k,
+                                           int buf, int c, int lane) {
+  if (k >= a.nk_full) issue_slab_k<T, true>(sm, a, cu, k, buf, c, lane);
+  else issue_slab_k<T, false>(sm, a, cu, k, buf, c, lane);
 }
 
 // Zero the W chunks of slab k (in stage buf) that lie past D; each copy wave clears the
