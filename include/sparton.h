@@ -132,6 +132,40 @@ int sparton_bwd(const void* grad_reps, const void* reps, int reps_dtype,
                 int grad_dtype, void* workspace, size_t workspace_bytes, int64_t B,
                 int64_t S, int64_t D, int64_t V, int dtype, void* stream);
 
+/*
+ * The MLM transform before the head (its output is the head's hidden input):
+ *     y = LayerNorm(gelu(x W^T + dense_bias)) * ln_weight + ln_bias, per row of D,
+ * gelu in the exact erf form -- BERT's cls.predictions.transform and RoBERTa's
+ * lm_head dense/gelu/layer_norm, which the reference calls before the head
+ * (training/model.py:14-40, :56-58). The two D x D GEMMs are plain library GEMMs that
+ * the caller runs; these entry points are the fused work around them, on M rows
+ * of D elements (D % 4 == 0, D <= 3072). `dtype` (enum sparton_dtype) is the type of
+ * z, y, dy and dz; dense_bias, ln_weight, ln_bias, mean and rstd are fp32.
+ */
+
+/* Bytes of device scratch sparton_transform_bwd needs (column partial sums). */
+size_t sparton_transform_workspace_bytes(int64_t M, int64_t D);
+
+/*
+ * Forward epilogue: z = x W^T [M,D] (from the GEMM) -> y [M,D], and each row's mean and
+ * 1/sqrt(var + eps) of gelu(z + dense_bias) for the backward.
+ */
+int sparton_transform_fwd(const void* z, const float* dense_bias, const float* ln_weight,
+                          const float* ln_bias, float eps, void* y, float* mean, float* rstd,
+                          int64_t M, int64_t D, int dtype, void* stream);
+
+/*
+ * Backward epilogue: dy [M,D] -> dz [M,D], the gradient at z (the caller's GEMMs then give
+ * dx = dz W and dW = dz^T x), and the fp32 column sums d_ln_weight = sum dy * xhat,
+ * d_ln_bias = sum dy, d_dense_bias = sum dz (each may be NULL). Deterministic: every sum
+ * runs in a fixed order.
+ */
+int sparton_transform_bwd(const void* dy, const void* z, const float* dense_bias,
+                          const float* ln_weight, const float* mean, const float* rstd, void* dz,
+                          float* d_ln_weight, float* d_ln_bias, float* d_dense_bias,
+                          void* workspace, size_t workspace_bytes, int64_t M, int64_t D,
+                          int dtype, void* stream);
+
 /* Static, thread-safe description of a status code. */
 const char* sparton_strerror(int code);
 

@@ -204,3 +204,61 @@ def test_c_header_compiles_as_c():
     out = subprocess.run(["gcc", "-std=c99", "-Wall", "-Werror", "-fsyntax-only", "-x", "c", src],
                          capture_output=True, text=True)
     assert out.returncode == 0, out.stderr
+
+
+# ---- the MLM transform entry points (argument checks only; nothing is launched) ----
+def xf_fwd(**kw):
+    a = dict(z=P, bd=P, g=P, bt=P, eps=1e-12, y=P, mean=P, rstd=P, M=8, D=64, dtype=1, stream=None)
+    a.update(kw)
+    return _lib.load().sparton_transform_fwd(*a.values())
+
+
+def xf_bwd(**kw):
+    a = dict(dy=P, z=P, bd=P, g=P, mean=P, rstd=P, dz=P, dg=None, dbt=None, dbd=None, ws=P,
+             ws_bytes=1 << 30, M=8, D=64, dtype=1, stream=None)
+    a.update(kw)
+    return _lib.load().sparton_transform_bwd(*a.values())
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(M=-1), -1), (dict(dtype=3), -1), (dict(D=62), -1), (dict(z=None), -1),
+    (dict(eps=-1.0), -1), (dict(eps=float("nan")), -1), (dict(bd=P + 4), -2), (dict(D=3076), -3),
+    (dict(M=0), 0), (dict(D=0), 0),
+])
+def test_transform_fwd_argument_validation(kw, code):
+    assert xf_fwd(**kw) == code
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(M=-1), -1), (dict(D=6), -1), (dict(dy=None), -1), (dict(ws=None), -4),
+    (dict(ws_bytes=16), -4), (dict(ws=P + 4), -2), (dict(g=P + 8), -2), (dict(D=4096), -3),
+    (dict(M=0), 0),
+])
+def test_transform_bwd_argument_validation(kw, code):
+    assert xf_bwd(**kw) == code
+
+
+def test_transform_workspace_size():
+    L = _lib.load()
+    # fp32 column partials of (dy * xhat, dy, dz) per 32-row block
+    assert L.sparton_transform_workspace_bytes(8192, 768) == 8192 // 32 * 3 * 768 * 4
+    assert L.sparton_transform_workspace_bytes(33, 8) == 2 * 3 * 8 * 4
+    assert L.sparton_transform_workspace_bytes(0, 768) == 0
+
+
+def test_transform_module_surface():
+    dense, ln = torch.nn.Linear(64, 64), torch.nn.LayerNorm(64, eps=1e-12)
+    m = sparton_amd.SpartonMLMTransform(dense, ln)
+    assert m.dense.weight is dense.weight and m.layer_norm.weight is ln.weight  # shared, not copied
+
+    class BertLike(torch.nn.Module):  # BertPredictionHeadTransform's attribute names
+        def __init__(self):
+            super().__init__()
+            self.dense, self.LayerNorm = torch.nn.Linear(64, 64), torch.nn.LayerNorm(64)
+
+    b = BertLike()
+    assert sparton_amd.SpartonMLMTransform.from_hf(b).layer_norm is b.LayerNorm
+    with pytest.raises(ValueError):
+        sparton_amd.SpartonMLMTransform(torch.nn.Linear(64, 32), ln)
+    with pytest.raises(RuntimeError, match="ROCm/HIP device tensors"):
+        m(torch.randn(2, 3, 64))
