@@ -20,6 +20,9 @@ Prints ONE JSON line. Besides the throughput it reports:
                 mean duration from the same in-step HIP events, vs 8 TB/s.
 The timed region holds the K steps and nothing else: an event recorded between two
 kernels drains the queue, so the per-op events live in their own pass.
+  transform     the MLM transform in front of the head (dense, gelu, LayerNorm) at the
+                same rows and width: fused op vs eager torch fwd+bwd, and each HIP
+                epilogue kernel's compulsory bytes / mean duration vs 8 TB/s.
   cpu_baseline  the reference's torch head (training/model.py:56-62, restated in
                 oracle/) fwd+bwd on the host cores, on a bounded sample of batch rows.
 """
@@ -167,6 +170,107 @@ def time_main_kernel(torch, H, W, b, mask, reps_n):
     return statistics.mean(times)
 
 
+def time_device(torch, fn, reps):
+    """Mean GPU time of fn() when the host is never the bottleneck: a bounded spin kernel
+    (torch.cuda._sleep) holds the queue while all reps are enqueued, so the events bracket
+    back-to-back GPU work only. Returns (device ms, host-bound ms of plain back-to-back)."""
+    host_ms = time_events(torch, fn, reps)
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    torch.cuda._sleep(int(2.5e6 * (host_ms * reps * 2.0 + 5.0)))  # cycles at <= 2.5 GHz
+    start.record()
+    for _ in range(reps):
+        fn()
+    end.record()
+    enqueue_ms = (time.perf_counter() - t0) * 1e3
+    torch.cuda.synchronize()
+    dev_ms = start.elapsed_time(end) / reps
+    return dev_ms, host_ms, enqueue_ms
+
+
+def transform_timing(torch, w, dev, reps_n):
+    """The MLM transform at this workload's M=B*S rows and width D (training/model.py:14-40):
+    SpartonMLMTransform's path (hipBLASLt GEMMs + the HIP epilogues) against the same
+    computation in eager torch, both fwd+bwd through autograd, and each epilogue kernel alone
+    against the bytes it must move (z read and y written; dy and z read and dz written; fp32
+    row statistics)."""
+    import torch.nn.functional as F
+    from sparton_amd import _lib
+    from sparton_amd.transform import _TransformFn
+    L = _lib.load()
+    M, D, dt = w.B * w.S, w.D, w.dtype
+    if D % 4 or D > 3072:
+        return None
+    gen = torch.Generator(device=dev).manual_seed(7)
+    x = torch.randn(M, D, device=dev, generator=gen).to(dt).requires_grad_()
+    W = (torch.randn(D, D, device=dev, generator=gen) / D ** 0.5).to(dt).requires_grad_()
+    vec = [torch.randn(D, device=dev, generator=gen).mul_(0.1).requires_grad_() for _ in range(3)]
+    vec[1].data.add_(1.0)
+    dy = torch.randn(M, D, device=dev, generator=gen).to(dt)
+    eps = 1e-12
+
+    def fused():
+        x.grad = W.grad = None
+        for v in vec:
+            v.grad = None
+        _TransformFn.apply(x, W, vec[0], vec[1], vec[2], eps).backward(dy)
+
+    vl = [v.detach().to(dt).requires_grad_() for v in vec]
+
+    def eager():
+        x.grad = W.grad = None
+        for v in vl:
+            v.grad = None
+        F.layer_norm(F.gelu(F.linear(x, W, vl[0])), (D,), vl[1], vl[2], eps).backward(dy)
+
+    fused_ms, fused_host, fused_enq = time_device(torch, fused, reps_n)
+    eager_ms, eager_host, eager_enq = time_device(torch, eager, reps_n)
+
+    with torch.no_grad():
+        y, z, mean, rstd = torch.ops.sparton.mlm_transform_fwd(x, W, vec[0], vec[1], vec[2], eps)
+    dz = torch.empty_like(z)
+    dg, dbt, dbd = (torch.empty(D, dtype=torch.float32, device=dev) for _ in range(3))
+    ws_bytes = int(L.sparton_transform_workspace_bytes(M, D))
+    ws = torch.empty((max(ws_bytes, 1),), dtype=torch.uint8, device=dev)
+    code, stream = _lib.DTYPE_CODE[dt], torch.cuda.current_stream().cuda_stream
+    b0, g0, t0 = (v.detach() for v in vec)
+
+    def epi_fwd():
+        _lib.check(L.sparton_transform_fwd(z.data_ptr(), b0.data_ptr(), g0.data_ptr(), t0.data_ptr(),
+                                           eps, y.data_ptr(), mean.data_ptr(), rstd.data_ptr(),
+                                           M, D, code, stream), "sparton_transform_fwd")
+
+    def epi_bwd():
+        _lib.check(L.sparton_transform_bwd(dy.data_ptr(), z.data_ptr(), b0.data_ptr(), g0.data_ptr(),
+                                           mean.data_ptr(), rstd.data_ptr(), dz.data_ptr(),
+                                           dg.data_ptr(), dbt.data_ptr(), dbd.data_ptr(),
+                                           ws.data_ptr(), ws_bytes, M, D, code, stream),
+                   "sparton_transform_bwd")
+
+    fwd_epi_ms = time_events(torch, epi_fwd, reps_n)
+    bwd_epi_ms = time_events(torch, epi_bwd, reps_n)
+    e = z.element_size()
+    fwd_bytes = 2 * M * D * e + 8 * M + 3 * D * 4
+    bwd_bytes = 3 * M * D * e + 8 * M + 5 * D * 4
+
+    def roof(nbytes, ms):
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        return {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                "frac": round(gbs / PEAK_HBM_GBS, 4), "bytes_per_call": nbytes, "mean_ms": round(ms, 4)}
+
+    return {"rows": M, "D": D, "dtype": DTYPE_NAME[str(dt)],
+            "fwd_bwd_ms": round(fused_ms, 4), "eager_torch_fwd_bwd_ms": round(eager_ms, 4),
+            "speedup_vs_eager": round(eager_ms / fused_ms, 3),
+            "timing": "HIP events over back-to-back autograd fwd+bwd (GEMMs included), mean of "
+                      "--kernel-reps, queue pre-filled by a spin kernel so host dispatch is hidden",
+            "host_bound_ms": {"sparton": round(fused_host, 4), "eager_torch": round(eager_host, 4)},
+            "enqueue_ms_per_step": {"sparton": round(fused_enq / reps_n, 4),
+                                    "eager_torch": round(eager_enq / reps_n, 4)},
+            "epilogue_fwd": roof(fwd_bytes, fwd_epi_ms),
+            "epilogue_bwd": roof(bwd_bytes, bwd_epi_ms)}
+
+
 def main():
     args = parse()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -254,6 +358,7 @@ def main():
                           args.kernel_reps)
     fwd_ms, bwd_ms = fwd_live, bwd_live
     main_ms = time_main_kernel(torch, Hd.contiguous(), Wd.contiguous(), bd, mask, args.kernel_reps)
+    xf = transform_timing(torch, w, dev, args.kernel_reps)
     if args.copy_probe_mib > 0:
         src = torch.empty(args.copy_probe_mib << 20, dtype=torch.uint8, device=dev)
         dst = torch.empty_like(src)
@@ -324,6 +429,7 @@ def main():
         "peak_gb": round(peak_bytes / 1e9, 4),
         "peak_extra_gb": round((peak_bytes - input_bytes) / 1e9, 4),
         "bsv_logits_gb_avoided": round(w.B * w.S * w.V * e / 1e9, 3),
+        "transform": xf,
         "cpu_baseline": None,
     }
     if not args.no_cpu_baseline and int(os.environ.get("RANK", "0")) == 0:

@@ -10,82 +10,143 @@
 //   backward epilogue dH -> dZ = d/dZ through LayerNorm and gelu (recomputing u from Z),
 //                     plus per-block column partial sums of dH * xhat, dH and dZ;
 //   column reduction  those partials summed in block order into d gamma, d beta, d b_d.
-// One wave per row; lane l holds elements 256 p + 4 l .. +3 of the row. All sums over a
-// row or a column run in a fixed order, so results are bitwise reproducible.
+// A wave works on whole rows; lane l holds elements 256 p + 4 l .. +3 of a row. All sums
+// over a row or a column run in a fixed order, so results are bitwise reproducible.
 
 #include <math.h>
+
+#include <algorithm>
 
 #include "sparton_common.h"
 
 namespace sparton {
 namespace xf {
 
-constexpr int MAX_NP = 12;          // D up to 12 * 256 (the backward's LDS: 4 waves x D floats)
-constexpr int ROW_WAVES = 4;        // waves per workgroup
-constexpr int ROWS_PER_WAVE = 8;    // backward: rows per wave (column partials per block)
-constexpr int BLOCK_ROWS = ROW_WAVES * ROWS_PER_WAVE;
+constexpr int MAX_NP = 12;          // D up to 12 * 256
+constexpr int FWD_WAVES = 4;        // forward: one row per wave, 4 waves per workgroup
+constexpr int BWD_WAVES_NARROW = 8; // backward waves per workgroup for D <= 1024
+constexpr int BWD_WAVES_WIDE = 4;   // wider rows: 512 registers per wave (VGPRs + AGPRs)
+constexpr int BWD_TARGET_BLOCKS = 256;  // enough backward workgroups for one per CU
+constexpr int MAX_ROWS_PER_WAVE = 32;
+constexpr int COL_WAVES = 16;       // column reduction: 64 columns x 16 waves per workgroup
 constexpr float kInvSqrt2 = 0.70710678118654752f;
 constexpr float kInvSqrt2Pi = 0.39894228040143268f;
+constexpr float kLog2e = 1.44269504088896341f;
 
-__device__ __forceinline__ float gelu(float x) { return 0.5f * x * (1.0f + erff(x * kInvSqrt2)); }
-__device__ __forceinline__ float gelu_grad(float x) {
-  return 0.5f * (1.0f + erff(x * kInvSqrt2)) + x * kInvSqrt2Pi * expf(-0.5f * x * x);
+// ---- the normal CDF for exact (erf) gelu ------------------------------------------------
+// gelu(x) = x Phi(x) and gelu'(x) = Phi(x) + x phi(x), with Phi(x) = erfc(-x / sqrt 2) / 2
+// and phi(x) = exp(-x^2 / 2) / sqrt(2 pi). erfc comes from the Chebyshev fit of Numerical
+// Recipes (Press et al., 2nd ed., section 6.2, erfcc):
+//     erfc(z) = t exp(-z^2 + P(t)),  t = 1 / (1 + z / 2),  z >= 0,
+// fractional error below 1.2e-7 for every z >= 0, so Phi keeps its relative accuracy in
+// the lower tail. One v_rcp, one v_exp and a 9-term Horner polynomial: about a fifth of
+// the VALU work of the library erff.
+__device__ __forceinline__ float erfc_pos(float z) {
+  const float t = __builtin_amdgcn_rcpf(fmaf(0.5f, z, 1.0f));
+  float p = 0.17087277f;
+  p = fmaf(t, p, -0.82215223f);
+  p = fmaf(t, p, 1.48851587f);
+  p = fmaf(t, p, -1.13520398f);
+  p = fmaf(t, p, 0.27886807f);
+  p = fmaf(t, p, -0.18628806f);
+  p = fmaf(t, p, 0.09678418f);
+  p = fmaf(t, p, 0.37409196f);
+  p = fmaf(t, p, 1.00002368f);
+  const float a = fmaf(t, p, fmaf(-z, z, -1.26551223f));
+  return t * __builtin_amdgcn_exp2f(a * kLog2e);
+}
+__device__ __forceinline__ float norm_cdf(float x) {
+  const float h = 0.5f * erfc_pos(fabsf(x) * kInvSqrt2);
+  return x >= 0.0f ? 1.0f - h : h;
+}
+__device__ __forceinline__ float gelu(float x) { return x * norm_cdf(x); }
+// x phi(x), the second term of gelu'(x)
+__device__ __forceinline__ float x_pdf(float x) {
+  return x * kInvSqrt2Pi * __builtin_amdgcn_exp2f((-0.5f * kLog2e) * (x * x));
 }
 
+// ---- wave-wide sum in a fixed order (reproducible), result in every lane ------------------
+// Within each 16-lane row by DPP (swap neighbours, swap pairs, half-row mirror, row mirror:
+// every lane of the row ends with the same value, as a + b == b + a), then the four row
+// totals read out in lane order.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL,
+                                                               0xF, 0xF, false));
+}
 __device__ __forceinline__ float wave_sum(float x) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o);
-  return x;
+  x += dpp_f<0xB1>(x);   // quad_perm [1,0,3,2]
+  x += dpp_f<0x4E>(x);   // quad_perm [2,3,0,1]
+  x += dpp_f<0x141>(x);  // row_half_mirror
+  x += dpp_f<0x140>(x);  // row_mirror
+  const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 0));
+  const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 16));
+  const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 32));
+  const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 48));
+  return (r0 + r1) + (r2 + r3);
 }
 
 // Four consecutive elements of a row (one 8- or 16-byte access; D % 4 == 0 keeps each
-// group of four whole, and rows start 8- or 16-byte aligned) as float, zeros past D.
+// group of four whole, and rows start 8- or 16-byte aligned). FULL: D == NP * 256, so every
+// lane's groups are in range and the bounds tests compile away.
 template <typename T> struct Vec4;
 template <> struct Vec4<bf16> { typedef bf16x4 type; };
 template <> struct Vec4<f16> { typedef f16x4 type; };
 template <> struct Vec4<float> { typedef f32x4 type; };
+template <typename T> using vec4_t = typename Vec4<T>::type;
+
+template <bool FULL>
+__device__ __forceinline__ bool in_row(int d, int D) { return FULL || d < D; }
+template <typename T, bool FULL>
+__device__ __forceinline__ vec4_t<T> load4(const T* p, int d, int D) {
+  vec4_t<T> v = {};
+  if (in_row<FULL>(d, D)) v = *(const vec4_t<T>*)(p + d);
+  return v;
+}
 template <typename T>
-__device__ __forceinline__ f32x4 load4f(const T* p, int d, int D) {
-  f32x4 r = f32x4{0.f, 0.f, 0.f, 0.f};
-  if (d < D) {
-    const typename Vec4<T>::type v = *(const typename Vec4<T>::type*)(p + d);
+__device__ __forceinline__ f32x4 to_f32(vec4_t<T> v) {
+  f32x4 r;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) r[e] = (float)v[e];
-  }
+  for (int e = 0; e < 4; ++e) r[e] = (float)v[e];
   return r;
 }
-template <typename T>
+template <typename T, bool FULL>
 __device__ __forceinline__ void store4t(T* p, int d, int D, f32x4 v) {
-  if (d < D) {
-    typename Vec4<T>::type o;
+  if (in_row<FULL>(d, D)) {
+    vec4_t<T> o;
 #pragma unroll
     for (int e = 0; e < 4; ++e) o[e] = from_f32<T>(v[e]);
-    *(typename Vec4<T>::type*)(p + d) = o;
+    *(vec4_t<T>*)(p + d) = o;
   }
 }
+template <bool FULL>
 __device__ __forceinline__ f32x4 load4p(const float* p, int d, int D) {
-  return d < D ? *(const f32x4*)(p + d) : f32x4{0.f, 0.f, 0.f, 0.f};
+  return in_row<FULL>(d, D) ? *(const f32x4*)(p + d) : f32x4{0.f, 0.f, 0.f, 0.f};
 }
 
 // ---- forward epilogue: one wave per row ------------------------------------------------
-template <typename T, int NP>
-__global__ __launch_bounds__(64 * ROW_WAVES) void xf_fwd_kernel(
+// u = gelu(Z + b_d), mean and 1/std of u over the row, Y = (u - mean) / std * gamma + beta.
+template <typename T, int NP, bool FULL>
+__global__ __launch_bounds__(64 * FWD_WAVES) void xf_fwd_kernel(
     const T* __restrict__ Z, const float* __restrict__ bd, const float* __restrict__ gamma,
     const float* __restrict__ beta, float eps, T* __restrict__ Y, float* __restrict__ mean_out,
     float* __restrict__ rstd_out, int M, int D) {
   const int lane = threadIdx.x & 63;
-  const int64_t row = (int64_t)blockIdx.x * ROW_WAVES + (threadIdx.x >> 6);
+  const int64_t row = (int64_t)blockIdx.x * FWD_WAVES + (threadIdx.x >> 6);
   if (row >= M) return;
   const T* z = Z + row * D;
+  vec4_t<T> zr[NP];
+#pragma unroll
+  for (int p = 0; p < NP; ++p) zr[p] = load4<T, FULL>(z, p * 256 + lane * 4, D);
   f32x4 u[NP];
   float s = 0.0f;
 #pragma unroll
   for (int p = 0; p < NP; ++p) {
     const int d = p * 256 + lane * 4;
-    const f32x4 zz = load4f(z, d, D), bb = load4p(bd, d, D);
+    const f32x4 zz = to_f32<T>(zr[p]), bb = load4p<FULL>(bd, d, D);
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      u[p][e] = d < D ? gelu(zz[e] + bb[e]) : 0.0f;
+      u[p][e] = in_row<FULL>(d, D) ? gelu(zz[e] + bb[e]) : 0.0f;
       s += u[p][e];
     }
   }
@@ -96,7 +157,7 @@ __global__ __launch_bounds__(64 * ROW_WAVES) void xf_fwd_kernel(
     const int d = p * 256 + lane * 4;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const float c = d < D ? u[p][e] - mu : 0.0f;
+      const float c = in_row<FULL>(d, D) ? u[p][e] - mu : 0.0f;
       q += c * c;
     }
   }
@@ -105,11 +166,11 @@ __global__ __launch_bounds__(64 * ROW_WAVES) void xf_fwd_kernel(
 #pragma unroll
   for (int p = 0; p < NP; ++p) {
     const int d = p * 256 + lane * 4;
-    const f32x4 g = load4p(gamma, d, D), bt = load4p(beta, d, D);
+    const f32x4 g = load4p<FULL>(gamma, d, D), bt = load4p<FULL>(beta, d, D);
     f32x4 o;
 #pragma unroll
     for (int e = 0; e < 4; ++e) o[e] = (u[p][e] - mu) * rs * g[e] + bt[e];
-    store4t(y, d, D, o);
+    store4t<T, FULL>(y, d, D, o);
   }
   if (lane == 0) {
     mean_out[row] = mu;
@@ -117,40 +178,95 @@ __global__ __launch_bounds__(64 * ROW_WAVES) void xf_fwd_kernel(
   }
 }
 
-// ---- backward epilogue: ROWS_PER_WAVE rows per wave, column partials per block ----------
+// ---- backward epilogue -----------------------------------------------------------------
 // Per row: xhat = (u - mean) * rstd, g = dY * gamma,
 //          du = rstd * (g - mean_D(g) - xhat * mean_D(g * xhat)),   dZ = du * gelu'(Z + b_d).
-// The block's rows add dY * xhat, dY and dZ into per-column partials in row order (each wave
-// its rows, then the waves in order through LDS, one quantity at a time), written to
-// part[block][3][D].
-template <typename T, int NP>
-__global__ __launch_bounds__(64 * ROW_WAVES) void xf_bwd_kernel(
+// Workgroup b owns rows [b R W, (b + 1) R W) (W waves, R rows per wave, each wave R
+// consecutive rows); every wave adds dY * xhat, dY and dZ of its rows, in row order,
+// into per-column register partials, and the workgroup sums its waves' partials in wave
+// order through LDS, one quantity at a time, into part[b][3][D].
+// KEEP (NP <= 4): the row's g, xhat and gelu' stay in registers between the two passes,
+// b_d and gamma are held for the whole loop and the next row's dY and Z are loaded while
+// the current one is computed. Wider rows reload b_d and gamma from cache and recompute
+// xhat and gelu' in the second pass and run 4 waves per workgroup, so that each wave may
+// hold 512 registers.
+template <int NP> struct BwdCfg {
+  static constexpr bool keep = NP <= 4;
+  static constexpr int waves = NP <= 4 ? BWD_WAVES_NARROW : BWD_WAVES_WIDE;
+  static constexpr int threads = 64 * waves;
+};
+
+template <typename T, int NP, bool FULL>
+__global__ __launch_bounds__(BwdCfg<NP>::threads) void xf_bwd_kernel(
     const T* __restrict__ dY, const T* __restrict__ Z, const float* __restrict__ bd,
     const float* __restrict__ gamma, const float* __restrict__ mean_in,
-    const float* __restrict__ rstd_in, T* __restrict__ dZ, float* __restrict__ part, int M, int D) {
-  extern __shared__ __attribute__((aligned(16))) float xf_smem[];  // [ROW_WAVES][D]
+    const float* __restrict__ rstd_in, T* __restrict__ dZ, float* __restrict__ part, int M, int D,
+    int rows_per_wave) {
+  constexpr bool KEEP = BwdCfg<NP>::keep;
+  constexpr int W = BwdCfg<NP>::waves;
+  extern __shared__ __attribute__((aligned(16))) float xf_smem[];  // [W][D]
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int64_t row0 = ((int64_t)blockIdx.x * W + wave) * rows_per_wave;
+  const int nrows = (int)max((int64_t)0, min((int64_t)rows_per_wave, (int64_t)M - row0));
+
   f32x4 pg[NP], pb[NP], pd[NP];  // partials of dY * xhat, dY, dZ
 #pragma unroll
   for (int p = 0; p < NP; ++p) pg[p] = pb[p] = pd[p] = f32x4{0.f, 0.f, 0.f, 0.f};
-  for (int r = 0; r < ROWS_PER_WAVE; ++r) {
-    const int64_t row = (int64_t)blockIdx.x * BLOCK_ROWS + wave * ROWS_PER_WAVE + r;
-    if (row >= M) break;
+  f32x4 vb[KEEP ? NP : 1], vg[KEEP ? NP : 1];
+  if constexpr (KEEP) {
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+      vb[p] = load4p<FULL>(bd, p * 256 + lane * 4, D);
+      vg[p] = load4p<FULL>(gamma, p * 256 + lane * 4, D);
+    }
+  }
+  vec4_t<T> ny[NP], nz[NP];  // the next row's dY and Z
+  if (nrows > 0) {
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+      ny[p] = load4<T, FULL>(dY + row0 * D, p * 256 + lane * 4, D);
+      nz[p] = load4<T, FULL>(Z + row0 * D, p * 256 + lane * 4, D);
+    }
+  }
+  for (int r = 0; r < nrows; ++r) {
+    const int64_t row = row0 + r;
+    vec4_t<T> cy[NP], cz[NP];
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+      cy[p] = ny[p];
+      cz[p] = nz[p];
+    }
+    if (KEEP && r + 1 < nrows) {
+#pragma unroll
+      for (int p = 0; p < NP; ++p) {
+        ny[p] = load4<T, FULL>(dY + (row + 1) * D, p * 256 + lane * 4, D);
+        nz[p] = load4<T, FULL>(Z + (row + 1) * D, p * 256 + lane * 4, D);
+      }
+    }
     const float mu = mean_in[row], rs = rstd_in[row];
-    f32x4 xh[NP], gg[NP], dy[NP], zb[NP];
+    f32x4 xh[KEEP ? NP : 1], gg[KEEP ? NP : 1], gp[KEEP ? NP : 1];
     float s1 = 0.0f, s2 = 0.0f;
 #pragma unroll
     for (int p = 0; p < NP; ++p) {
       const int d = p * 256 + lane * 4;
-      dy[p] = load4f(dY + row * D, d, D);
-      const f32x4 zz = load4f(Z + row * D, d, D), bb = load4p(bd, d, D), ga = load4p(gamma, d, D);
+      const f32x4 dy = to_f32<T>(cy[p]), zz = to_f32<T>(cz[p]);
+      const f32x4 bb = KEEP ? vb[p] : load4p<FULL>(bd, d, D);
+      const f32x4 ga = KEEP ? vg[p] : load4p<FULL>(gamma, d, D);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        zb[p][e] = zz[e] + bb[e];
-        xh[p][e] = d < D ? (gelu(zb[p][e]) - mu) * rs : 0.0f;
-        gg[p][e] = dy[p][e] * ga[e];
-        s1 += gg[p][e];
-        s2 += gg[p][e] * xh[p][e];
+        const float zb = zz[e] + bb[e];
+        const float cdf = norm_cdf(zb);
+        const float x = in_row<FULL>(d, D) ? (zb * cdf - mu) * rs : 0.0f;
+        const float g = dy[e] * ga[e];
+        s1 += g;
+        s2 += g * x;
+        pg[p][e] += dy[e] * x;
+        pb[p][e] += dy[e];
+        if constexpr (KEEP) {
+          xh[p][e] = x;
+          gg[p][e] = g;
+          gp[p][e] = cdf + x_pdf(zb);
+        }
       }
     }
     const float c1 = wave_sum(s1) / (float)D, c2 = wave_sum(s2) / (float)D;
@@ -158,14 +274,30 @@ __global__ __launch_bounds__(64 * ROW_WAVES) void xf_bwd_kernel(
     for (int p = 0; p < NP; ++p) {
       const int d = p * 256 + lane * 4;
       f32x4 o;
+      if constexpr (KEEP) {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        o[e] = rs * (gg[p][e] - c1 - xh[p][e] * c2) * gelu_grad(zb[p][e]);
-        pg[p][e] += dy[p][e] * xh[p][e];
-        pb[p][e] += dy[p][e];
-        pd[p][e] += o[e];
+        for (int e = 0; e < 4; ++e) o[e] = rs * (gg[p][e] - c1 - xh[p][e] * c2) * gp[p][e];
+      } else {
+        const f32x4 dy = to_f32<T>(cy[p]), zz = to_f32<T>(cz[p]);
+        const f32x4 bb = load4p<FULL>(bd, d, D), ga = load4p<FULL>(gamma, d, D);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float zb = zz[e] + bb[e];
+          const float cdf = norm_cdf(zb);
+          const float x = in_row<FULL>(d, D) ? (zb * cdf - mu) * rs : 0.0f;
+          o[e] = rs * (dy[e] * ga[e] - c1 - x * c2) * (cdf + x_pdf(zb));
+        }
       }
-      store4t(dZ + row * D, d, D, o);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) pd[p][e] += o[e];
+      store4t<T, FULL>(dZ + row * D, d, D, o);
+    }
+    if (!KEEP && r + 1 < nrows) {
+#pragma unroll
+      for (int p = 0; p < NP; ++p) {
+        ny[p] = load4<T, FULL>(dY + (row + 1) * D, p * 256 + lane * 4, D);
+        nz[p] = load4<T, FULL>(Z + (row + 1) * D, p * 256 + lane * 4, D);
+      }
     }
   }
   float* mine = xf_smem + (size_t)wave * D;
@@ -175,44 +307,80 @@ __global__ __launch_bounds__(64 * ROW_WAVES) void xf_bwd_kernel(
 #pragma unroll
     for (int p = 0; p < NP; ++p) {
       const int d = p * 256 + lane * 4;
-      if (d < D) *(f32x4*)(mine + d) = qn == 0 ? pg[p] : qn == 1 ? pb[p] : pd[p];
+      if (in_row<FULL>(d, D)) *(f32x4*)(mine + d) = qn == 0 ? pg[p] : qn == 1 ? pb[p] : pd[p];
     }
     __syncthreads();
-    for (int i = threadIdx.x; i < D; i += 64 * ROW_WAVES) {
+    for (int i = threadIdx.x; i < D; i += 64 * W) {
       float acc = 0.0f;
 #pragma unroll
-      for (int w = 0; w < ROW_WAVES; ++w) acc += xf_smem[(size_t)w * D + i];
+      for (int w = 0; w < W; ++w) acc += xf_smem[(size_t)w * D + i];
       out[qn * D + i] = acc;
     }
     __syncthreads();  // the buffer is refilled with the next quantity
   }
 }
 
-// ---- column reduction: d gamma, d beta, d b_d = the blocks' partials summed in order ----
-constexpr int COL_THREADS = 256;
-__global__ __launch_bounds__(COL_THREADS) void xf_colsum_kernel(const float* __restrict__ part,
-                                                               int nblk, int D,
-                                                               float* __restrict__ dgamma,
-                                                               float* __restrict__ dbeta,
-                                                               float* __restrict__ dbd) {
-  const int i = blockIdx.x * COL_THREADS + threadIdx.x;  // i in [0, 3D)
-  if (i >= 3 * D) return;
+// ---- column reduction: d gamma, d beta, d b_d = the blocks' partials summed --------------
+// Workgroup c owns columns [64 c, 64 c + 64) of part's 3D columns, one per lane; wave w sums
+// blocks [w S, (w + 1) S) (S = ceil(nblk / COL_WAVES)) in block order, eight loads in flight,
+// and lane i of wave 0 adds the 16 wave sums in wave order. Fixed order: reproducible.
+__global__ __launch_bounds__(64 * COL_WAVES) void xf_colsum_kernel(const float* __restrict__ part,
+                                                                   int nblk, int D,
+                                                                   float* __restrict__ dgamma,
+                                                                   float* __restrict__ dbeta,
+                                                                   float* __restrict__ dbd) {
+  __shared__ float wsum[COL_WAVES][64];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int col = blockIdx.x * 64 + lane;
+  const int ncol = 3 * D;
+  const int seg = (nblk + COL_WAVES - 1) / COL_WAVES;
+  const int beg = min(nblk, wave * seg), end = min(nblk, beg + seg);
   float acc = 0.0f;
-  for (int k = 0; k < nblk; ++k) acc += part[(size_t)k * 3 * D + i];
-  const int which = i / D, d = i - which * D;
-  float* dst = which == 0 ? dgamma : which == 1 ? dbeta : dbd;
-  if (dst != nullptr) dst[d] = acc;
+  if (col < ncol) {
+    for (int k0 = beg; k0 < end; k0 += 8) {
+      float v[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[j] = k0 + j < end ? part[(size_t)(k0 + j) * ncol + col] : 0.0f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc += v[j];
+    }
+  }
+  wsum[wave][lane] = acc;
+  __syncthreads();
+  if (wave == 0 && col < ncol) {
+    float t = 0.0f;
+#pragma unroll
+    for (int w = 0; w < COL_WAVES; ++w) t += wsum[w][lane];
+    const int which = col / D, d = col - which * D;
+    float* dst = which == 0 ? dgamma : which == 1 ? dbeta : dbd;
+    if (dst != nullptr) dst[d] = t;
+  }
 }
 
 static int passes(int64_t D) { return (int)cdiv(D, 256); }
+static int bwd_waves(int64_t D) { return D <= 4 * 256 ? BWD_WAVES_NARROW : BWD_WAVES_WIDE; }
+static int rows_per_wave(int64_t M, int64_t D) {
+  return (int)std::min<int64_t>(
+      MAX_ROWS_PER_WAVE, std::max<int64_t>(1, cdiv(M, (int64_t)bwd_waves(D) * BWD_TARGET_BLOCKS)));
+}
+static int64_t bwd_blocks(int64_t M, int64_t D) {
+  return cdiv(M, (int64_t)bwd_waves(D) * rows_per_wave(M, D));
+}
 
 template <typename T>
 static int fwd(const void* z, const float* bd, const float* gamma, const float* beta, float eps,
                void* y, float* mean, float* rstd, int64_t M, int64_t D, hipStream_t st) {
-  const dim3 grid((unsigned)cdiv(M, ROW_WAVES)), block(64 * ROW_WAVES);
-#define XF_FWD(NP)                                                                          \
-  hipLaunchKernelGGL((xf_fwd_kernel<T, NP>), grid, block, 0, st, (const T*)z, bd, gamma, beta, \
-                     eps, (T*)y, mean, rstd, (int)M, (int)D)
+  const dim3 grid((unsigned)cdiv(M, FWD_WAVES)), block(64 * FWD_WAVES);
+  const bool full = D % 256 == 0;
+#define XF_FWD(NP)                                                                            \
+  do {                                                                                        \
+    if (full && D == NP * 256)                                                                \
+      hipLaunchKernelGGL((xf_fwd_kernel<T, NP, true>), grid, block, 0, st, (const T*)z, bd,   \
+                         gamma, beta, eps, (T*)y, mean, rstd, (int)M, (int)D);                \
+    else                                                                                      \
+      hipLaunchKernelGGL((xf_fwd_kernel<T, NP, false>), grid, block, 0, st, (const T*)z, bd,  \
+                         gamma, beta, eps, (T*)y, mean, rstd, (int)M, (int)D);                \
+  } while (0)
   switch (passes(D)) {
     case 1: XF_FWD(1); break;
     case 2: XF_FWD(2); break;
@@ -231,12 +399,20 @@ template <typename T>
 static int bwd(const void* dy, const void* z, const float* bd, const float* gamma,
                const float* mean, const float* rstd, void* dz, float* part, float* dgamma,
                float* dbeta, float* dbd, int64_t M, int64_t D, hipStream_t st) {
-  const int nblk = (int)cdiv(M, BLOCK_ROWS);
-  const dim3 grid((unsigned)nblk), block(64 * ROW_WAVES);
-  const size_t lds = (size_t)ROW_WAVES * D * sizeof(float);
-#define XF_BWD(NP)                                                                              \
-  hipLaunchKernelGGL((xf_bwd_kernel<T, NP>), grid, block, lds, st, (const T*)dy, (const T*)z, bd, \
-                     gamma, mean, rstd, (T*)dz, part, (int)M, (int)D)
+  const int rpw = rows_per_wave(M, D);
+  const int nblk = (int)bwd_blocks(M, D);
+  const dim3 grid((unsigned)nblk), block(64 * bwd_waves(D));
+  const size_t lds = (size_t)bwd_waves(D) * D * sizeof(float);
+  const bool full = D % 256 == 0;
+#define XF_BWD(NP)                                                                               \
+  do {                                                                                           \
+    if (full && D == NP * 256)                                                                   \
+      hipLaunchKernelGGL((xf_bwd_kernel<T, NP, true>), grid, block, lds, st, (const T*)dy,       \
+                         (const T*)z, bd, gamma, mean, rstd, (T*)dz, part, (int)M, (int)D, rpw); \
+    else                                                                                         \
+      hipLaunchKernelGGL((xf_bwd_kernel<T, NP, false>), grid, block, lds, st, (const T*)dy,      \
+                         (const T*)z, bd, gamma, mean, rstd, (T*)dz, part, (int)M, (int)D, rpw); \
+  } while (0)
   switch (passes(D)) {
     case 1: XF_BWD(1); break;
     case 2: XF_BWD(2); break;
@@ -247,8 +423,8 @@ static int bwd(const void* dy, const void* z, const float* bd, const float* gamm
     default: XF_BWD(12); break;
   }
 #undef XF_BWD
-  hipLaunchKernelGGL(xf_colsum_kernel, dim3((unsigned)cdiv(3 * D, COL_THREADS)), dim3(COL_THREADS),
-                     0, st, (const float*)part, nblk, (int)D, dgamma, dbeta, dbd);
+  hipLaunchKernelGGL(xf_colsum_kernel, dim3((unsigned)cdiv(3 * D, 64)), dim3(64 * COL_WAVES), 0, st,
+                     (const float*)part, nblk, (int)D, dgamma, dbeta, dbd);
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? SPARTON_OK : (int)e;
 }
@@ -269,7 +445,7 @@ static int xf_check(int64_t M, int64_t D, int dtype) {
 extern "C" __attribute__((visibility("default"))) size_t sparton_transform_workspace_bytes(
     int64_t M, int64_t D) {
   if (M <= 0 || D <= 0) return 0;
-  return (size_t)(cdiv(M, xf::BLOCK_ROWS) * 3 * D) * sizeof(float);
+  return (size_t)(xf::bwd_blocks(M, D) * 3 * D) * sizeof(float);
 }
 
 extern "C" __attribute__((visibility("default"))) int sparton_transform_fwd(

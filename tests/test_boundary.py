@@ -240,9 +240,14 @@ def test_transform_bwd_argument_validation(kw, code):
 
 def test_transform_workspace_size():
     L = _lib.load()
-    # fp32 column partials of (dy * xhat, dy, dz) per 32-row block
-    assert L.sparton_transform_workspace_bytes(8192, 768) == 8192 // 32 * 3 * 768 * 4
-    assert L.sparton_transform_workspace_bytes(33, 8) == 2 * 3 * 8 * 4
+    # fp32 column partials of (dy * xhat, dy, dz) per backward workgroup: 8 waves (4 when
+    # D > 1024) of R rows each, R = ceil(M / (waves * 256)) clamped to [1, 32]
+    part = lambda blocks, D: blocks * 3 * D * 4
+    assert L.sparton_transform_workspace_bytes(8192, 768) == part(256, 768)      # R = 4
+    assert L.sparton_transform_workspace_bytes(33, 8) == part(5, 8)              # R = 1
+    assert L.sparton_transform_workspace_bytes(65536, 768) == part(256, 768)     # R = 32
+    assert L.sparton_transform_workspace_bytes(200000, 768) == part(782, 768)    # R capped
+    assert L.sparton_transform_workspace_bytes(8192, 2048) == part(256, 2048)    # 4 waves, R = 8
     assert L.sparton_transform_workspace_bytes(0, 768) == 0
 
 

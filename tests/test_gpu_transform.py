@@ -51,6 +51,10 @@ CASES = [
     ("fp16", (100,), 3072, 1e-5),      # the largest D the kernels take
     ("fp32", (2, 3), 4, 1e-12),        # one partial pass
     ("bf16", (1, 1), 12, 1e-5),
+    ("fp32", (2050,), 768, 1e-12),     # 2 rows per backward wave, last workgroup partial
+    ("fp16", (16411,), 256, 1e-5),     # 9 rows per wave, ragged
+    ("bf16", (4133,), 1540, 1e-5),     # wide rows (4-wave backward), partial last pass
+    ("fp32", (9, 64), 2048, 1e-12),    # wide rows, full passes
 ]
 
 
@@ -126,6 +130,13 @@ def test_transform_module_autograd_and_autocast(device):
         ya = m(x)
     assert ya.dtype == torch.bfloat16
     close(ya, ref, 3e-2, "bf16 autocast module")
+    # the module's autograd function and the custom ops run the same kernels: bitwise equal
+    vecs = [dense.bias, ln.weight, ln.bias]
+    y_op = torch.ops.sparton.mlm_transform_fwd(x, dense.weight, *vecs, 1e-12)[0]
+    g_op = torch.autograd.grad(y_op, params, dy)
+    assert torch.equal(y_op, y)
+    for a, b in zip(g_op, g):
+        assert torch.equal(a, b)
 
 
 def test_transform_feeds_the_head(device):
