@@ -166,6 +166,36 @@ int sparton_transform_bwd(const void* dy, const void* z, const float* dense_bias
                           void* workspace, size_t workspace_bytes, int64_t M, int64_t D,
                           int dtype, void* stream);
 
+/*
+ * The SPLADE training loss on the head's reps (reference training/train.py:73-88, combined in
+ * compute_loss at :164-197). q [Bq,V] are query reps, d [Bd,V] document reps (row-major, the
+ * reps dtype; d may be NULL with Bd = 0). With S = q d^T / temperature:
+ *   CE = mean_i (logsumexp_j S[i,j] - S[i,i])   info_nce_loss, labels arange(Bq) (:73-77)
+ *   L1(x) = mean_b sum_v |x[b,v]|               l1_regularization (:80-82)
+ *   FL(x) = mean_v (sum_b x[b,v])^2             flops_regularization (:85-87)
+ *   total = w_ce CE + w_l1 (L1(q) + L1(d)) + w_flops (FL(q) + FL(d))   (:196-197)
+ * Limits: 1 <= Bq <= 128, 0 <= Bd <= 128, Bq <= Bd when Bd > 0 (the labels index d's
+ * rows), temperature > 0 and finite when Bd > 0. Computed in fp32 whatever the reps dtype.
+ */
+size_t sparton_loss_workspace_bytes(int64_t Bq, int64_t Bd, int64_t V);
+
+/*
+ * out[6] (device fp32) = (total, CE, L1(q), L1(d), FL(q), FL(d)); probs [Bq,Bd] (device
+ * fp32, unused when Bd = 0) = (softmax(S) - I) / (Bq temperature), kept for the backward.
+ */
+int sparton_loss_fwd(const void* q, const void* d, int64_t Bq, int64_t Bd, int64_t V,
+                     float temperature, float w_ce, float w_l1, float w_flops, float* out,
+                     float* probs, void* workspace, size_t workspace_bytes, int dtype,
+                     void* stream);
+
+/*
+ * grad_q [Bq,V] and grad_d [Bd,V] (reps dtype) from grad_out[6] (device fp32), the upstream
+ * gradients of the six outputs of sparton_loss_fwd, and its probs. Deterministic.
+ */
+int sparton_loss_bwd(const void* q, const void* d, const float* probs, const float* grad_out,
+                     int64_t Bq, int64_t Bd, int64_t V, float w_ce, float w_l1, float w_flops,
+                     void* grad_q, void* grad_d, int dtype, void* stream);
+
 /* Static, thread-safe description of a status code. */
 const char* sparton_strerror(int code);
 

@@ -1,0 +1,393 @@
+// The SPLADE training loss on the head's output, on gfx950 (reference training/train.py:73-88,
+// combined at :164-197). For query reps Q [Bq,V] and document reps R [Bd,V] (row-major, the
+// head's reps dtype):
+//   S      = Q R^T / T                                   in-batch scores
+//   CE     = mean_i ( logsumexp_j S[i,j] - S[i,i] )       InfoNCE with labels arange(Bq) (:73-77)
+//   L1(X)  = mean_b sum_v |X[b,v]|                        (:80-82)
+//   FL(X)  = mean_v ( sum_b X[b,v] )^2                    (:85-87)
+//   total  = w_ce CE + w_l1 (L1(Q) + L1(R)) + w_fl (FL(Q) + FL(R))    (:196-197)
+// R may be absent (Bd = 0): then CE, L1(R) and FL(R) are 0.
+//
+// Forward, three launches:
+//   loss_partial_kernel   one workgroup per 64-column vocabulary slice: stages the slice of Q
+//                         and R as fp32 in LDS and writes the slice's partial S (4x4 register
+//                         tiles), each row's partial sum |X| and the slice's sum_v (sum_b X)^2;
+//   loss_slice_sum_kernel those partials summed over the slices in a fixed order;
+//   loss_final_kernel     one workgroup: the rows' softmax, CE, the means, total, and
+//                         P = (softmax(S) - I) / (Bq T), which the backward uses.
+// Backward, one launch (loss_bwd_kernel, one workgroup per slice), with the upstream
+// gradients g[0..5] of (total, CE, L1(Q), L1(R), FL(Q), FL(R)) read from device memory:
+//   dQ = (g0 w_ce + g1) P R + (g0 w_l1 + g2) sign(Q) / Bq + (g0 w_fl + g4) 2 colsum(Q) / V
+//   dR = (g0 w_ce + g1) P^T Q + (g0 w_l1 + g3) sign(R) / Bd + (g0 w_fl + g5) 2 colsum(R) / V
+// Everything accumulates in fp32 in a fixed order, so results are bitwise reproducible.
+// The whole loss moves each of Q and R once forward and once backward: HBM-bound, small.
+
+#include <math.h>
+
+#include "sparton_common.h"
+
+namespace sparton {
+namespace loss {
+
+constexpr int SLICE = 64;            // vocabulary columns per workgroup, one per lane
+constexpr int NWAVES = 4;
+constexpr int NT = 64 * NWAVES;
+constexpr int MAX_B = 128;           // rows of Q and of R
+constexpr int LD = SLICE + 4;        // LDS row stride (floats) of a staged slice
+constexpr int SUM_WAVES = 16;        // slice reduction: 64 entries x 16 waves per workgroup
+
+__host__ __device__ constexpr int round4(int x) { return (x + 3) & ~3; }
+
+// Rows [0, Bq) of Q then [0, Bd) of R, columns [c0, c0 + 64), as fp32 into sq / sd, zeros past
+// V and in the padding rows up to a multiple of 4. Wave w stages rows w, w + 4, ...; lane l
+// column c0 + l (one 128-byte segment per row for 16-bit types). Calls row_fn(isq, row, x)
+// for every real row with the lane's value (wave-uniform control flow).
+template <typename T, typename F>
+__device__ __forceinline__ void stage_slice(const T* __restrict__ Q, const T* __restrict__ R, int Bq,
+                                            int Bd, int V, int c0, float* sq, float* sd, F row_fn) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int c = c0 + lane;
+  const int Bqp = round4(Bq), Bdp = round4(Bd);
+  for (int r = wave; r < Bqp + Bdp; r += NWAVES) {
+    const bool isq = r < Bqp;
+    const int row = isq ? r : r - Bqp;
+    const int nrows = isq ? Bq : Bd;
+    float x = 0.0f;
+    if (row < nrows && c < V) x = to_f32((isq ? Q : R)[(size_t)row * V + c]);
+    (isq ? sq : sd)[row * LD + lane] = x;
+    if (row < nrows) row_fn(isq, row, x);
+  }
+}
+
+// Partials of one slice, at part + slice * K:
+//   [0, Bq Bd)                     S without the 1/T (only when Bd > 0)
+//   [o, o + Bq), [o + Bq, o + Bq + Bd)   sum over the slice of |Q[i,:]|, |R[j,:]|
+//   o + Bq + Bd, o + Bq + Bd + 1   sum over the slice of colsum(Q)^2, colsum(R)^2
+template <typename T, int MB>
+__global__ __launch_bounds__(NT) void loss_partial_kernel(const T* __restrict__ Q,
+                                                          const T* __restrict__ R, int Bq, int Bd,
+                                                          int V, float* __restrict__ part, int K) {
+  __shared__ __attribute__((aligned(16))) float sq[MB * LD];
+  __shared__ __attribute__((aligned(16))) float sd[MB * LD];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  float* out = part + (size_t)blockIdx.x * K;
+  const int o = Bq * Bd;
+  stage_slice<T>(Q, R, Bq, Bd, V, blockIdx.x * SLICE, sq, sd, [&](bool isq, int row, float x) {
+    const float s = wave_sum(fabsf(x));
+    if (lane == 0) out[o + (isq ? 0 : Bq) + row] = s;
+  });
+  __syncthreads();
+  if (wave < 2) {  // wave 0: Q's column sums, wave 1: R's
+    const float* s = wave == 0 ? sq : sd;
+    const int nrows = wave == 0 ? Bq : Bd;
+    float cs = 0.0f;
+    for (int r = 0; r < nrows; ++r) cs += s[r * LD + lane];
+    const float t = wave_sum(cs * cs);
+    if (lane == 0) out[o + Bq + Bd + wave] = t;
+  }
+  if (Bd == 0) return;
+  const int nbi = round4(Bq) / 4, nbj = round4(Bd) / 4;
+  for (int blk = threadIdx.x; blk < nbi * nbj; blk += NT) {
+    const int i0 = (blk / nbj) * 4, j0 = (blk % nbj) * 4;
+    float acc[4][4];
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+      for (int b = 0; b < 4; ++b) acc[a][b] = 0.0f;
+#pragma unroll 4
+    for (int cc = 0; cc < SLICE; cc += 4) {
+      f32x4 qa[4], rb[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        qa[k] = *(const f32x4*)(sq + (i0 + k) * LD + cc);
+        rb[k] = *(const f32x4*)(sd + (j0 + k) * LD + cc);
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+#pragma unroll
+        for (int a = 0; a < 4; ++a)
+#pragma unroll
+          for (int b = 0; b < 4; ++b) acc[a][b] = fmaf(qa[a][e], rb[b][e], acc[a][b]);
+    }
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+      for (int b = 0; b < 4; ++b)
+        if (i0 + a < Bq && j0 + b < Bd) out[(i0 + a) * Bd + j0 + b] = acc[a][b];
+  }
+}
+
+// sums[k] = sum over slices of part[slice][k]. Workgroup g owns entries [64 g, 64 g + 64), one
+// per lane; wave w sums slices [w S, (w + 1) S) in order (S = ceil(nslice / 16)), eight loads
+// in flight, and wave 0 adds the 16 wave sums in wave order.
+__global__ __launch_bounds__(64 * SUM_WAVES) void loss_slice_sum_kernel(const float* __restrict__ part,
+                                                                       int nslice, int K,
+                                                                       float* __restrict__ sums) {
+  __shared__ float wsum[SUM_WAVES][64];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int k = blockIdx.x * 64 + lane;
+  const int seg = (nslice + SUM_WAVES - 1) / SUM_WAVES;
+  const int beg = min(nslice, wave * seg), end = min(nslice, beg + seg);
+  float acc = 0.0f;
+  if (k < K) {
+    for (int s0 = beg; s0 < end; s0 += 8) {
+      float v[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[j] = s0 + j < end ? part[(size_t)(s0 + j) * K + k] : 0.0f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc += v[j];
+    }
+  }
+  wsum[wave][lane] = acc;
+  __syncthreads();
+  if (wave == 0 && k < K) {
+    float t = 0.0f;
+#pragma unroll
+    for (int w = 0; w < SUM_WAVES; ++w) t += wsum[w][lane];
+    sums[k] = t;
+  }
+}
+
+// One workgroup. Wave w takes score rows w, w + 4, ...; lane l holds columns l and l + 64.
+// out = (total, CE, L1(Q), L1(R), FL(Q), FL(R)); probs[i][j] = (softmax_j(S[i,:]) - [i == j]) / (Bq T).
+__global__ __launch_bounds__(NT) void loss_final_kernel(const float* __restrict__ sums, int Bq, int Bd,
+                                                        int V, float inv_t, float w_ce, float w_l1,
+                                                        float w_fl, float* __restrict__ out,
+                                                        float* __restrict__ probs) {
+  __shared__ float row_loss[MAX_B];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  if (Bd > 0) {
+    const float pscale = inv_t / (float)Bq;
+    for (int i = wave; i < Bq; i += NWAVES) {
+      const float* srow = sums + (size_t)i * Bd;
+      const bool h0 = lane < Bd, h1 = lane + 64 < Bd;
+      const float x0 = h0 ? srow[lane] * inv_t : -INFINITY;
+      const float x1 = h1 ? srow[lane + 64] * inv_t : -INFINITY;
+      const float m = wave_max(fmaxf(x0, x1));
+      const float e0 = h0 ? expf(x0 - m) : 0.0f, e1 = h1 ? expf(x1 - m) : 0.0f;
+      const float s = wave_sum(e0 + e1);
+      if (lane == 0) row_loss[i] = m + logf(s) - srow[i] * inv_t;
+      const float rs = 1.0f / s;
+      if (h0) probs[(size_t)i * Bd + lane] = (e0 * rs - (lane == i ? 1.0f : 0.0f)) * pscale;
+      if (h1) probs[(size_t)i * Bd + lane + 64] = (e1 * rs - (lane + 64 == i ? 1.0f : 0.0f)) * pscale;
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const int o = Bq * Bd;
+    float ce = 0.0f, l1q = 0.0f, l1d = 0.0f;
+    for (int i = 0; i < (Bd > 0 ? Bq : 0); ++i) ce += row_loss[i];
+    for (int i = 0; i < Bq; ++i) l1q += sums[o + i];
+    for (int j = 0; j < Bd; ++j) l1d += sums[o + Bq + j];
+    ce = Bd > 0 ? ce / (float)Bq : 0.0f;
+    l1q /= (float)Bq;
+    l1d = Bd > 0 ? l1d / (float)Bd : 0.0f;
+    const float flq = sums[o + Bq + Bd] / (float)V, fld = sums[o + Bq + Bd + 1] / (float)V;
+    out[0] = w_ce * ce + w_l1 * (l1q + l1d) + w_fl * (flq + fld);
+    out[1] = ce;
+    out[2] = l1q;
+    out[3] = l1d;
+    out[4] = flq;
+    out[5] = fld;
+  }
+}
+
+// One workgroup per slice: stages Q, R and P, the slice's column sums, then 4x4 tiles of
+// dQ (rows i0..i0+3 x 4 columns) and dR (rows j0..j0+3 x 4 columns), each thread a tile.
+template <typename T, int MB>
+__global__ __launch_bounds__(NT) void loss_bwd_kernel(const T* __restrict__ Q, const T* __restrict__ R,
+                                                      const float* __restrict__ P,
+                                                      const float* __restrict__ g, int Bq, int Bd,
+                                                      int V, float w_ce, float w_l1, float w_fl,
+                                                      T* __restrict__ GQ, T* __restrict__ GR) {
+  constexpr int PLD = MB + 4;
+  __shared__ __attribute__((aligned(16))) float sq[MB * LD];
+  __shared__ __attribute__((aligned(16))) float sd[MB * LD];
+  __shared__ __attribute__((aligned(16))) float sp[MB * PLD];
+  __shared__ float colsum[2][SLICE];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int c0 = blockIdx.x * SLICE;
+  const int Bqp = round4(Bq), Bdp = round4(Bd);
+  stage_slice<T>(Q, R, Bq, Bd, V, c0, sq, sd, [](bool, int, float) {});
+  for (int e = threadIdx.x; e < Bqp * Bdp; e += NT) {  // P, zero-padded to Bqp x Bdp
+    const int i = e / Bdp, j = e - i * Bdp;
+    sp[i * PLD + j] = (i < Bq && j < Bd) ? P[(size_t)i * Bd + j] : 0.0f;
+  }
+  __syncthreads();
+  if (wave < 2) {
+    const float* s = wave == 0 ? sq : sd;
+    const int nrows = wave == 0 ? Bq : Bd;
+    float cs = 0.0f;
+    for (int r = 0; r < nrows; ++r) cs += s[r * LD + lane];
+    colsum[wave][lane] = cs;
+  }
+  __syncthreads();
+  const float g0 = g[0];
+  const float c_ce = g0 * w_ce + g[1];
+  const float c_sq = (g0 * w_l1 + g[2]) / (float)Bq;
+  const float c_sd = Bd > 0 ? (g0 * w_l1 + g[3]) / (float)Bd : 0.0f;
+  const float c_fq = 2.0f * (g0 * w_fl + g[4]) / (float)V;
+  const float c_fd = 2.0f * (g0 * w_fl + g[5]) / (float)V;
+  const int nbi = Bqp / 4, nbj = Bdp / 4;
+  constexpr int CT = SLICE / 4;  // column tiles per slice
+  for (int t = threadIdx.x; t < (nbi + nbj) * CT; t += NT) {
+    const bool isq = t < nbi * CT;
+    const int tt = isq ? t : t - nbi * CT;
+    const int r0 = (tt / CT) * 4, cc = (tt % CT) * 4;
+    float acc[4][4];
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+      for (int b = 0; b < 4; ++b) acc[a][b] = 0.0f;
+    if (isq) {  // sum_j P[i][j] R[j][c]
+      for (int j = 0; j < Bd; ++j) {
+        const f32x4 rv = *(const f32x4*)(sd + j * LD + cc);
+        float p[4];
+#pragma unroll
+        for (int a = 0; a < 4; ++a) p[a] = sp[(r0 + a) * PLD + j];
+#pragma unroll
+        for (int a = 0; a < 4; ++a)
+#pragma unroll
+          for (int b = 0; b < 4; ++b) acc[a][b] = fmaf(p[a], rv[b], acc[a][b]);
+      }
+    } else {  // sum_i P[i][j] Q[i][c]
+      for (int i = 0; i < Bq; ++i) {
+        const f32x4 qv = *(const f32x4*)(sq + i * LD + cc);
+        const f32x4 p = *(const f32x4*)(sp + i * PLD + r0);
+#pragma unroll
+        for (int a = 0; a < 4; ++a)
+#pragma unroll
+          for (int b = 0; b < 4; ++b) acc[a][b] = fmaf(p[a], qv[b], acc[a][b]);
+      }
+    }
+    const float* own = isq ? sq : sd;
+    const float* cs = colsum[isq ? 0 : 1];
+    const float c_s = isq ? c_sq : c_sd, c_f = isq ? c_fq : c_fd;
+    const int nrows = isq ? Bq : Bd;
+    T* G = isq ? GQ : GR;
+#pragma unroll
+    for (int a = 0; a < 4; ++a) {
+      const int row = r0 + a;
+      if (row >= nrows) continue;
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        const int c = c0 + cc + b;
+        if (c >= V) continue;
+        const float x = own[row * LD + cc + b];
+        const float sg = x > 0.0f ? 1.0f : (x < 0.0f ? -1.0f : 0.0f);
+        G[(size_t)row * V + c] = from_f32<T>(c_ce * acc[a][b] + c_s * sg + c_f * cs[cc + b]);
+      }
+    }
+  }
+}
+
+static int64_t slices(int64_t V) { return cdiv(V, (int64_t)SLICE); }
+static int64_t entries(int64_t Bq, int64_t Bd) { return Bq * Bd + Bq + Bd + 2; }
+
+template <typename T, int MB>
+static void launch_fwd(const void* q, const void* d, int Bq, int Bd, int V, float* part, int K,
+                       hipStream_t st) {
+  hipLaunchKernelGGL((loss_partial_kernel<T, MB>), dim3((unsigned)slices(V)), dim3(NT), 0, st,
+                     (const T*)q, (const T*)d, Bq, Bd, V, part, K);
+}
+template <typename T, int MB>
+static void launch_bwd(const void* q, const void* d, const float* P, const float* g, int Bq, int Bd,
+                       int V, float w_ce, float w_l1, float w_fl, void* gq, void* gd, hipStream_t st) {
+  hipLaunchKernelGGL((loss_bwd_kernel<T, MB>), dim3((unsigned)slices(V)), dim3(NT), 0, st,
+                     (const T*)q, (const T*)d, P, g, Bq, Bd, V, w_ce, w_l1, w_fl, (T*)gq, (T*)gd);
+}
+
+template <typename T>
+static void fwd_partial(const void* q, const void* d, int Bq, int Bd, int V, float* part, int K,
+                        hipStream_t st) {
+  const int mb = Bq > Bd ? Bq : Bd;
+  if (mb <= 32) launch_fwd<T, 32>(q, d, Bq, Bd, V, part, K, st);
+  else if (mb <= 64) launch_fwd<T, 64>(q, d, Bq, Bd, V, part, K, st);
+  else launch_fwd<T, 128>(q, d, Bq, Bd, V, part, K, st);
+}
+template <typename T>
+static void bwd_all(const void* q, const void* d, const float* P, const float* g, int Bq, int Bd,
+                    int V, float w_ce, float w_l1, float w_fl, void* gq, void* gd, hipStream_t st) {
+  const int mb = Bq > Bd ? Bq : Bd;
+  if (mb <= 32) launch_bwd<T, 32>(q, d, P, g, Bq, Bd, V, w_ce, w_l1, w_fl, gq, gd, st);
+  else if (mb <= 64) launch_bwd<T, 64>(q, d, P, g, Bq, Bd, V, w_ce, w_l1, w_fl, gq, gd, st);
+  else launch_bwd<T, 128>(q, d, P, g, Bq, Bd, V, w_ce, w_l1, w_fl, gq, gd, st);
+}
+
+}  // namespace loss
+}  // namespace sparton
+
+using namespace sparton;
+
+static int loss_check(int64_t Bq, int64_t Bd, int64_t V, int dtype) {
+  if (dtype < SPARTON_F32 || dtype > SPARTON_F16) return SPARTON_EINVAL;
+  if (Bq < 1 || Bd < 0 || V < 1) return SPARTON_EINVAL;
+  if (Bq > loss::MAX_B || Bd > loss::MAX_B || V > INT32_MAX) return SPARTON_EUNSUPPORTED;
+  if (Bd > 0 && Bq > Bd) return SPARTON_EINVAL;  // labels arange(Bq) index R's rows
+  return SPARTON_OK;
+}
+
+extern "C" __attribute__((visibility("default"))) size_t sparton_loss_workspace_bytes(int64_t Bq,
+                                                                                      int64_t Bd,
+                                                                                      int64_t V) {
+  if (Bq < 1 || Bd < 0 || V < 1) return 0;
+  return (size_t)((loss::slices(V) + 1) * loss::entries(Bq, Bd)) * sizeof(float);
+}
+
+extern "C" __attribute__((visibility("default"))) int sparton_loss_fwd(
+    const void* q, const void* d, int64_t Bq, int64_t Bd, int64_t V, float temperature, float w_ce,
+    float w_l1, float w_flops, float* out, float* probs, void* workspace, size_t workspace_bytes,
+    int dtype, void* stream) {
+  const int rc = loss_check(Bq, Bd, V, dtype);
+  if (rc != SPARTON_OK) return rc;
+  if (q == nullptr || out == nullptr || (Bd > 0 && (d == nullptr || probs == nullptr)))
+    return SPARTON_EINVAL;
+  if (Bd > 0 && !(temperature > 0.0f && temperature < INFINITY)) return SPARTON_EINVAL;
+  if (workspace == nullptr || workspace_bytes < sparton_loss_workspace_bytes(Bq, Bd, V))
+    return SPARTON_EWORKSPACE;
+  if ((uintptr_t)workspace % 16 != 0) return SPARTON_EALIGN;
+  hipStream_t st = (hipStream_t)stream;
+  const int K = (int)loss::entries(Bq, Bd), ns = (int)loss::slices(V);
+  float* part = (float*)workspace;
+  float* sums = part + (size_t)ns * K;
+  switch (dtype) {
+    case SPARTON_BF16: loss::fwd_partial<bf16>(q, d, (int)Bq, (int)Bd, (int)V, part, K, st); break;
+    case SPARTON_F16: loss::fwd_partial<f16>(q, d, (int)Bq, (int)Bd, (int)V, part, K, st); break;
+    default: loss::fwd_partial<float>(q, d, (int)Bq, (int)Bd, (int)V, part, K, st); break;
+  }
+  hipLaunchKernelGGL(loss::loss_slice_sum_kernel, dim3((unsigned)cdiv((int64_t)K, (int64_t)64)),
+                     dim3(64 * loss::SUM_WAVES), 0, st, (const float*)part, ns, K, sums);
+  hipLaunchKernelGGL(loss::loss_final_kernel, dim3(1), dim3(loss::NT), 0, st, (const float*)sums,
+                     (int)Bq, (int)Bd, (int)V, Bd > 0 ? 1.0f / temperature : 0.0f, w_ce, w_l1,
+                     w_flops, out, probs);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? SPARTON_OK : (int)e;
+}
+
+extern "C" __attribute__((visibility("default"))) int sparton_loss_bwd(
+    const void* q, const void* d, const float* probs, const float* grad_out, int64_t Bq, int64_t Bd,
+    int64_t V, float w_ce, float w_l1, float w_flops, void* grad_q, void* grad_d, int dtype,
+    void* stream) {
+  const int rc = loss_check(Bq, Bd, V, dtype);
+  if (rc != SPARTON_OK) return rc;
+  if (q == nullptr || grad_out == nullptr || grad_q == nullptr ||
+      (Bd > 0 && (d == nullptr || probs == nullptr || grad_d == nullptr)))
+    return SPARTON_EINVAL;
+  hipStream_t st = (hipStream_t)stream;
+  switch (dtype) {
+    case SPARTON_BF16:
+      loss::bwd_all<bf16>(q, d, probs, grad_out, (int)Bq, (int)Bd, (int)V, w_ce, w_l1, w_flops, grad_q,
+                          grad_d, st);
+      break;
+    case SPARTON_F16:
+      loss::bwd_all<f16>(q, d, probs, grad_out, (int)Bq, (int)Bd, (int)V, w_ce, w_l1, w_flops, grad_q,
+                         grad_d, st);
+      break;
+    default:
+      loss::bwd_all<float>(q, d, probs, grad_out, (int)Bq, (int)Bd, (int)V, w_ce, w_l1, w_flops,
+                           grad_q, grad_d, st);
+      break;
+  }
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? SPARTON_OK : (int)e;
+}

@@ -65,27 +65,6 @@ __device__ __forceinline__ float x_pdf(float x) {
   return x * kInvSqrt2Pi * __builtin_amdgcn_exp2f((-0.5f * kLog2e) * (x * x));
 }
 
-// ---- wave-wide sum in a fixed order (reproducible), result in every lane ------------------
-// Within each 16-lane row by DPP (swap neighbours, swap pairs, half-row mirror, row mirror:
-// every lane of the row ends with the same value, as a + b == b + a), then the four row
-// totals read out in lane order.
-template <int CTRL>
-__device__ __forceinline__ float dpp_f(float x) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL,
-                                                               0xF, 0xF, false));
-}
-__device__ __forceinline__ float wave_sum(float x) {
-  x += dpp_f<0xB1>(x);   // quad_perm [1,0,3,2]
-  x += dpp_f<0x4E>(x);   // quad_perm [2,3,0,1]
-  x += dpp_f<0x141>(x);  // row_half_mirror
-  x += dpp_f<0x140>(x);  // row_mirror
-  const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 0));
-  const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 16));
-  const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 32));
-  const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 48));
-  return (r0 + r1) + (r2 + r3);
-}
-
 // Four consecutive elements of a row (one 8- or 16-byte access; D % 4 == 0 keeps each
 // group of four whole, and rows start 8- or 16-byte aligned). FULL: D == NP * 256, so every
 // lane's groups are in range and the bounds tests compile away.

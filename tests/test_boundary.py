@@ -267,3 +267,55 @@ def test_transform_module_surface():
         sparton_amd.SpartonMLMTransform(torch.nn.Linear(64, 32), ln)
     with pytest.raises(RuntimeError, match="ROCm/HIP device tensors"):
         m(torch.randn(2, 3, 64))
+
+
+# ---- the SPLADE loss entry points (argument checks only; nothing is launched) ----
+def loss_fwd(**kw):
+    a = dict(q=P, d=P, Bq=4, Bd=8, V=100, T=1.0, w_ce=1.0, w_l1=0.0, w_fl=0.0, out=P, probs=P,
+             ws=P, ws_bytes=1 << 30, dtype=1, stream=None)
+    a.update(kw)
+    return _lib.load().sparton_loss_fwd(*a.values())
+
+
+def loss_bwd(**kw):
+    a = dict(q=P, d=P, probs=P, g=P, Bq=4, Bd=8, V=100, w_ce=1.0, w_l1=0.0, w_fl=0.0, gq=P, gd=P,
+             dtype=1, stream=None)
+    a.update(kw)
+    return _lib.load().sparton_loss_bwd(*a.values())
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(Bq=0), -1), (dict(V=0), -1), (dict(dtype=3), -1), (dict(Bq=9), -1),   # Bq > Bd
+    (dict(q=None), -1), (dict(d=None), -1), (dict(probs=None), -1), (dict(out=None), -1),
+    (dict(T=0.0), -1), (dict(T=float("inf")), -1), (dict(T=float("nan")), -1),
+    (dict(Bq=129, Bd=129), -3), (dict(Bd=200), -3),
+    (dict(ws=None), -4), (dict(ws_bytes=64), -4), (dict(ws=P + 4), -2),
+])
+def test_loss_fwd_argument_validation(kw, code):
+    assert loss_fwd(**kw) == code
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(Bq=0), -1), (dict(g=None), -1), (dict(gq=None), -1), (dict(gd=None), -1),
+    (dict(probs=None), -1), (dict(Bq=9), -1), (dict(Bd=129), -3), (dict(dtype=-1), -1),
+])
+def test_loss_bwd_argument_validation(kw, code):
+    assert loss_bwd(**kw) == code
+
+
+def test_loss_workspace_size():
+    L = _lib.load()
+    # fp32 partials per 64-column slice plus their sums: Bq*Bd scores, Bq + Bd row sums of
+    # |x| and two sums of squared column sums
+    assert L.sparton_loss_workspace_bytes(32, 32, 30522) == (477 + 1) * (1024 + 64 + 2) * 4
+    assert L.sparton_loss_workspace_bytes(4, 0, 64) == 2 * (4 + 2) * 4
+    assert L.sparton_loss_workspace_bytes(0, 4, 64) == 0
+
+
+def test_loss_module_surface():
+    from sparton_amd import loss
+    assert loss.get_reg_weight(50, 100, 1e-3) == pytest.approx(5e-4)
+    assert loss.get_reg_weight(5, 0, 1e-3) == 1e-3
+    with pytest.raises(RuntimeError, match="ROCm/HIP device tensors"):
+        loss.splade_loss(torch.rand(2, 10), torch.rand(2, 10))
+    assert callable(torch.ops.sparton.splade_loss_fwd) and callable(torch.ops.sparton.splade_loss_bwd)
