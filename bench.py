@@ -23,6 +23,8 @@ kernels drains the queue, so the per-op events live in their own pass.
   transform     the MLM transform in front of the head (dense, gelu, LayerNorm) at the
                 same rows and width: fused op vs eager torch fwd+bwd, and each HIP
                 epilogue kernel's compulsory bytes / mean duration vs 8 TB/s.
+  loss          the SPLADE loss on reps of this shape (B queries, B documents): fused
+                vs eager torch fwd+bwd, and the HIP passes' compulsory bytes vs 8 TB/s.
   cpu_baseline  the reference's torch head (training/model.py:56-62, restated in
                 oracle/) fwd+bwd on the host cores, on a bounded sample of batch rows.
 """
@@ -271,6 +273,79 @@ def transform_timing(torch, w, dev, reps_n):
             "epilogue_bwd": roof(bwd_bytes, bwd_epi_ms)}
 
 
+def loss_timing(torch, w, dev, reps_n):
+    """The SPLADE loss on this workload's reps shape (training/train.py:73-197): B query and
+    B document reps [B, V] in the reps dtype, train.py's default weights. sparton_amd.loss
+    against the same formulas in eager torch, both fwd+bwd through autograd, and the two HIP
+    passes alone against the bytes they must move (q and d read; q and d read, dq and dd
+    written)."""
+    import torch.nn.functional as F
+    from sparton_amd import _lib
+    from sparton_amd import loss as sl
+    B, V, dt = w.B, w.V, w.dtype
+    if B > sl.MAX_ROWS:
+        return None
+    gen = torch.Generator(device=dev).manual_seed(11)
+
+    def reps():
+        x = torch.randn(B, V, device=dev, generator=gen) - 1.0
+        return torch.log1p(torch.relu(x)).to(dt).requires_grad_()
+
+    q, d = reps(), reps()
+    T, w_l1, w_fl = 1.0, 1e-4, 1e-4
+
+    def fused():
+        q.grad = d.grad = None
+        sl.splade_loss(q, d, T, w_l1, w_fl).total.backward()
+
+    def eager():
+        q.grad = d.grad = None
+        s = torch.matmul(q, d.t()) / T
+        ce = F.cross_entropy(s, torch.arange(B, device=dev))
+        reg = (w_l1 * (q.abs().sum(-1).mean() + d.abs().sum(-1).mean())
+               + w_fl * ((q.sum(0) ** 2).mean() + (d.sum(0) ** 2).mean()))
+        (ce + reg).backward()
+
+    fused_ms, fused_host, _ = time_device(torch, fused, reps_n)
+    eager_ms, eager_host, _ = time_device(torch, eager, reps_n)
+
+    L = _lib.load()
+    code, stream = _lib.DTYPE_CODE[dt], torch.cuda.current_stream().cuda_stream
+    out = torch.empty(6, dtype=torch.float32, device=dev)
+    probs = torch.empty(B, B, dtype=torch.float32, device=dev)
+    g = torch.ones(6, dtype=torch.float32, device=dev)
+    gq, gd = torch.empty_like(q), torch.empty_like(d)
+    nbytes = int(L.sparton_loss_workspace_bytes(B, B, V))
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+
+    def fwd():
+        _lib.check(L.sparton_loss_fwd(q.data_ptr(), d.data_ptr(), B, B, V, T, 1.0, w_l1, w_fl,
+                                      out.data_ptr(), probs.data_ptr(), ws.data_ptr(), nbytes,
+                                      code, stream), "sparton_loss_fwd")
+
+    def bwd():
+        _lib.check(L.sparton_loss_bwd(q.data_ptr(), d.data_ptr(), probs.data_ptr(), g.data_ptr(),
+                                      B, B, V, 1.0, w_l1, w_fl, gq.data_ptr(), gd.data_ptr(), code,
+                                      stream), "sparton_loss_bwd")
+
+    fwd_ms = time_events(torch, fwd, reps_n)
+    bwd_ms = time_events(torch, bwd, reps_n)
+    e = q.element_size()
+
+    def roof(nbytes_, ms):
+        gbs = nbytes_ / (ms * 1e-3) / 1e9
+        return {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                "frac": round(gbs / PEAK_HBM_GBS, 4), "bytes_per_call": nbytes_, "mean_ms": round(ms, 4)}
+
+    return {"Bq": B, "Bd": B, "V": V, "dtype": DTYPE_NAME[str(dt)],
+            "fwd_bwd_ms": round(fused_ms, 4), "eager_torch_fwd_bwd_ms": round(eager_ms, 4),
+            "speedup_vs_eager": round(eager_ms / fused_ms, 3),
+            "timing": "HIP events over back-to-back autograd fwd+bwd, queue pre-filled by a spin "
+                      "kernel so host dispatch is hidden",
+            "host_bound_ms": {"sparton": round(fused_host, 4), "eager_torch": round(eager_host, 4)},
+            "fwd_passes": roof(2 * B * V * e, fwd_ms), "bwd_pass": roof(4 * B * V * e, bwd_ms)}
+
+
 def main():
     args = parse()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -359,6 +434,7 @@ def main():
     fwd_ms, bwd_ms = fwd_live, bwd_live
     main_ms = time_main_kernel(torch, Hd.contiguous(), Wd.contiguous(), bd, mask, args.kernel_reps)
     xf = transform_timing(torch, w, dev, args.kernel_reps)
+    lossr = loss_timing(torch, w, dev, args.kernel_reps)
     if args.copy_probe_mib > 0:
         src = torch.empty(args.copy_probe_mib << 20, dtype=torch.uint8, device=dev)
         dst = torch.empty_like(src)
@@ -430,6 +506,7 @@ def main():
         "peak_extra_gb": round((peak_bytes - input_bytes) / 1e9, 4),
         "bsv_logits_gb_avoided": round(w.B * w.S * w.V * e / 1e9, 3),
         "transform": xf,
+        "loss": lossr,
         "cpu_baseline": None,
     }
     if not args.no_cpu_baseline and int(os.environ.get("RANK", "0")) == 0:

@@ -10,8 +10,9 @@
 //
 // Forward, three launches:
 //   loss_partial_kernel   one workgroup per 64-column vocabulary slice: stages the slice of Q
-//                         and R as fp32 in LDS and writes the slice's partial S (4x4 register
-//                         tiles), each row's partial sum |X| and the slice's sum_v (sum_b X)^2;
+//                         and R as fp32 in LDS and writes the slice's partial S (4x4 or 2x2
+//                         register tiles), each row's partial sum |X| and the slice's
+//                         sum_v (sum_b X)^2;
 //   loss_slice_sum_kernel those partials summed over the slices in a fixed order;
 //   loss_final_kernel     one workgroup: the rows' softmax, CE, the means, total, and
 //                         P = (softmax(S) - I) / (Bq T), which the backward uses.
@@ -40,22 +41,34 @@ __host__ __device__ constexpr int round4(int x) { return (x + 3) & ~3; }
 
 // Rows [0, Bq) of Q then [0, Bd) of R, columns [c0, c0 + 64), as fp32 into sq / sd, zeros past
 // V and in the padding rows up to a multiple of 4. Wave w stages rows w, w + 4, ...; lane l
-// column c0 + l (one 128-byte segment per row for 16-bit types). Calls row_fn(isq, row, x)
-// for every real row with the lane's value (wave-uniform control flow).
-template <typename T, typename F>
+// column c0 + l (one 128-byte segment per row for 16-bit types). All of a wave's loads are
+// issued before the first is used, so they share one round trip. Then row_fn(isq, row, x)
+// runs for every real row with the lane's value (wave-uniform control flow).
+template <typename T, int MB, typename F>
 __device__ __forceinline__ void stage_slice(const T* __restrict__ Q, const T* __restrict__ R, int Bq,
                                             int Bd, int V, int c0, float* sq, float* sd, F row_fn) {
+  constexpr int RPW = 2 * MB / NWAVES;  // rows per wave at most (Q and R padded to MB each)
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int c = c0 + lane;
   const int Bqp = round4(Bq), Bdp = round4(Bd);
-  for (int r = wave; r < Bqp + Bdp; r += NWAVES) {
+  T raw[RPW];
+#pragma unroll
+  for (int k = 0; k < RPW; ++k) {
+    const int r = wave + k * NWAVES;
     const bool isq = r < Bqp;
     const int row = isq ? r : r - Bqp;
-    const int nrows = isq ? Bq : Bd;
-    float x = 0.0f;
-    if (row < nrows && c < V) x = to_f32((isq ? Q : R)[(size_t)row * V + c]);
+    const bool real = r < Bqp + Bdp && row < (isq ? Bq : Bd) && c < V;
+    raw[k] = real ? (isq ? Q : R)[(size_t)row * V + c] : T(0.0f);
+  }
+#pragma unroll
+  for (int k = 0; k < RPW; ++k) {
+    const int r = wave + k * NWAVES;
+    if (r >= Bqp + Bdp) break;
+    const bool isq = r < Bqp;
+    const int row = isq ? r : r - Bqp;
+    const float x = to_f32(raw[k]);
     (isq ? sq : sd)[row * LD + lane] = x;
-    if (row < nrows) row_fn(isq, row, x);
+    if (row < (isq ? Bq : Bd)) row_fn(isq, row, x);
   }
 }
 
@@ -63,7 +76,7 @@ __device__ __forceinline__ void stage_slice(const T* __restrict__ Q, const T* __
 //   [0, Bq Bd)                     S without the 1/T (only when Bd > 0)
 //   [o, o + Bq), [o + Bq, o + Bq + Bd)   sum over the slice of |Q[i,:]|, |R[j,:]|
 //   o + Bq + Bd, o + Bq + Bd + 1   sum over the slice of colsum(Q)^2, colsum(R)^2
-template <typename T, int MB>
+template <typename T, int MB, int TM>
 __global__ __launch_bounds__(NT) void loss_partial_kernel(const T* __restrict__ Q,
                                                           const T* __restrict__ R, int Bq, int Bd,
                                                           int V, float* __restrict__ part, int K) {
@@ -72,7 +85,7 @@ __global__ __launch_bounds__(NT) void loss_partial_kernel(const T* __restrict__ 
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   float* out = part + (size_t)blockIdx.x * K;
   const int o = Bq * Bd;
-  stage_slice<T>(Q, R, Bq, Bd, V, blockIdx.x * SLICE, sq, sd, [&](bool isq, int row, float x) {
+  stage_slice<T, MB>(Q, R, Bq, Bd, V, blockIdx.x * SLICE, sq, sd, [&](bool isq, int row, float x) {
     const float s = wave_sum(fabsf(x));
     if (lane == 0) out[o + (isq ? 0 : Bq) + row] = s;
   });
@@ -86,33 +99,34 @@ __global__ __launch_bounds__(NT) void loss_partial_kernel(const T* __restrict__ 
     if (lane == 0) out[o + Bq + Bd + wave] = t;
   }
   if (Bd == 0) return;
-  const int nbi = round4(Bq) / 4, nbj = round4(Bd) / 4;
+  // S tiles of TM x TM (TM = 2 when 4 x 4 tiles would leave threads idle)
+  const int nbi = round4(Bq) / TM, nbj = round4(Bd) / TM;
   for (int blk = threadIdx.x; blk < nbi * nbj; blk += NT) {
-    const int i0 = (blk / nbj) * 4, j0 = (blk % nbj) * 4;
-    float acc[4][4];
+    const int i0 = (blk / nbj) * TM, j0 = (blk % nbj) * TM;
+    float acc[TM][TM];
 #pragma unroll
-    for (int a = 0; a < 4; ++a)
+    for (int a = 0; a < TM; ++a)
 #pragma unroll
-      for (int b = 0; b < 4; ++b) acc[a][b] = 0.0f;
+      for (int b = 0; b < TM; ++b) acc[a][b] = 0.0f;
 #pragma unroll 4
     for (int cc = 0; cc < SLICE; cc += 4) {
-      f32x4 qa[4], rb[4];
+      f32x4 qa[TM], rb[TM];
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
+      for (int k = 0; k < TM; ++k) {
         qa[k] = *(const f32x4*)(sq + (i0 + k) * LD + cc);
         rb[k] = *(const f32x4*)(sd + (j0 + k) * LD + cc);
       }
 #pragma unroll
       for (int e = 0; e < 4; ++e)
 #pragma unroll
-        for (int a = 0; a < 4; ++a)
+        for (int a = 0; a < TM; ++a)
 #pragma unroll
-          for (int b = 0; b < 4; ++b) acc[a][b] = fmaf(qa[a][e], rb[b][e], acc[a][b]);
+          for (int b = 0; b < TM; ++b) acc[a][b] = fmaf(qa[a][e], rb[b][e], acc[a][b]);
     }
 #pragma unroll
-    for (int a = 0; a < 4; ++a)
+    for (int a = 0; a < TM; ++a)
 #pragma unroll
-      for (int b = 0; b < 4; ++b)
+      for (int b = 0; b < TM; ++b)
         if (i0 + a < Bq && j0 + b < Bd) out[(i0 + a) * Bd + j0 + b] = acc[a][b];
   }
 }
@@ -155,11 +169,29 @@ __global__ __launch_bounds__(NT) void loss_final_kernel(const float* __restrict_
                                                         float w_fl, float* __restrict__ out,
                                                         float* __restrict__ probs) {
   __shared__ float row_loss[MAX_B];
+  __shared__ float tail[2 * MAX_B + 2];  // the row sums of |x| and the two FLOPS sums
+  __shared__ float ss[MAX_B * MAX_B];     // S without the 1/T
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int o = Bq * Bd, n = o + Bq + Bd + 2;
+  for (int k0 = 0; k0 < n; k0 += 8 * NT) {  // every load of a round issued before any store
+    float v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int k = k0 + u * NT + threadIdx.x;
+      v[u] = k < n ? sums[k] : 0.0f;
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int k = k0 + u * NT + threadIdx.x;
+      if (k < o) ss[k] = v[u];
+      else if (k < n) tail[k - o] = v[u];
+    }
+  }
+  __syncthreads();
   if (Bd > 0) {
     const float pscale = inv_t / (float)Bq;
     for (int i = wave; i < Bq; i += NWAVES) {
-      const float* srow = sums + (size_t)i * Bd;
+      const float* srow = ss + i * Bd;
       const bool h0 = lane < Bd, h1 = lane + 64 < Bd;
       const float x0 = h0 ? srow[lane] * inv_t : -INFINITY;
       const float x1 = h1 ? srow[lane + 64] * inv_t : -INFINITY;
@@ -174,15 +206,14 @@ __global__ __launch_bounds__(NT) void loss_final_kernel(const float* __restrict_
   }
   __syncthreads();
   if (threadIdx.x == 0) {
-    const int o = Bq * Bd;
     float ce = 0.0f, l1q = 0.0f, l1d = 0.0f;
     for (int i = 0; i < (Bd > 0 ? Bq : 0); ++i) ce += row_loss[i];
-    for (int i = 0; i < Bq; ++i) l1q += sums[o + i];
-    for (int j = 0; j < Bd; ++j) l1d += sums[o + Bq + j];
+    for (int i = 0; i < Bq; ++i) l1q += tail[i];
+    for (int j = 0; j < Bd; ++j) l1d += tail[Bq + j];
     ce = Bd > 0 ? ce / (float)Bq : 0.0f;
     l1q /= (float)Bq;
     l1d = Bd > 0 ? l1d / (float)Bd : 0.0f;
-    const float flq = sums[o + Bq + Bd] / (float)V, fld = sums[o + Bq + Bd + 1] / (float)V;
+    const float flq = tail[Bq + Bd] / (float)V, fld = tail[Bq + Bd + 1] / (float)V;
     out[0] = w_ce * ce + w_l1 * (l1q + l1d) + w_fl * (flq + fld);
     out[1] = ce;
     out[2] = l1q;
@@ -208,10 +239,21 @@ __global__ __launch_bounds__(NT) void loss_bwd_kernel(const T* __restrict__ Q, c
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int c0 = blockIdx.x * SLICE;
   const int Bqp = round4(Bq), Bdp = round4(Bd);
-  stage_slice<T>(Q, R, Bq, Bd, V, c0, sq, sd, [](bool, int, float) {});
-  for (int e = threadIdx.x; e < Bqp * Bdp; e += NT) {  // P, zero-padded to Bqp x Bdp
-    const int i = e / Bdp, j = e - i * Bdp;
-    sp[i * PLD + j] = (i < Bq && j < Bd) ? P[(size_t)i * Bd + j] : 0.0f;
+  // P, zero-padded to Bqp x Bdp: its loads are issued first, so that they are in flight
+  // together with the slice's
+  constexpr int PPT = MB * MB / NT;  // P entries per thread at most
+  float pr[PPT];
+#pragma unroll
+  for (int u = 0; u < PPT; ++u) {
+    const int e = u * NT + threadIdx.x;
+    const int i = Bdp > 0 ? e / Bdp : 0, j = e - i * Bdp;
+    pr[u] = (Bdp > 0 && e < Bqp * Bdp && i < Bq && j < Bd) ? P[(size_t)i * Bd + j] : 0.0f;
+  }
+  stage_slice<T, MB>(Q, R, Bq, Bd, V, c0, sq, sd, [](bool, int, float) {});
+#pragma unroll
+  for (int u = 0; u < PPT; ++u) {
+    const int e = u * NT + threadIdx.x;
+    if (Bdp > 0 && e < Bqp * Bdp) sp[(e / Bdp) * PLD + e % Bdp] = pr[u];
   }
   __syncthreads();
   if (wave < 2) {
@@ -287,8 +329,13 @@ static int64_t entries(int64_t Bq, int64_t Bd) { return Bq * Bd + Bq + Bd + 2; }
 template <typename T, int MB>
 static void launch_fwd(const void* q, const void* d, int Bq, int Bd, int V, float* part, int K,
                        hipStream_t st) {
-  hipLaunchKernelGGL((loss_partial_kernel<T, MB>), dim3((unsigned)slices(V)), dim3(NT), 0, st,
-                     (const T*)q, (const T*)d, Bq, Bd, V, part, K);
+  const dim3 grid((unsigned)slices(V));
+  if ((round4(Bq) / 4) * (round4(Bd) / 4) >= NT)
+    hipLaunchKernelGGL((loss_partial_kernel<T, MB, 4>), grid, dim3(NT), 0, st, (const T*)q,
+                       (const T*)d, Bq, Bd, V, part, K);
+  else
+    hipLaunchKernelGGL((loss_partial_kernel<T, MB, 2>), grid, dim3(NT), 0, st, (const T*)q,
+                       (const T*)d, Bq, Bd, V, part, K);
 }
 template <typename T, int MB>
 static void launch_bwd(const void* q, const void* d, const float* P, const float* g, int Bq, int Bd,
