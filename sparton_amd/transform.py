@@ -163,6 +163,16 @@ class _TransformFn(torch.autograd.Function):
         return dx, dw, dbd, dg, dbt, None
 
 
+def _is_erf_gelu(act) -> bool:
+    """torch's F.gelu / nn.GELU() without the tanh approximation, or transformers'
+    GELUActivation (hidden_act "gelu" or "gelu_python", both the erf form)."""
+    if act is F.gelu:
+        return True
+    if isinstance(act, nn.GELU):
+        return act.approximate == "none"
+    return type(act).__name__ == "GELUActivation"
+
+
 class SpartonMLMTransform(nn.Module):
     """Drop-in for the transform: shares the parameters of an existing dense (nn.Linear
     D x D) and LayerNorm, e.g. BERT's `cls.predictions.transform.dense` and `.LayerNorm` or
@@ -180,8 +190,14 @@ class SpartonMLMTransform(nn.Module):
 
     @classmethod
     def from_hf(cls, transform: nn.Module) -> "SpartonMLMTransform":
-        """From BERT's BertPredictionHeadTransform (dense, LayerNorm) or a module with
-        `dense` and `layer_norm` (the RoBERTa wrapper of training/model.py:25-34)."""
+        """From BERT's BertPredictionHeadTransform (dense, transform_act_fn, LayerNorm) or a
+        module with `dense` and `layer_norm` (the RoBERTa wrapper of training/model.py:25-34,
+        whose activation is transformers' erf gelu). The kernels compute the exact (erf) gelu,
+        so a BERT transform configured with another activation is refused."""
+        act = getattr(transform, "transform_act_fn", None)
+        if act is not None and not _is_erf_gelu(act):
+            raise ValueError(f"SpartonMLMTransform computes the exact (erf) gelu; this transform's "
+                             f"activation is {act!r}")
         ln = getattr(transform, "LayerNorm", None) or getattr(transform, "layer_norm")
         return cls(transform.dense, ln)
 

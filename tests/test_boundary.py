@@ -265,6 +265,16 @@ def test_transform_module_surface():
     assert sparton_amd.SpartonMLMTransform.from_hf(b).layer_norm is b.LayerNorm
     with pytest.raises(ValueError):
         sparton_amd.SpartonMLMTransform(torch.nn.Linear(64, 32), ln)
+    # BERT's own transform module: erf gelu accepted, other activations refused
+    from transformers import BertConfig
+    from transformers.models.bert.modeling_bert import BertPredictionHeadTransform
+    for act, ok in (("gelu", True), ("gelu_python", True), ("gelu_new", False), ("relu", False)):
+        t = BertPredictionHeadTransform(BertConfig(hidden_size=64, hidden_act=act))
+        if ok:
+            assert sparton_amd.SpartonMLMTransform.from_hf(t).dense is t.dense
+        else:
+            with pytest.raises(ValueError, match="erf"):
+                sparton_amd.SpartonMLMTransform.from_hf(t)
     with pytest.raises(RuntimeError, match="ROCm/HIP device tensors"):
         m(torch.randn(2, 3, 64))
 
