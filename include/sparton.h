@@ -167,6 +167,20 @@ int sparton_transform_bwd(const void* dy, const void* z, const float* dense_bias
                           int dtype, void* stream);
 
 /*
+ * Weight gradient of the transform's dense layer, dW = dz^T x, as a batched GEMM over C row
+ * chunks (the caller runs the GEMM): sparton_transform_dz_chunks writes dzt [C, D, M/C] with
+ * dzt[c][i][l] = dz[c (M/C) + l][i] (M % C == 0 and (M/C) % 64 == 0), the K-contiguous left
+ * operands of part[c] = dzt[c] x[c (M/C) : (c+1) (M/C), :] (fp32 [C, D, D]); then
+ * sparton_transform_chunk_sum writes out[k] = sum_c part[c][k] in chunk order, in dtype
+ * (n % 4 == 0, 16-byte aligned). The reference gets dW from autograd of nn.Linear
+ * (training/model.py:14-40); these two calls and one batched GEMM replace that one GEMM.
+ */
+int sparton_transform_dz_chunks(const void* dz, void* dzt, int64_t M, int64_t D, int64_t C,
+                                int dtype, void* stream);
+int sparton_transform_chunk_sum(const float* part, void* out, int64_t C, int64_t n, int dtype,
+                                void* stream);
+
+/*
  * The SPLADE training loss on the head's reps (reference training/train.py:73-88, combined in
  * compute_loss at :164-197). q [Bq,V] are query reps, d [Bd,V] document reps (row-major, the
  * reps dtype; d may be NULL with Bd = 0). With S = q d^T / temperature:

@@ -15,7 +15,7 @@ import torch  # noqa: F401  (must be imported first: see module docstring)
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 DEFAULT_LIB = os.path.join(_HERE, "libsparton_hip.so")
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 # enum sparton_dtype / sparton_mask_dtype (include/sparton.h)
 DTYPE_CODE = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
@@ -38,6 +38,8 @@ EXPORTED_SYMBOLS = (
     "sparton_transform_fwd",
     "sparton_transform_bwd",
     "sparton_transform_workspace_bytes",
+    "sparton_transform_dz_chunks",
+    "sparton_transform_chunk_sum",
     "sparton_loss_fwd",
     "sparton_loss_bwd",
     "sparton_loss_workspace_bytes",
@@ -94,6 +96,10 @@ def load() -> ctypes.CDLL:
         L.sparton_transform_bwd.argtypes = [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                                             _vp, ctypes.c_size_t, _i64, _i64, ctypes.c_int, _vp]
         L.sparton_transform_bwd.restype = ctypes.c_int
+        L.sparton_transform_dz_chunks.argtypes = [_vp, _vp, _i64, _i64, _i64, ctypes.c_int, _vp]
+        L.sparton_transform_dz_chunks.restype = ctypes.c_int
+        L.sparton_transform_chunk_sum.argtypes = [_vp, _vp, _i64, _i64, ctypes.c_int, _vp]
+        L.sparton_transform_chunk_sum.restype = ctypes.c_int
         L.sparton_loss_workspace_bytes.argtypes = [_i64, _i64, _i64]
         L.sparton_loss_workspace_bytes.restype = ctypes.c_size_t
         L.sparton_loss_fwd.argtypes = [_vp, _vp, _i64, _i64, _i64, ctypes.c_float, ctypes.c_float,

@@ -4,7 +4,7 @@
 #define SPARTON_EXPORT extern "C" __attribute__((visibility("default")))
 
 namespace {
-constexpr int kAbiVersion = 5;
+constexpr int kAbiVersion = 6;
 constexpr int64_t kMaxBwdSeq = 16384;   // must match bwd::MAX_S in sparton_bwd.hip
 constexpr int64_t kMaxBwdBatch = 8192;  // must match bwd::MAX_B in sparton_bwd.hip
 }  // namespace

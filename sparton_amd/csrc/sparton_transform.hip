@@ -336,6 +336,52 @@ __global__ __launch_bounds__(64 * COL_WAVES) void xf_colsum_kernel(const float* 
   }
 }
 
+// ---- weight gradient support: dW = dZ^T X as a batched GEMM over C row chunks -----------
+// A plain dZ^T X GEMM has K = M (thousands of rows) and a D x D output of only a few dozen
+// tiles, so a library GEMM leaves most CUs idle. Split into C chunks of L = M / C rows,
+// dW = sum_c dZ_c^T X_c is a batched GEMM whose left operands dZ_c^T are K-contiguous
+// [D, L] matrices (X_c are views of X, no copy). These two kernels write those operands
+// and sum the C fp32 products in chunk order.
+
+// dzt[c][i][l] = dz[c L + l][i] for a 64 x 64 (row x column) tile of dz per workgroup,
+// staged in LDS; L % 64 == 0, so a tile never straddles two chunks.
+constexpr int TR_TILE = 64;
+template <typename T>
+__global__ __launch_bounds__(256) void xf_chunk_transpose_kernel(const T* __restrict__ dz,
+                                                                 T* __restrict__ dzt, int M,
+                                                                 int D, int L) {
+  __shared__ T tile[TR_TILE][TR_TILE + 2];
+  const int m0 = blockIdx.x * TR_TILE, i0 = blockIdx.y * TR_TILE;
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+#pragma unroll
+  for (int r = ty; r < TR_TILE; r += 4) {  // coalesced rows of dz
+    const int m = m0 + r, i = i0 + tx;
+    tile[r][tx] = (m < M && i < D) ? dz[(size_t)m * D + i] : T(0.0f);
+  }
+  __syncthreads();
+  const int c = m0 / L, l0 = m0 - c * L;
+#pragma unroll
+  for (int r = ty; r < TR_TILE; r += 4) {  // coalesced rows of dzt
+    const int i = i0 + r, m = m0 + tx;
+    if (i < D && m < M) dzt[((size_t)c * D + i) * L + l0 + tx] = tile[tx][r];
+  }
+}
+
+// out[k] = sum_c part[c][k] in chunk order, cast to T; four entries per thread.
+template <typename T>
+__global__ __launch_bounds__(256) void xf_chunk_sum_kernel(const float* __restrict__ part,
+                                                           T* __restrict__ out, int C,
+                                                           int64_t n) {
+  const int64_t k = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+  if (k >= n) return;
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  for (int c = 0; c < C; ++c) acc += *(const f32x4*)(part + (size_t)c * n + k);
+  vec4_t<T> o;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) o[e] = from_f32<T>(acc[e]);
+  *(vec4_t<T>*)(out + k) = o;
+}
+
 static int passes(int64_t D) { return (int)cdiv(D, 256); }
 static int bwd_waves(int64_t D) { return D <= 4 * 256 ? BWD_WAVES_NARROW : BWD_WAVES_WIDE; }
 static int rows_per_wave(int64_t M, int64_t D) {
@@ -474,4 +520,54 @@ extern "C" __attribute__((visibility("default"))) int sparton_transform_bwd(
       return xf::bwd<float>(dy, z, dense_bias, ln_weight, mean, rstd, dz, part, d_ln_weight,
                             d_ln_bias, d_dense_bias, M, D, st);
   }
+}
+
+extern "C" __attribute__((visibility("default"))) int sparton_transform_dz_chunks(
+    const void* dz, void* dzt, int64_t M, int64_t D, int64_t C, int dtype, void* stream) {
+  if (dtype < SPARTON_F32 || dtype > SPARTON_F16 || M < 0 || D < 0 || C < 1) return SPARTON_EINVAL;
+  if (M == 0 || D == 0) return SPARTON_OK;
+  if (dz == nullptr || dzt == nullptr || M % C != 0 || (M / C) % xf::TR_TILE != 0) return SPARTON_EINVAL;
+  if (M > INT32_MAX || D > INT32_MAX) return SPARTON_EUNSUPPORTED;
+  const dim3 grid((unsigned)cdiv(M, (int64_t)xf::TR_TILE), (unsigned)cdiv(D, (int64_t)xf::TR_TILE));
+  hipStream_t st = (hipStream_t)stream;
+  const int L = (int)(M / C);
+  switch (dtype) {
+    case SPARTON_BF16:
+      hipLaunchKernelGGL(xf::xf_chunk_transpose_kernel<bf16>, grid, dim3(256), 0, st, (const bf16*)dz,
+                         (bf16*)dzt, (int)M, (int)D, L);
+      break;
+    case SPARTON_F16:
+      hipLaunchKernelGGL(xf::xf_chunk_transpose_kernel<f16>, grid, dim3(256), 0, st, (const f16*)dz,
+                         (f16*)dzt, (int)M, (int)D, L);
+      break;
+    default:
+      hipLaunchKernelGGL(xf::xf_chunk_transpose_kernel<float>, grid, dim3(256), 0, st, (const float*)dz,
+                         (float*)dzt, (int)M, (int)D, L);
+      break;
+  }
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? SPARTON_OK : (int)e;
+}
+
+extern "C" __attribute__((visibility("default"))) int sparton_transform_chunk_sum(
+    const float* part, void* out, int64_t C, int64_t n, int dtype, void* stream) {
+  if (dtype < SPARTON_F32 || dtype > SPARTON_F16 || C < 1 || n < 0) return SPARTON_EINVAL;
+  if (n == 0) return SPARTON_OK;
+  if (part == nullptr || out == nullptr || n % 4 != 0) return SPARTON_EINVAL;
+  if ((((uintptr_t)part) | ((uintptr_t)out)) % 16 != 0) return SPARTON_EALIGN;
+  const dim3 grid((unsigned)cdiv(n / 4, (int64_t)256));
+  hipStream_t st = (hipStream_t)stream;
+  switch (dtype) {
+    case SPARTON_BF16:
+      hipLaunchKernelGGL(xf::xf_chunk_sum_kernel<bf16>, grid, dim3(256), 0, st, part, (bf16*)out, (int)C, n);
+      break;
+    case SPARTON_F16:
+      hipLaunchKernelGGL(xf::xf_chunk_sum_kernel<f16>, grid, dim3(256), 0, st, part, (f16*)out, (int)C, n);
+      break;
+    default:
+      hipLaunchKernelGGL(xf::xf_chunk_sum_kernel<float>, grid, dim3(256), 0, st, part, (float*)out, (int)C, n);
+      break;
+  }
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? SPARTON_OK : (int)e;
 }

@@ -329,3 +329,16 @@ def test_loss_module_surface():
     with pytest.raises(RuntimeError, match="ROCm/HIP device tensors"):
         loss.splade_loss(torch.rand(2, 10), torch.rand(2, 10))
     assert callable(torch.ops.sparton.splade_loss_fwd) and callable(torch.ops.sparton.splade_loss_bwd)
+
+
+def test_transform_dw_chunk_argument_validation():
+    L = _lib.load()
+    chunks = lambda **kw: L.sparton_transform_dz_chunks(*{**dict(dz=P, dzt=P, M=8192, D=768, C=8, dtype=1, stream=None), **kw}.values())
+    csum = lambda **kw: L.sparton_transform_chunk_sum(*{**dict(part=P, out=P, C=8, n=768 * 768, dtype=1, stream=None), **kw}.values())
+    assert chunks(M=8000) == -1          # M % C != 0
+    assert chunks(M=8 * 96) == -1        # M / C not a multiple of 64
+    assert chunks(C=0) == -1 and chunks(dtype=5) == -1 and chunks(dz=None) == -1
+    assert chunks(M=0) == 0
+    assert csum(n=6) == -1 and csum(C=0) == -1 and csum(out=None) == -1
+    assert csum(part=P + 4) == -2
+    assert csum(n=0) == 0

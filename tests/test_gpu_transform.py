@@ -55,6 +55,8 @@ CASES = [
     ("fp16", (16411,), 256, 1e-5),     # 9 rows per wave, ragged
     ("bf16", (4133,), 1540, 1e-5),     # wide rows (4-wave backward), partial last pass
     ("fp32", (9, 64), 2048, 1e-12),    # wide rows, full passes
+    ("bf16", (64, 512), 768, 1e-12),   # M = 32768: dW as 16 row chunks
+    ("bf16", (16, 512), 1024, 1e-5),   # BERT-large width, dW as 8 row chunks
 ]
 
 
@@ -160,3 +162,32 @@ def test_transform_opcheck(device):
     x, w, b, g, bt, dy = (t.to(device) for t in case("fp32", (3, 5), 64, seed=2))
     torch.library.opcheck(torch.ops.sparton.mlm_transform_fwd, (x, w, b, g, bt, 1e-5),
                           test_utils=("test_schema", "test_faketensor", "test_autograd_registration"))
+
+
+def test_weight_grad_chunk_kernels(device):
+    """The chunked dW pieces on their own: the K-contiguous chunks of dz and the ordered
+    chunk sum, against torch; and dW itself against one fp32 GEMM."""
+    from sparton_amd import _lib
+    from sparton_amd.transform import _weight_grad, _wgrad_chunks
+    L = _lib.load()
+    stream = torch.cuda.current_stream().cuda_stream
+    for dt, M, D in (("bf16", 8192, 768), ("fp16", 4096, 1024), ("bf16", 32768, 256)):
+        C = _wgrad_chunks(M, D, DT[dt])
+        assert C in (4, 8, 16)
+        gen = torch.Generator(device=device).manual_seed(M + D)
+        dz = torch.randn(M, D, device=device, generator=gen).to(DT[dt])
+        x = torch.randn(M, D, device=device, generator=gen).to(DT[dt])
+        dzt = torch.empty(C, D, M // C, dtype=DT[dt], device=device)
+        assert L.sparton_transform_dz_chunks(dz.data_ptr(), dzt.data_ptr(), M, D, C, 1 if dt == "bf16" else 2, stream) == 0
+        assert torch.equal(dzt, dz.view(C, M // C, D).transpose(1, 2))
+        part = torch.randn(C, D * D, device=device, generator=gen)
+        out = torch.empty(D * D, dtype=torch.float32, device=device)
+        assert L.sparton_transform_chunk_sum(part.data_ptr(), out.data_ptr(), C, D * D, 0, stream) == 0
+        want = part[0].clone()
+        for c in range(1, C):
+            want += part[c]
+        assert torch.equal(out, want)  # same order, same fp32 additions
+        dw = _weight_grad(L, dz, x, M, D)
+        ref = dz.float().t() @ x.float()
+        close(dw, ref, 2 ** -8, f"dW {dt} M={M} D={D}")
+        assert torch.equal(_weight_grad(L, dz, x, M, D), dw)
