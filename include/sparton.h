@@ -169,8 +169,8 @@ int sparton_transform_bwd(const void* dy, const void* z, const float* dense_bias
 /*
  * Weight gradient of the transform's dense layer, dW = dz^T x, as a batched GEMM over C row
  * chunks (the caller runs the GEMM): sparton_transform_dz_chunks writes dzt [C, D, M/C] with
- * dzt[c][i][l] = dz[c (M/C) + l][i] (M % C == 0 and (M/C) % 64 == 0), the K-contiguous left
- * operands of part[c] = dzt[c] x[c (M/C) : (c+1) (M/C), :] (fp32 [C, D, D]); then
+ * dzt[c][i][l] = dz[c (M/C) + l][i] (bf16/fp16; M % C == 0, (M/C) % 64 == 0, D % 64 == 0,
+ * 16-byte aligned), the K-contiguous left operands of part[c] = dzt[c] x[c (M/C) : (c+1) (M/C), :] (fp32 [C, D, D]); then
  * sparton_transform_chunk_sum writes out[k] = sum_c part[c][k] in chunk order, in dtype
  * (n % 4 == 0, 16-byte aligned). The reference gets dW from autograd of nn.Linear
  * (training/model.py:14-40); these two calls and one batched GEMM replace that one GEMM.

@@ -343,27 +343,34 @@ __global__ __launch_bounds__(64 * COL_WAVES) void xf_colsum_kernel(const float* 
 // [D, L] matrices (X_c are views of X, no copy). These two kernels write those operands
 // and sum the C fp32 products in chunk order.
 
-// dzt[c][i][l] = dz[c L + l][i] for a 64 x 64 (row x column) tile of dz per workgroup,
-// staged in LDS; L % 64 == 0, so a tile never straddles two chunks.
+// dzt[c][i][l] = dz[c L + l][i] for 16-bit types, in registers: each wave takes a 64 x 64
+// (row x column) tile of dz and each lane an 8 x 8 block of it -- eight 16-byte row loads,
+// a transpose by 32 v_perm_b32 (output dword q of column j = the j-th halves of rows 2q and
+// 2q + 1), eight 16-byte column stores. A wave's loads cover 8 rows x 128 contiguous bytes
+// and its stores 8 columns x 128 contiguous bytes. L % 64 == 0 and D % 64 == 0, so a tile
+// never straddles two chunks or the row end.
 constexpr int TR_TILE = 64;
+constexpr int TR_WAVES = 4;  // tiles side by side along D per workgroup
 template <typename T>
-__global__ __launch_bounds__(256) void xf_chunk_transpose_kernel(const T* __restrict__ dz,
-                                                                 T* __restrict__ dzt, int M,
-                                                                 int D, int L) {
-  __shared__ T tile[TR_TILE][TR_TILE + 2];
-  const int m0 = blockIdx.x * TR_TILE, i0 = blockIdx.y * TR_TILE;
-  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+__global__ __launch_bounds__(64 * TR_WAVES) void xf_chunk_transpose_kernel(const T* __restrict__ dz,
+                                                                          T* __restrict__ dzt, int M,
+                                                                          int D, int L) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int m0 = blockIdx.x * TR_TILE, i0 = (blockIdx.y * TR_WAVES + wave) * TR_TILE;
+  if (i0 >= D) return;
+  const int rb = lane >> 3, cb = lane & 7;  // the lane's 8-row and 8-column block
+  u32x4 r[8];
 #pragma unroll
-  for (int r = ty; r < TR_TILE; r += 4) {  // coalesced rows of dz
-    const int m = m0 + r, i = i0 + tx;
-    tile[r][tx] = (m < M && i < D) ? dz[(size_t)m * D + i] : T(0.0f);
-  }
-  __syncthreads();
-  const int c = m0 / L, l0 = m0 - c * L;
+  for (int e = 0; e < 8; ++e)
+    r[e] = *(const u32x4*)(dz + (size_t)(m0 + 8 * rb + e) * D + i0 + 8 * cb);
+  const int c = m0 / L, l = m0 - c * L + 8 * rb;
 #pragma unroll
-  for (int r = ty; r < TR_TILE; r += 4) {  // coalesced rows of dzt
-    const int i = i0 + r, m = m0 + tx;
-    if (i < D && m < M) dzt[((size_t)c * D + i) * L + l0 + tx] = tile[tx][r];
+  for (int j = 0; j < 8; ++j) {
+    const uint32_t sel = (j & 1) ? 0x07060302u : 0x05040100u;
+    u32x4 o;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) o[q] = __builtin_amdgcn_perm(r[2 * q + 1][j >> 1], r[2 * q][j >> 1], sel);
+    *(u32x4*)(dzt + ((size_t)c * D + i0 + 8 * cb + j) * L + l) = o;
   }
 }
 
@@ -524,27 +531,22 @@ extern "C" __attribute__((visibility("default"))) int sparton_transform_bwd(
 
 extern "C" __attribute__((visibility("default"))) int sparton_transform_dz_chunks(
     const void* dz, void* dzt, int64_t M, int64_t D, int64_t C, int dtype, void* stream) {
-  if (dtype < SPARTON_F32 || dtype > SPARTON_F16 || M < 0 || D < 0 || C < 1) return SPARTON_EINVAL;
+  if ((dtype != SPARTON_BF16 && dtype != SPARTON_F16) || M < 0 || D < 0 || C < 1) return SPARTON_EINVAL;
   if (M == 0 || D == 0) return SPARTON_OK;
-  if (dz == nullptr || dzt == nullptr || M % C != 0 || (M / C) % xf::TR_TILE != 0) return SPARTON_EINVAL;
+  if (dz == nullptr || dzt == nullptr || M % C != 0 || (M / C) % xf::TR_TILE != 0 ||
+      D % xf::TR_TILE != 0)
+    return SPARTON_EINVAL;
+  if ((((uintptr_t)dz) | ((uintptr_t)dzt)) % 16 != 0) return SPARTON_EALIGN;
   if (M > INT32_MAX || D > INT32_MAX) return SPARTON_EUNSUPPORTED;
-  const dim3 grid((unsigned)cdiv(M, (int64_t)xf::TR_TILE), (unsigned)cdiv(D, (int64_t)xf::TR_TILE));
+  const dim3 grid((unsigned)(M / xf::TR_TILE), (unsigned)cdiv(D, (int64_t)xf::TR_TILE * xf::TR_WAVES));
   hipStream_t st = (hipStream_t)stream;
   const int L = (int)(M / C);
-  switch (dtype) {
-    case SPARTON_BF16:
-      hipLaunchKernelGGL(xf::xf_chunk_transpose_kernel<bf16>, grid, dim3(256), 0, st, (const bf16*)dz,
-                         (bf16*)dzt, (int)M, (int)D, L);
-      break;
-    case SPARTON_F16:
-      hipLaunchKernelGGL(xf::xf_chunk_transpose_kernel<f16>, grid, dim3(256), 0, st, (const f16*)dz,
-                         (f16*)dzt, (int)M, (int)D, L);
-      break;
-    default:
-      hipLaunchKernelGGL(xf::xf_chunk_transpose_kernel<float>, grid, dim3(256), 0, st, (const float*)dz,
-                         (float*)dzt, (int)M, (int)D, L);
-      break;
-  }
+  if (dtype == SPARTON_BF16)
+    hipLaunchKernelGGL(xf::xf_chunk_transpose_kernel<bf16>, grid, dim3(64 * xf::TR_WAVES), 0, st,
+                       (const bf16*)dz, (bf16*)dzt, (int)M, (int)D, L);
+  else
+    hipLaunchKernelGGL(xf::xf_chunk_transpose_kernel<f16>, grid, dim3(64 * xf::TR_WAVES), 0, st,
+                       (const f16*)dz, (f16*)dzt, (int)M, (int)D, L);
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? SPARTON_OK : (int)e;
 }

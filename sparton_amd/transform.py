@@ -118,7 +118,7 @@ def _wgrad_chunks(M: int, D: int, dtype: torch.dtype) -> int:
     D = 768 bf16, dz^T x as one hipBLASLt GEMM takes 28 / 50 / 187 us at M = 4096 / 8192 /
     32768 (a D x D output is too few tiles for K = M); C = 4 / 8 / 16 chunks take 15 / 20 / 57
     us for the batched GEMM."""
-    if dtype not in (torch.bfloat16, torch.float16) or M < 2048 or D % 4:
+    if dtype not in (torch.bfloat16, torch.float16) or M < 2048 or D % 64:
         return 0
     C = 4 if M <= 4096 else (8 if M <= 16384 else 16)
     return C if M % (C * 64) == 0 else 0

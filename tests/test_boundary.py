@@ -338,6 +338,9 @@ def test_transform_dw_chunk_argument_validation():
     assert chunks(M=8000) == -1          # M % C != 0
     assert chunks(M=8 * 96) == -1        # M / C not a multiple of 64
     assert chunks(C=0) == -1 and chunks(dtype=5) == -1 and chunks(dz=None) == -1
+    assert chunks(dtype=0) == -1         # 16-bit types only
+    assert chunks(D=740) == -1           # D % 64 != 0
+    assert chunks(dz=P + 8) == -2
     assert chunks(M=0) == 0
     assert csum(n=6) == -1 and csum(C=0) == -1 and csum(out=None) == -1
     assert csum(part=P + 4) == -2
