@@ -138,11 +138,14 @@ def _setup_context(ctx, inputs, output):
     _out, probs = output
     ctx.has_d = d is not None
     ctx.w = (w_ce, w_l1, w_flops)
+    ctx.mark_non_differentiable(probs)  # kept for the backward only
     ctx.save_for_backward(q, d if d is not None else q.new_empty(0), probs)
 
 
 def _backward(ctx, g_out, _g_probs):
     q, d, probs = ctx.saved_tensors
+    if g_out is None:  # out did not reach the loss
+        return None, None, None, None, None, None
     dq, dd = torch.ops.sparton.splade_loss_bwd(g_out, q, d if ctx.has_d else None, probs, *ctx.w)
     return dq, (dd if ctx.has_d else None), None, None, None, None
 

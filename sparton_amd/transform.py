@@ -11,7 +11,8 @@ and the LayerNorm and gelu backward with deterministic column sums for the Layer
 dense-bias gradients (sparton_transform_bwd). Device tensors only, like the head.
 
     sparton::mlm_transform_fwd(x, weight, dense_bias, ln_weight, ln_bias, eps)
-        -> (y, z, mean, rstd)        y in x's dtype; z = x W^T is kept for the backward
+        -> (y, z, mean, rstd)        y in x's dtype; z = x W^T, mean and 1/std are kept for
+                                     the backward and are not differentiable
     sparton::mlm_transform_bwd(dy, x, weight, z, dense_bias, ln_weight, mean, rstd)
         -> (dx, d_weight, d_dense_bias, d_ln_weight, d_ln_bias)
 """
@@ -164,11 +165,14 @@ def _(dy, x, weight, z, dense_bias, ln_weight, mean, rstd):
 def _setup_context(ctx, inputs, output):
     x, weight, dense_bias, ln_weight, ln_bias, eps = inputs
     _y, z, mean, rstd = output
+    ctx.mark_non_differentiable(z, mean, rstd)  # kept for the backward only
     ctx.save_for_backward(x, weight, z, dense_bias, ln_weight, mean, rstd)
 
 
 def _backward(ctx, dy, _dz, _dmean, _drstd):
     x, weight, z, dense_bias, ln_weight, mean, rstd = ctx.saved_tensors
+    if dy is None:  # y did not reach the loss
+        return None, None, None, None, None, None
     dx, dw, dbd, dg, dbt = torch.ops.sparton.mlm_transform_bwd(dy, x, weight, z, dense_bias,
                                                               ln_weight, mean, rstd)
     return dx, dw, dbd, dg, dbt, None

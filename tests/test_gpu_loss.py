@@ -157,3 +157,10 @@ def test_loss_opcheck_and_compile(device):
 
     cf = torch.compile(f, backend="aot_eager", fullgraph=True)
     torch.testing.assert_close(cf(q, d), f(q, d))
+
+
+def test_loss_probs_not_differentiable(device):
+    q = reps_like(4, 100, "fp32", seed=9).to(device).requires_grad_()
+    d = reps_like(4, 100, "fp32", seed=10).to(device).requires_grad_()
+    out, probs = torch.ops.sparton.splade_loss_fwd(q, d, 1.0, 1.0, 0.0, 0.0)
+    assert out.requires_grad and not probs.requires_grad

@@ -191,3 +191,12 @@ def test_weight_grad_chunk_kernels(device):
         ref = dz.float().t() @ x.float()
         close(dw, ref, 2 ** -8, f"dW {dt} M={M} D={D}")
         assert torch.equal(_weight_grad(L, dz, x, M, D), dw)
+
+
+def test_transform_auxiliary_outputs_not_differentiable(device):
+    """z, mean and 1/std exist for the backward: autograd does not track them, and a loss
+    that uses only y gives the same gradients whatever else is read."""
+    x, w, b, g, bt, dy = (t.to(device) for t in case("fp32", (6,), 64, seed=4))
+    x.requires_grad_()
+    y, z, mean, rstd = torch.ops.sparton.mlm_transform_fwd(x, w, b, g, bt, 1e-5)
+    assert y.requires_grad and not (z.requires_grad or mean.requires_grad or rstd.requires_grad)
