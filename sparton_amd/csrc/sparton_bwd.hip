@@ -371,6 +371,76 @@ __global__ __launch_bounds__(256) void bwd_dh_kernel(
   }
 }
 
+// Few rows (B*S small, e.g. 2 x 32 with every v active): one workgroup of RW waves per
+// row instead of one wave. Wave w sums entries [w c, (w + 1) c) of the row's segment
+// (c = ceil(cnt / RW)) in v order, as bwd_dh_kernel does, and wave 0 adds the RW partial
+// rows in wave order through LDS: deterministic, and RW times the gathers in flight.
+template <int NP> struct SplitLds { static constexpr int floats = NP * 256; };
+// RW clamped to the LDS budget (RW * NP KB <= 64 KB), as dh_row_waves chooses it.
+template <int NP, int RW> struct SplitRW {
+  static constexpr int value = RW * NP <= 64 ? RW : SplitRW<NP, RW / 2>::value;
+};
+template <int NP> struct SplitRW<NP, 1> { static constexpr int value = 1; };
+template <typename T, typename O, int NP, int RW>
+__global__ __launch_bounds__(64 * RW) void bwd_dh_split_kernel(
+    const T* __restrict__ W, const int2* __restrict__ list, const int* __restrict__ seg_start,
+    const int* __restrict__ seg_cnt, O* __restrict__ dH, int B, int S, int D, int V) {
+  constexpr int U = Batch<NP>::U;
+  __shared__ __attribute__((aligned(16))) float red[RW][SplitLds<NP>::floats];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int64_t row = blockIdx.x;  // grid = B * S exactly
+  const int64_t b = row / S;
+  const int start = __builtin_amdgcn_readfirstlane(seg_start[row]);
+  const int cnt = __builtin_amdgcn_readfirstlane(seg_cnt[row]);
+  const int per = (cnt + RW - 1) / RW;
+  const int e_beg = min(cnt, wave * per), e_end = min(cnt, e_beg + per);
+  const int2* seg = list + b * V + start;
+  for (int d0 = 0; d0 < D; d0 += NP * 256) {
+    f32x4 acc[NP];
+#pragma unroll
+    for (int p = 0; p < NP; ++p) acc[p] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int e0 = e_beg; e0 < e_end; e0 += 64) {
+      const int2 ent = e0 + lane < e_end ? seg[e0 + lane] : make_int2(0, 0);
+      const int n = min(64, e_end - e0);
+      for (int j = 0; j < n; j += U) {
+        Raw4<T> w[U][NP];
+        float g[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const int jj = min(j + u, n - 1);
+          const int v = __builtin_amdgcn_readlane(ent.x, jj);
+          g[u] = j + u < n ? __int_as_float(__builtin_amdgcn_readlane(ent.y, jj)) : 0.0f;
+#pragma unroll
+          for (int p = 0; p < NP; ++p) {
+            const int d = d0 + p * 256 + lane * 4;
+            if (d < D) w[u][p].load(W + (int64_t)v * D + d);
+            else w[u][p].zero();
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+#pragma unroll
+          for (int p = 0; p < NP; ++p) acc[p] += g[u] * w[u][p].f();
+      }
+    }
+#pragma unroll
+    for (int p = 0; p < NP; ++p) *(f32x4*)&red[wave][p * 256 + lane * 4] = acc[p];
+    __syncthreads();
+    if (wave == 0) {
+      O* out = dH + row * D;
+#pragma unroll
+      for (int p = 0; p < NP; ++p) {
+        f32x4 t = *(const f32x4*)&red[0][p * 256 + lane * 4];
+#pragma unroll
+        for (int w = 1; w < RW; ++w) t += *(const f32x4*)&red[w][p * 256 + lane * 4];
+        const int d = d0 + p * 256 + lane * 4;
+        if (d < D) store4(out + d, t);
+      }
+    }
+    __syncthreads();  // red is refilled by the next D chunk
+  }
+}
+
 // Entries (b_i, v) for N batch rows (b_i >= B or v >= V: inactive): g' (0 if inactive) and
 // s. Three raw loads per row, issued together; then the mask of the candidates, issued
 // together; then the coefficients. Inactive entries get s = 0.
@@ -482,6 +552,8 @@ constexpr int FUSE_V_BITS = 18;
 constexpr int FUSE_MAX_S = 1024;
 constexpr int FUSE_MAX_NVB = (1 << FUSE_V_BITS) / 64;  // 64-id blocks
 constexpr int FUSE_ROWS = 16;                          // rows per range (one workgroup)
+constexpr int FUSE_V_FAST = 1 << 16;    // above this the five-kernel path is faster
+constexpr int FUSE_MIN_RANGES = 64;     // below this too (too few workgroups)
 constexpr int FUSE_MAX_NR = FUSE_MAX_S / FUSE_ROWS;    // ranges (<= 64: one lane each)
 
 // A workgroup of 16 waves owns 64 consecutive vocab ids. It loads G, reps and I of all
@@ -798,6 +870,14 @@ static int passes_for(int64_t D) {
   return (int)std::min<int64_t>(MAX_NP, std::max<int64_t>(1, cdiv(D, 256)));
 }
 
+// Waves per dH row of the five-kernel path: enough to keep ~1024 waves gathering when
+// there are few rows (1 from 1024 rows up), at most 8 (512-thread workgroups: fp32 rows
+// keep their gather batch in registers), within 64 KB of LDS for the partial rows.
+static int dh_row_waves(int64_t rows, int np) {
+  int rw = 1;
+  while (rw < 8 && rows * rw < 1024 && 2 * rw * np <= 64) rw *= 2;
+  return rw;
+}
 // SPARTON_BWD_PATH=five forces the five-kernel path (tests compare the two paths).
 static bool fused_path_enabled() {
   const char* e = getenv("SPARTON_BWD_PATH");
@@ -809,9 +889,14 @@ static void launch_rows(const T* g, const RT* r, const int32_t* idx, const void*
                         int mdt, const T* H, const T* W, O* dH, O* dW, O* dbias, void* ws,
                         int64_t B, int64_t S, int64_t D, int64_t V, hipStream_t st) {
   constexpr int FNP = NP <= FuseMaxNp<T>::value ? NP : FuseMaxNp<T>::value;
+  // The fused path stages, per (b, 16-row range), a prefix over every 64-id block, and
+  // gives each dH row one wave: it needs many ranges and few blocks. Measured on MI355X:
+  // B = 32, S = 256, V = 30522: fused 61 us vs 65 us; B = 2, S = 32 (dense grads):
+  // 1133 us vs 331 us; V = 250002: 753 us vs 460 us.
   const bool fused = fused_path_enabled() && dH != nullptr && dW != nullptr && B * S > 0 &&
                      D > 0 && V > 0 &&
-                     B <= DW_STAGE_B && S <= FUSE_MAX_S && V <= (1 << FUSE_V_BITS) &&
+                     B <= DW_STAGE_B && S <= FUSE_MAX_S && V <= FUSE_V_FAST &&
+                     B * cdiv(S, FUSE_ROWS) >= FUSE_MIN_RANGES &&
                      D <= (int64_t)FNP * 256;
   if (fused) {
     const Layout L = layout(B, S, V);
@@ -849,9 +934,20 @@ static void launch_rows(const T* g, const RT* r, const int32_t* idx, const void*
       hipLaunchKernelGGL(bwd_scatter_kernel, cgrid, dim3(64 * wpb), (size_t)S * 4 * wpb, st, idx,
                          (int)S, (int)V, (int)L.nch, (const int*)hist, (const int2*)comp,
                          (const int*)ccount, list);
-    hipLaunchKernelGGL((bwd_dh_kernel<T, O, NP>), dim3((unsigned)cdiv(B * S, 4)), dim3(256), 0,
-                       st, W, (const int2*)list, (const int*)seg_start, (const int*)seg_cnt, dH,
-                       (int)B, (int)S, (int)D, (int)V);
+    const int rw = dh_row_waves(B * S, NP);
+#define DH_SPLIT(RW)                                                                            \
+  hipLaunchKernelGGL((bwd_dh_split_kernel<T, O, NP, SplitRW<NP, RW>::value>), dim3((unsigned)(B * S)), \
+                     dim3(64 * SplitRW<NP, RW>::value), 0,                                           \
+                     st, W, (const int2*)list, (const int*)seg_start, (const int*)seg_cnt, dH,   \
+                     (int)B, (int)S, (int)D, (int)V)
+    if (rw >= 8) DH_SPLIT(8);
+    else if (rw >= 4) DH_SPLIT(4);
+    else if (rw >= 2) DH_SPLIT(2);
+    else
+      hipLaunchKernelGGL((bwd_dh_kernel<T, O, NP>), dim3((unsigned)cdiv(B * S, 4)), dim3(256), 0,
+                         st, W, (const int2*)list, (const int*)seg_start, (const int*)seg_cnt, dH,
+                         (int)B, (int)S, (int)D, (int)V);
+#undef DH_SPLIT
   }
   if ((dW != nullptr || dbias != nullptr) && V > 0) {
     if (B <= DW_STAGE_B)

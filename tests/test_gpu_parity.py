@@ -208,12 +208,14 @@ def test_deterministic_repeat(device):
 @pytest.mark.parametrize("case", [
     ("bf16", 32, 256, 768, 30522, True, "int64"),   # the headline shape
     ("fp16", 8, 512, 768, 9000, True, "holes"),
-    ("fp32", 5, 70, 132, 900, False, "frac"),
+    ("fp32", 16, 70, 132, 900, False, "frac"),
     ("bf16", 37, 40, 256, 700, True, "int64"),      # many short rows
 ], ids=lambda c: "-".join(map(str, c)))
 def test_backward_paths_agree_bitwise(case, device, monkeypatch):
     """The fused backward (entries compacted by the dW kernel) and the five-kernel one
-    (count, scan, scatter) sum every gradient in the same order: bitwise equal."""
+    (count, scan, scatter) sum every gradient in the same order: bitwise equal. (Shapes
+    where the fused path is taken: >= 64 row ranges, and >= 1024 rows, so that the
+    five-kernel path also gives each dH row one wave.)"""
     say(f"backward paths, case {case}")
     H, W, b, m, G = make_case(*case)
     Hd, Wd, md, Gd = H.to(device), W.to(device), m.to(device), G.to(device)
@@ -487,3 +489,24 @@ def test_opcheck_and_compile(device):
     ye = f(He, m)
     ye.backward()
     assert torch.equal(y, ye) and torch.equal(Hc.grad, He.grad)
+
+
+@pytest.mark.parametrize("case", [
+    ("fp32", 2, 32, 768, 3000, True, "int64"),     # 64 rows: 8 waves per dH row
+    ("bf16", 3, 100, 256, 2000, True, "holes"),    # 300 rows: 4 waves per row
+    ("fp16", 1, 700, 64, 500, False, "frac"),      # 700 rows: 2 waves per row
+], ids=lambda c: "-".join(map(str, c)))
+def test_backward_few_rows_split(case, device):
+    """Few dH rows: the five-kernel path splits each row's entries over several waves and
+    adds their partial rows in wave order. Against the oracle, and bitwise repeatable."""
+    say(f"backward few rows, case {case}")
+    H, W, b, m, G = make_case(*case)
+    Hd, Wd, md, Gd = H.to(device), W.to(device), m.to(device), G.to(device)
+    bd = None if b is None else b.to(device)
+    _, idx, reps32 = torch.ops.sparton.fused_sparton_fwd_train(Hd, Wd, bd, md)
+    outs = [[t.clone() for t in torch.ops.sparton.fused_sparton_bwd(Gd, reps32, idx, Hd, Wd, bd, md)]
+            for _ in range(2)]
+    torch.cuda.synchronize()
+    for a, c in zip(*outs):
+        assert torch.equal(a, c)
+    check_bwd_isolated(H, W, b, m, G, reps32, idx, *outs[0])
