@@ -229,6 +229,74 @@ __global__ __launch_bounds__(SCAN_THREADS) void bwd_scan_kernel(int* __restrict_
   }
 }
 
+// S <= 512: one workgroup of SCAN_THREADS per batch row, as P = floor(SCAN_THREADS / Sr)
+// parts of Sr = round_up(S, 64) positions (the remaining threads idle); part p sums and rewrites chunks [p n / P, (p + 1) n / P)
+// of every position, so every thread works instead of S of them. Part 0 scans the
+// positions' totals; each part then starts its chunks at the position's segment start
+// plus the counts of the parts before it (integer sums: the same offsets as above).
+__global__ __launch_bounds__(SCAN_THREADS) void bwd_scan_parts_kernel(int* __restrict__ hist,
+                                                                      int* __restrict__ seg_start,
+                                                                      int* __restrict__ seg_cnt,
+                                                                      int S, int nch, int Sr) {
+  __shared__ int ptot[SCAN_THREADS];
+  __shared__ int base[SCAN_THREADS];
+  __shared__ int wsum[SCAN_THREADS / 64];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int P = SCAN_THREADS / Sr;            // Sr need not divide SCAN_THREADS:
+  const int part = tid / Sr, s = tid - part * Sr;
+  const bool in = s < S && part < P;          // threads past P * Sr take no chunks
+  const int c_beg = part < P ? (int)((int64_t)nch * part / P) : 0;
+  const int c_end = part < P ? (int)((int64_t)nch * (part + 1) / P) : 0;
+  const int64_t b = blockIdx.x;
+  int* hb = hist + b * nch * S;
+  int tot = 0;
+  for (int c0 = c_beg; c0 < c_end; c0 += SCAN_BATCH) {
+    int x[SCAN_BATCH];
+#pragma unroll
+    for (int i = 0; i < SCAN_BATCH; ++i)
+      x[i] = (in && c0 + i < c_end) ? hb[(int64_t)(c0 + i) * S + s] : 0;
+#pragma unroll
+    for (int i = 0; i < SCAN_BATCH; ++i) tot += x[i];
+  }
+  ptot[tid] = tot;
+  __syncthreads();
+  int t = 0, incl = 0;
+  if (part == 0) {  // waves 0 .. Sr/64 - 1: the positions' totals and their inclusive scan
+    for (int q = 0; q < P; ++q) t += ptot[q * Sr + s];
+    incl = t;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const int y = __shfl_up(incl, d);
+      if (lane >= d) incl += y;
+    }
+    if (lane == 63) wsum[wave] = incl;
+  }
+  __syncthreads();
+  if (part == 0) {
+    int run = incl - t;
+    for (int w = 0; w < wave; ++w) run += wsum[w];
+    if (in) {
+      seg_start[b * S + s] = run;
+      seg_cnt[b * S + s] = t;
+    }
+    base[s] = run;
+  }
+  __syncthreads();
+  int off = base[s];
+  for (int q = 0; q < part; ++q) off += ptot[q * Sr + s];
+  for (int c0 = c_beg; c0 < c_end; c0 += SCAN_BATCH) {
+    int x[SCAN_BATCH];
+#pragma unroll
+    for (int i = 0; i < SCAN_BATCH; ++i)
+      x[i] = (in && c0 + i < c_end) ? hb[(int64_t)(c0 + i) * S + s] : 0;
+#pragma unroll
+    for (int i = 0; i < SCAN_BATCH; ++i) {
+      if (in && c0 + i < c_end) hb[(int64_t)(c0 + i) * S + s] = off;
+      off += x[i];
+    }
+  }
+}
+
 // ---- 3. scatter ----------------------------------------------------------------
 // One wave per chunk: its compacted entries (in v order) are ranked among equal s and
 // written to their segments. Lanes with equal s are found with one ballot per bit of
@@ -927,9 +995,13 @@ static void launch_rows(const T* g, const RT* r, const int32_t* idx, const void*
     if (L.nch > 0)
       hipLaunchKernelGGL((bwd_count_kernel<T, RT>), cgrid, dim3(64 * wpb), cl, st, g, r, idx,
                          mask, mdt, (int)S, (int)V, (int)L.nch, hist, comp, ccount);
-    hipLaunchKernelGGL(bwd_scan_kernel, dim3((unsigned)B),
-                       dim3((unsigned)std::min<int64_t>(SCAN_THREADS, round_up(S, 64))), 0, st, hist,
-                       seg_start, seg_cnt, (int)S, (int)L.nch);
+    if (S <= SCAN_THREADS / 2)
+      hipLaunchKernelGGL(bwd_scan_parts_kernel, dim3((unsigned)B), dim3(SCAN_THREADS), 0, st, hist,
+                         seg_start, seg_cnt, (int)S, (int)L.nch, (int)round_up(S, 64));
+    else
+      hipLaunchKernelGGL(bwd_scan_kernel, dim3((unsigned)B),
+                         dim3((unsigned)std::min<int64_t>(SCAN_THREADS, round_up(S, 64))), 0, st, hist,
+                         seg_start, seg_cnt, (int)S, (int)L.nch);
     if (L.nch > 0)
       hipLaunchKernelGGL(bwd_scatter_kernel, cgrid, dim3(64 * wpb), (size_t)S * 4 * wpb, st, idx,
                          (int)S, (int)V, (int)L.nch, (const int*)hist, (const int2*)comp,
