@@ -230,9 +230,9 @@ def test_backward_paths_agree_bitwise(case, device, monkeypatch):
 
 
 def test_graph_capture_replays(device):
-    """Forward and backward captured into one graph (the backward forks its dW kernel onto a
-    second stream and joins it back) replay to the eager results, bitwise, with eager work
-    and synchronizations between the replays."""
+    """Forward and backward captured into one HIP graph (all of their kernels and workspace
+    allocations) replay to the eager results, bitwise, with eager work and synchronizations
+    between the replays."""
     say("graph capture of fwd + bwd, config 3, 3 replays")
     inp = make_inputs(WORKLOADS[3]).to(device)
     H, W, b, m, G = inp.hidden, inp.weight, inp.bias, inp.mask, inp.grad
