@@ -345,3 +345,17 @@ def test_transform_dw_chunk_argument_validation():
     assert csum(n=6) == -1 and csum(C=0) == -1 and csum(out=None) == -1
     assert csum(part=P + 4) == -2
     assert csum(n=0) == 0
+
+
+def test_transform_weight_grad_chunk_rule():
+    """dW = dz^T x runs as a batched GEMM over C row chunks only for 16-bit types, M >= 2048,
+    D % 64 == 0 and M % (64 C) == 0; C = 4 / 8 / 16 for M <= 4096 / <= 16384 / larger."""
+    from sparton_amd.transform import _wgrad_chunks
+    bf, f32 = torch.bfloat16, torch.float32
+    assert _wgrad_chunks(8192, 768, bf) == 8
+    assert _wgrad_chunks(4096, 768, torch.float16) == 4
+    assert _wgrad_chunks(32768, 1024, bf) == 16
+    assert _wgrad_chunks(8192, 768, f32) == 0          # fp32: one plain GEMM
+    assert _wgrad_chunks(1024, 768, bf) == 0           # few rows
+    assert _wgrad_chunks(8192, 740, bf) == 0           # D % 64 != 0
+    assert _wgrad_chunks(8192 + 64, 768, bf) == 0      # M % (64 * 8) != 0
