@@ -273,6 +273,49 @@ def transform_timing(torch, w, dev, reps_n):
             "epilogue_bwd": roof(bwd_bytes, bwd_epi_ms)}
 
 
+def autocast_timing(torch, w, inp, dev, reps_n):
+    """The head's training fwd+bwd as mixed-precision training runs it (training/train.py under
+    bf16/fp16 autocast): fp32 master W and bias, fp32 hidden states, compute in the workload's
+    dtype. SpartonHead's autocast path (fp32 gradients straight from the kernels) against the
+    plain one (cast the parameters, run the 16-bit training op, autograd casts the gradients
+    back to fp32), both through autograd on the same data."""
+    import torch.nn.functional as F
+    import sparton_amd
+    dt = w.dtype
+    if dt not in (torch.bfloat16, torch.float16):
+        return None
+    head = sparton_amd.SpartonHead(w.V, w.D, use_bias=inp.bias is not None).to(dev)
+    with torch.no_grad():
+        head.weight.copy_(inp.weight.float())
+        if inp.bias is not None:
+            head.bias.copy_(inp.bias.float())
+    h = inp.hidden.float().requires_grad_()
+    g = inp.grad  # the workload's upstream gradient, as in the timed steps
+    params = [p for p in head.parameters()]
+
+    def fused():
+        for t in [h] + params:
+            t.grad = None
+        with torch.autocast("cuda", dtype=dt):
+            out = head(h, inp.mask)
+        out.backward(g)
+
+    def plain():
+        for t in [h] + params:
+            t.grad = None
+        b = head.bias.to(dt) if head.bias is not None else None
+        out = torch.ops.sparton.fused_sparton_fwd_train(h.to(dt), head.weight.to(dt), b, inp.mask)[0]
+        out.backward(g)
+
+    fused_ms, _, _ = time_device(torch, fused, reps_n)
+    plain_ms, _, _ = time_device(torch, plain, reps_n)
+    return {"dtype": DTYPE_NAME[str(dt)], "params": "fp32", "hidden": "fp32",
+            "fwd_bwd_ms": round(fused_ms, 4), "cast_grads_fwd_bwd_ms": round(plain_ms, 4),
+            "speedup": round(plain_ms / fused_ms, 3),
+            "timing": "HIP events over back-to-back autograd fwd+bwd, queue pre-filled by a spin "
+                      "kernel so host dispatch is hidden"}
+
+
 def loss_timing(torch, w, dev, reps_n):
     """The SPLADE loss on this workload's reps shape (training/train.py:73-197): B query and
     B document reps [B, V] in the reps dtype, train.py's default weights. sparton_amd.loss
@@ -435,6 +478,7 @@ def main():
     main_ms = time_main_kernel(torch, Hd.contiguous(), Wd.contiguous(), bd, mask, args.kernel_reps)
     xf = transform_timing(torch, w, dev, args.kernel_reps)
     lossr = loss_timing(torch, w, dev, args.kernel_reps)
+    mixed = autocast_timing(torch, w, inp, dev, args.kernel_reps)
     if args.copy_probe_mib > 0:
         src = torch.empty(args.copy_probe_mib << 20, dtype=torch.uint8, device=dev)
         dst = torch.empty_like(src)
@@ -507,6 +551,7 @@ def main():
         "bsv_logits_gb_avoided": round(w.B * w.S * w.V * e / 1e9, 3),
         "transform": xf,
         "loss": lossr,
+        "autocast_fp32_params": mixed,
         "cpu_baseline": None,
     }
     if not args.no_cpu_baseline and int(os.environ.get("RANK", "0")) == 0:

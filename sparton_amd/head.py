@@ -16,6 +16,38 @@ from torch import nn
 from . import ops  # noqa: F401  (registers torch.ops.sparton.*)
 
 
+class _AutocastTrainFn(torch.autograd.Function):
+    """Training forward/backward under autocast with fp32 parameters (the usual
+    mixed-precision setup: fp32 master weights, bf16/fp16 compute).
+
+    The forward casts W, bias and H to the compute dtype and runs the training kernels on
+    them, as the plain path does. The backward writes dH, dW and dbias in fp32 straight from
+    the kernels' fp32 sums, so dW reaches the fp32 master without autograd's cast pass
+    (read a [V,D] 16-bit gradient, write it again as fp32) and without being rounded to
+    16 bits on the way."""
+
+    @staticmethod
+    def forward(ctx, hidden, weight, bias, mask, dt, pad):
+        h, w = hidden.to(dt), weight.to(dt)
+        b = bias.to(dt) if bias is not None else None
+        if pad:
+            h, w = F.pad(h, (0, pad)), F.pad(w, (0, pad))
+        reps, idx, reps32 = ops._fwd_impl(h, w, b, mask, True, True,
+                                          "sparton::fused_sparton_fwd_train")
+        ctx.save_for_backward(reps32, idx, h, w, b, mask)
+        ctx.hidden_dtype, ctx.D, ctx.has_bias = hidden.dtype, hidden.shape[-1], bias is not None
+        return reps
+
+    @staticmethod
+    def backward(ctx, grad_reps):
+        reps32, idx, h, w, b, mask = ctx.saved_tensors
+        d_h, d_w, d_b = ops._bwd_impl(grad_reps, reps32, idx, h, w, b, mask, torch.float32,
+                                      "sparton::fused_sparton_bwd")
+        if d_h.shape[-1] != ctx.D:  # drop the zero padding columns
+            d_h, d_w = d_h[..., :ctx.D], d_w[:, :ctx.D]
+        return (d_h.to(ctx.hidden_dtype), d_w, d_b if ctx.has_bias else None, None, None, None)
+
+
 class SpartonHead(nn.Module):
     def __init__(self, vocab_size, hidden_dim, use_bias=False):
         super().__init__()
@@ -55,6 +87,13 @@ class SpartonHead(nn.Module):
         # op does not see autocast, so apply the autocast dtype here explicitly.
         if dev in ("cuda", "cpu") and torch.is_autocast_enabled(dev):
             dt = torch.get_autocast_dtype(dev)
+            if (dt in (torch.bfloat16, torch.float16) and weight.dtype == torch.float32
+                    and (bias is None or bias.dtype == torch.float32)
+                    and torch.is_grad_enabled() and not torch.compiler.is_compiling()
+                    and (hidden.requires_grad or weight.requires_grad
+                         or (bias is not None and bias.requires_grad))):
+                pad = (-hidden.shape[-1]) % (128 // torch.finfo(dt).bits)  # 16-byte chunks
+                return _AutocastTrainFn.apply(hidden, weight, bias, attention_mask, dt, pad)
             hidden, weight = hidden.to(dt), weight.to(dt)
             bias = bias.to(dt) if bias is not None else None
         elif weight.dtype != hidden.dtype:

@@ -7,6 +7,7 @@ import os
 import numpy as np
 import pytest
 import torch
+import torch.nn.functional as F
 
 import oracle
 import sparton
@@ -465,6 +466,47 @@ def test_autocast_policy(device):
     ref = oracle.torch_head(H.cpu().bfloat16().double(), head.weight.detach().cpu().bfloat16().double(),
                             head.bias.detach().cpu().bfloat16().double(), m.cpu())
     torch.testing.assert_close(out.cpu().double(), ref, **FWD_TOL)
+
+
+@pytest.mark.parametrize("dt,D", [(torch.bfloat16, 60), (torch.float16, 64)])
+def test_autocast_fp32_master_gradients(dt, D, device):
+    """Autocast over fp32 parameters and fp32 hidden states (mixed-precision training):
+    the gradients come out in fp32, equal to the oracle's at the kernel's own argmax and
+    unrounded reps, and equal, once rounded to the compute dtype, to the plain path's
+    (cast the parameters, run the training op, let autograd cast the gradients back)."""
+    say(f"autocast {dt} fp32 masters D={D}")
+    B, S, V = 3, 70, 700
+    g = torch.Generator().manual_seed(D)
+    head = sparton.SpartonHead(V, D, use_bias=True).to(device)
+    H = torch.randn(B, S, D, generator=g).to(device).requires_grad_()
+    lens = torch.tensor([70, 33, 5])
+    m = (torch.arange(S)[None] < lens[:, None]).long().to(device)
+    G = torch.rand(B, V, generator=g).to(dt).to(device)
+    with torch.autocast("cuda", dtype=dt):
+        out = head(H, m)
+    assert out.dtype == dt
+    out.backward(G)
+    dH, dW, db = H.grad, head.weight.grad, head.bias.grad
+    assert dH.dtype == dW.dtype == db.dtype == torch.float32
+    # the oracle at the kernel's own argmax and fp32 reps, on the rounded inputs
+    pad = (-D) % 8
+    Hl = F.pad(H.detach().to(dt), (0, pad))
+    Wl = F.pad(head.weight.detach().to(dt), (0, pad))
+    bl = head.bias.detach().to(dt)
+    reps, idx, reps32 = torch.ops.sparton.fused_sparton_fwd_train(Hl, Wl, bl, m)
+    assert torch.equal(reps, out.detach())
+    rH, rW, rb = oracle.fused_bwd_ref(G.cpu(), reps32.cpu(), idx.cpu(), Hl.cpu(), Wl.cpu(), True, m.cpu())
+    torch.testing.assert_close(dH.cpu().to(F64), rH[..., :D], **BWD_TOL)
+    torch.testing.assert_close(dW.cpu().to(F64), rW[:, :D], **BWD_TOL)
+    torch.testing.assert_close(db.cpu().to(F64), rb, **BWD_TOL)
+    # the plain path: 16-bit gradients rounded once from the same fp32 sums
+    hp = H.detach().to(dt).requires_grad_()
+    wp = head.weight.detach().to(dt).requires_grad_()
+    bp = head.bias.detach().to(dt).requires_grad_()
+    rp, _, _ = torch.ops.sparton.fused_sparton_fwd_train(F.pad(hp, (0, pad)), F.pad(wp, (0, pad)), bp, m)
+    rp.backward(G)
+    assert torch.equal(dW.to(dt), wp.grad) and torch.equal(db.to(dt), bp.grad)
+    assert torch.equal(dH.to(dt), hp.grad)
 
 
 def test_opcheck_and_compile(device):
