@@ -468,14 +468,15 @@ def test_autocast_policy(device):
     torch.testing.assert_close(out.cpu().double(), ref, **FWD_TOL)
 
 
-@pytest.mark.parametrize("dt,D", [(torch.bfloat16, 60), (torch.float16, 64)])
-def test_autocast_fp32_master_gradients(dt, D, device):
+@pytest.mark.parametrize("dt,D,V", [(torch.bfloat16, 60, 700), (torch.float16, 64, 700),
+                                    (torch.bfloat16, 40, 70001)])  # V > 65536: five-kernel backward
+def test_autocast_fp32_master_gradients(dt, D, V, device):
     """Autocast over fp32 parameters and fp32 hidden states (mixed-precision training):
     the gradients come out in fp32, equal to the oracle's at the kernel's own argmax and
     unrounded reps, and equal, once rounded to the compute dtype, to the plain path's
     (cast the parameters, run the training op, let autograd cast the gradients back)."""
-    say(f"autocast {dt} fp32 masters D={D}")
-    B, S, V = 3, 70, 700
+    say(f"autocast {dt} fp32 masters D={D} V={V}")
+    B, S = 3, 70
     g = torch.Generator().manual_seed(D)
     head = sparton.SpartonHead(V, D, use_bias=True).to(device)
     H = torch.randn(B, S, D, generator=g).to(device).requires_grad_()
