@@ -227,3 +227,30 @@ def test_training_step_matches_torch_head(kind, device):
             worst = max(worst, (p.grad - r).abs().max().item() / max(r.abs().max().item(), floor))
     say(f"  loss {res.total.item():.6f} (torch {lr.item():.6f}), worst grad rel err {worst:.2e}")
     assert worst <= 1e-3
+
+
+@pytest.mark.gpu
+def test_projection_compiles_fullgraph(device):
+    """torch.compile(fullgraph=True) over the Sparton projection (the transform's and the
+    head's custom ops, with their fakes and autograd): the same kernels as eager, so the
+    reps and every gradient are bitwise equal."""
+    llm = tiny_mlm("bert", seed=9).to(device)
+    backbone, transform, decoder = backbone_and_head(llm)
+    xf, head = sparton_projection(transform, decoder)
+    ids, mask = batch(2, 24, seed=10, device=device)
+    with torch.no_grad():
+        hidden = backbone(ids, mask).last_hidden_state
+
+    def proj(h, m):
+        return head(xf(h), m)
+
+    compiled = torch.compile(proj, backend="aot_eager", fullgraph=True)
+    G = torch.rand(2, VOCAB, generator=torch.Generator().manual_seed(11)).to(device)
+    params = [transform.dense.weight, transform.dense.bias, decoder.weight, decoder.bias]
+    outs = []
+    for fn in (proj, compiled):
+        h = hidden.clone().requires_grad_()
+        r = fn(h, mask)
+        outs.append([r.detach()] + list(torch.autograd.grad(r, [h] + params, G)))
+    for a, b in zip(*outs):
+        assert torch.equal(a, b)
