@@ -161,9 +161,16 @@ def _bwd_impl(grad_out, max_scores, max_idx, hidden, embed, bias, mask, grad_dty
     if tuple(max_scores.shape) != (B, V) or max_scores.dtype not in (hidden.dtype, torch.float32):
         raise ValueError(f"{op}: max_scores must be [{B},{V}] {hidden.dtype} or float32, "
                          f"got {tuple(max_scores.shape)} {max_scores.dtype}")
-    if tuple(max_idx.shape) != (B, V) or max_idx.dtype != torch.int32:
-        raise ValueError(f"{op}: max_idx must be [{B},{V}] int32, got "
+    if tuple(max_idx.shape) != (B, V) or max_idx.dtype not in (torch.int32, torch.int64):
+        raise ValueError(f"{op}: max_idx must be [{B},{V}] int32 (or int64), got "
                          f"{tuple(max_idx.shape)} {max_idx.dtype}")
+    if max_idx.dtype == torch.int64:
+        # The reference's ops exchange int64 indices (sparton_kernel.py:658-667); accept them,
+        # range-checked (this reads the tensor on the host) and narrowed to the int32 the
+        # kernels take.
+        if max_idx.numel() and (int(max_idx.min()) < 0 or int(max_idx.max()) >= max(S, 1)):
+            raise ValueError(f"{op}: max_idx values must lie in [0, {S})")
+        max_idx = max_idx.to(torch.int32)
     if tuple(grad_out.shape) != (B, V):
         raise ValueError(f"{op}: grad_out must be [{B},{V}], got {tuple(grad_out.shape)}")
     grad_out = _dense(grad_out.to(hidden.dtype))

@@ -519,6 +519,10 @@ def test_opcheck_and_compile(device):
     m = torch.ones(B, S, dtype=torch.long, device=device)
     torch.library.opcheck(torch.ops.sparton.fused_sparton_fwd.default, (H, W, b, m),
                           test_utils=("test_schema", "test_faketensor"))
+    # with inputs that require grad, the autograd registration is checked as well
+    Hg, Wg, bg = (t.clone().requires_grad_() for t in (H, W, b))
+    for op in (torch.ops.sparton.fused_sparton_fwd.default, torch.ops.sparton.fused_sparton_fwd_train.default):
+        torch.library.opcheck(op, (Hg, Wg, bg, m), test_utils=("test_autograd_registration",))
     head = sparton.SpartonHead(V, D, use_bias=True).to(device).bfloat16()
 
     def f(h, mm):
@@ -553,3 +557,85 @@ def test_backward_few_rows_split(case, device):
     for a, c in zip(*outs):
         assert torch.equal(a, c)
     check_bwd_isolated(H, W, b, m, G, reps32, idx, *outs[0])
+
+
+@pytest.mark.parametrize("cfg,use_bias", [(2, True), (3, False)])
+def test_reference_op_autograd(cfg, use_bias, device):
+    """Backprop through torch.ops.sparton.fused_sparton_fwd, the route the reference's
+    SpartonHead.forward takes (sparton_kernel.py:744 and register_autograd at :707): its
+    backward calls sparton::fused_sparton_bwd with the op's rounded scores (:701-705), which
+    returns fp32 gradients (:676-678); autograd casts them to each input's dtype. Checked
+    bitwise against that fp32 op's output cast once, and against the oracle's closed form at
+    the op's own reps and argmax."""
+    w = WORKLOADS[cfg]
+    say(f"reference-op autograd, config {cfg} {w.name} bias={use_bias}")
+    inp = make_inputs(w)
+    H, W, m, G = inp.hidden, inp.weight, inp.mask, inp.grad
+    b = inp.bias if use_bias else None
+    Hd, Wd = H.to(device).requires_grad_(), W.to(device).requires_grad_()
+    bd = b.to(device).requires_grad_() if b is not None else None
+    md, Gd = m.to(device), G.to(device)
+    reps, idx = torch.ops.sparton.fused_sparton_fwd(Hd, Wd, bd, md)
+    assert idx.dtype == torch.int32 and not idx.requires_grad and reps.dtype == w.dtype
+    reps.backward(Gd)
+    torch.cuda.synchronize()
+    assert Hd.grad.dtype == Wd.grad.dtype == w.dtype
+    if b is not None:
+        assert bd.grad.dtype == w.dtype
+    # the registered backward is the fp32 reference op at the rounded reps, cast once
+    dH32, dW32, db32 = torch.ops.sparton.fused_sparton_bwd(Gd, reps.detach(), idx, Hd.detach(),
+                                                           Wd.detach(), None if bd is None else bd.detach(), md)
+    assert dH32.dtype == dW32.dtype == torch.float32
+    assert torch.equal(Hd.grad, dH32.to(w.dtype)) and torch.equal(Wd.grad, dW32.to(w.dtype))
+    if b is not None:
+        assert torch.equal(bd.grad, db32.to(w.dtype))
+    else:
+        assert db32.numel() == 0
+    # the fp32 gradients against the oracle at the op's own reps and argmax
+    reps_c, idx_c = reps.detach().cpu(), idx.cpu()
+    rH, _, rb = oracle.fused_bwd_ref(G, reps_c, idx_c, H, W, b is not None, m, with_dW=False)
+    torch.testing.assert_close(dH32.cpu().to(F64), rH, **BWD_TOL)
+    cols = sample_cols(w.V)
+    _, rW, _ = oracle.fused_bwd_ref(G[:, cols], reps_c[:, cols], idx_c[:, cols], H, W[cols],
+                                    b is not None, m)
+    torch.testing.assert_close(dW32[cols.to(device)].cpu().to(F64), rW, **BWD_TOL)
+    if b is not None:
+        torch.testing.assert_close(db32.cpu().to(F64), rb, **BWD_TOL)
+    say(f"  nnz={int((G != 0).sum())} ok")
+
+
+def test_reps_value_truncation_bound(device):
+    """The kernel's max keeps each logit with its 5 low mantissa bits cleared (the row index
+    takes them), so in fp32 reps = log1p(M') with M - M' <= 2^-18 M, always rounding down,
+    plus the fp32 accumulation error. Bounded here on an fp32 case, entry by entry:
+    |reps - log1p(M)| <= (2^-18 M + gamma_{D+2} * sum|h w + b| at the oracle's argmax) / (1 + M)
+    + 2^-23."""
+    say("fp32 reps value bound")
+    H, W, b, m, _ = make_case("fp32", 4, 200, 384, 3000, True, "int64", seed=3)
+    reps, idx, r32 = torch.ops.sparton.fused_sparton_fwd_train(H.to(device), W.to(device), b.to(device),
+                                                               m.to(device))
+    M, I, ref = oracle.fused_fwd_ref(H, W, b, m)
+    A = oracle.logit_at(H.abs(), W.abs(), b.abs(), m.abs(), I)
+    D = H.shape[-1]
+    bound = (2.0 ** -18 * M + (D + 2) * 2.0 ** -24 * A) / (1 + M) + 2.0 ** -23
+    err = (r32.cpu().to(F64) - ref).abs()
+    assert bool((err <= bound).all()), float((err - bound).max())
+    say(f"  max |reps - log1p(M)| = {float(err.max()):.3e}, mean bound {float(bound.mean()):.3e}")
+
+
+def test_bwd_accepts_reference_int64_index(device):
+    """sparton::fused_sparton_bwd also takes the int64 indices the reference's ops exchange
+    (sparton_kernel.py:658-667): same gradients as with int32; out-of-range values raise."""
+    say("bwd with int64 max_idx")
+    H, W, b, m, G = make_case("bf16", 3, 77, 64, 1000, True, "int64")
+    Hd, Wd, bd, md, Gd = (t.to(device) for t in (H, W, b, m, G))
+    reps, idx = torch.ops.sparton.fused_sparton_fwd(Hd, Wd, bd, md)
+    a = torch.ops.sparton.fused_sparton_bwd(Gd, reps, idx, Hd, Wd, bd, md)
+    c = torch.ops.sparton.fused_sparton_bwd(Gd, reps, idx.long(), Hd, Wd, bd, md)
+    torch.cuda.synchronize()
+    for x, y in zip(a, c):
+        assert torch.equal(x, y)
+    bad = idx.long().clone()
+    bad[0, 0] = H.shape[1]
+    with pytest.raises(ValueError, match="max_idx values"):
+        torch.ops.sparton.fused_sparton_bwd(Gd, reps, bad, Hd, Wd, bd, md)
