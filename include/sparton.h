@@ -23,7 +23,8 @@
  *   - D must be a multiple of 8 (16-bit dtypes) or 4 (fp32).
  *   - Return value: 0 on success, < 0 for an invalid argument (nothing is launched),
  *     > 0 is the hipError_t of a failed launch. sparton_strerror() names each code.
- *   - Calls are reentrant; the library has no mutable global state.
+ *   - Calls are reentrant. The only mutable global state is the per-device address of
+ *     the static scratch of sparton_fwd_noalloc, resolved once per device under a lock.
  */
 #ifndef SPARTON_H
 #define SPARTON_H
@@ -58,6 +59,7 @@ enum sparton_status {
   SPARTON_EALIGN = -2,       /* a base pointer is not 16-byte aligned */
   SPARTON_EUNSUPPORTED = -3, /* shape outside the supported range (see sparton_limits) */
   SPARTON_EWORKSPACE = -4,   /* workspace missing or smaller than sparton_{fwd,bwd}_workspace_bytes */
+  SPARTON_ESCRATCH = -5,     /* sparton_fwd_noalloc: sizes need more than its static scratch */
 };
 
 /*
@@ -87,6 +89,24 @@ int sparton_fwd(const void* hidden, const void* weight, const void* bias,
                 const void* mask, int mask_dtype, void* reps, int32_t* argmax,
                 float* reps_f32, int64_t B, int64_t S, int64_t D, int64_t V,
                 int dtype, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * sparton_fwd without a workspace argument, for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). No
+ * counterpart in the reference. The same kernels and results as sparton_fwd; the workspace
+ * is a static device array of sparton_fwd_noalloc_max_workspace() bytes (32 MiB), one per
+ * GPU, held until the process ends. Sizes whose sparton_fwd_workspace_bytes() exceeds it
+ * return SPARTON_ESCRATCH and launch nothing (at V = 30522 that allows about 68 row tiles of
+ * 256 packed positions, e.g. B = 64, S = 256). Calls that overlap on one GPU share that
+ * array and race: the caller serialises them. Allocates, frees and synchronises nothing.
+ */
+int sparton_fwd_noalloc(const void* hidden, const void* weight, const void* bias,
+                        const void* mask, int mask_dtype, void* reps, int32_t* argmax,
+                        float* reps_f32, int64_t B, int64_t S, int64_t D, int64_t V,
+                        int dtype, void* stream);
+
+/* Size in bytes of sparton_fwd_noalloc's static scratch. */
+size_t sparton_fwd_noalloc_max_workspace(void);
 
 /*
  * Profiling variant of sparton_fwd: the same work and results; *main_ms receives the

@@ -15,7 +15,7 @@ import torch  # noqa: F401  (must be imported first: see module docstring)
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 DEFAULT_LIB = os.path.join(_HERE, "libsparton_hip.so")
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 # enum sparton_dtype / sparton_mask_dtype (include/sparton.h)
 DTYPE_CODE = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
@@ -33,6 +33,8 @@ EXPORTED_SYMBOLS = (
     "sparton_fwd",
     "sparton_fwd_profile",
     "sparton_fwd_workspace_bytes",
+    "sparton_fwd_noalloc",
+    "sparton_fwd_noalloc_max_workspace",
     "sparton_bwd",
     "sparton_bwd_workspace_bytes",
     "sparton_transform_fwd",
@@ -80,6 +82,11 @@ def load() -> ctypes.CDLL:
                                           _i64, _i64, _i64, _i64, ctypes.c_int, _vp, ctypes.c_size_t,
                                           _vp, ctypes.POINTER(ctypes.c_float)]
         L.sparton_fwd_profile.restype = ctypes.c_int
+        L.sparton_fwd_noalloc.argtypes = [_vp, _vp, _vp, _vp, ctypes.c_int, _vp, _vp, _vp,
+                                          _i64, _i64, _i64, _i64, ctypes.c_int, _vp]
+        L.sparton_fwd_noalloc.restype = ctypes.c_int
+        L.sparton_fwd_noalloc_max_workspace.argtypes = []
+        L.sparton_fwd_noalloc_max_workspace.restype = ctypes.c_size_t
         L.sparton_fwd_workspace_bytes.argtypes = [_i64, _i64, _i64, _i64, ctypes.c_int]
         L.sparton_fwd_workspace_bytes.restype = ctypes.c_size_t
         L.sparton_bwd.argtypes = [_vp, _vp, ctypes.c_int, _vp, _vp, ctypes.c_int, _vp, _vp, _vp,

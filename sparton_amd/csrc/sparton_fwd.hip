@@ -48,6 +48,7 @@
 #include <stdlib.h>
 
 #include <algorithm>
+#include <mutex>
 
 #include "sparton_common.h"
 
@@ -1317,6 +1318,66 @@ extern "C" __attribute__((visibility("default"))) int sparton_fwd(
     int64_t D, int64_t V, int dtype, void* workspace, size_t workspace_bytes, void* stream) {
   return fwd_run(hidden, weight, bias, mask, mask_dtype, reps, argmax, reps_f32, B, S, D, V,
                  dtype, workspace, workspace_bytes, stream, nullptr);
+}
+
+// ---- no-allocation entry point ----------------------------------------------------
+//
+// sparton_fwd_noalloc runs the same kernels as sparton_fwd with the workspace taken from
+// `scratch`, a file-scope device array: one copy per GPU, created when the library's code
+// object is loaded there and held until the process ends. Its device address on the
+// current GPU comes from hipGetSymbolAddress, once per device (the array's name in host
+// code is only a stand-in for the symbol). Nothing in the workspace has to start at zero:
+// the plan kernels write every count, list entry and row-mask value they use, and the
+// fixup reads only partials the main kernel wrote in the same launch. Every call on one
+// GPU shares the array, so calls that overlap on that GPU (other streams, other threads)
+// race and must be serialised by the caller.
+constexpr size_t kNoAllocScratchBytes = (size_t)32 << 20;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices];  // device address of `scratch` per device, once resolved
+}  // namespace
+
+// Device address of `scratch` on the current device (resolved on its first call there).
+static int scratch_address(void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return (int)e;
+  if (dev < 0 || dev >= kMaxDevices) return SPARTON_EUNSUPPORTED;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return (int)e;
+    if (p == nullptr || (uintptr_t)p % 256 != 0) return SPARTON_EALIGN;
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return SPARTON_OK;
+}
+
+extern "C" __attribute__((visibility("default"))) size_t sparton_fwd_noalloc_max_workspace(void) {
+  return kNoAllocScratchBytes;
+}
+
+extern "C" __attribute__((visibility("default"))) int sparton_fwd_noalloc(
+    const void* hidden, const void* weight, const void* bias, const void* mask,
+    int mask_dtype, void* reps, int32_t* argmax, float* reps_f32, int64_t B, int64_t S,
+    int64_t D, int64_t V, int dtype, void* stream) {
+  if (B < 0 || S < 0 || D < 0 || V < 0) return SPARTON_EINVAL;
+  if (dtype < SPARTON_F32 || dtype > SPARTON_F16) return SPARTON_EINVAL;
+  if (mask_dtype < SPARTON_MASK_I64 || mask_dtype > SPARTON_MASK_F16) return SPARTON_EINVAL;
+  const size_t need = sparton_fwd_workspace_bytes(B, S, D, V, dtype);
+  if (need > kNoAllocScratchBytes) return SPARTON_ESCRATCH;
+  void* ws = nullptr;
+  if (need > 0) {
+    const int rc = scratch_address(&ws);
+    if (rc != SPARTON_OK) return rc;
+  }
+  return fwd_run(hidden, weight, bias, mask, mask_dtype, reps, argmax, reps_f32, B, S, D, V,
+                 dtype, ws, need > 0 ? kNoAllocScratchBytes : 0, stream, nullptr);
 }
 
 extern "C" __attribute__((visibility("default"))) int sparton_fwd_profile(

@@ -38,7 +38,7 @@ def test_host_side_entry_points():
     L = _lib.load()
     assert L.sparton_abi_version() == _lib.ABI_VERSION
     assert L.sparton_strerror(0) == b"success"
-    for code in (-1, -2, -3, -4, 7, -99):
+    for code in (-1, -2, -3, -4, -5, 7, -99):
         assert len(L.sparton_strerror(code)) > 0
     max_s, max_b = _lib.limits()
     assert max_s >= 4096 and max_b >= 1024
@@ -359,3 +359,25 @@ def test_transform_weight_grad_chunk_rule():
     assert _wgrad_chunks(1024, 768, bf) == 0           # few rows
     assert _wgrad_chunks(8192, 740, bf) == 0           # D % 64 != 0
     assert _wgrad_chunks(8192 + 64, 768, bf) == 0      # M % (64 * 8) != 0
+
+
+def test_fwd_noalloc_rejections_before_any_hip_call():
+    """sparton_fwd_noalloc validates its arguments and its scratch limit before touching
+    the device (fake, never-dereferenced pointers)."""
+    L = _lib.load()
+    cap = L.sparton_fwd_noalloc_max_workspace()
+    assert cap == 32 << 20
+
+    def call(**kw):
+        a = dict(hidden=P, weight=P, bias=None, mask=P, mask_dtype=0, reps=P, argmax=P, reps32=None,
+                 B=2, S=4, D=64, V=10, dtype=1, stream=None)
+        a.update(kw)
+        return L.sparton_fwd_noalloc(*a.values())
+
+    assert call(B=-1) == -1 and call(dtype=3) == -1 and call(mask_dtype=9) == -1
+    # config 4's sizes need a 128 MB workspace: refused with SPARTON_ESCRATCH
+    assert L.sparton_fwd_workspace_bytes(32, 256, 768, 250002, 1) > cap
+    assert call(B=32, S=256, D=768, V=250002) == -5
+    # config 2's fit
+    assert L.sparton_fwd_workspace_bytes(32, 256, 768, 30522, 1) <= cap
+    assert b"static scratch" in L.sparton_strerror(-5)
