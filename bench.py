@@ -102,7 +102,8 @@ def time_events(torch, fn, reps):
 def cpu_baseline(torch, w, inp, budget_s):
     """The reference torch head fwd+bwd on the host, on the first rows of the batch."""
     import oracle
-    threads = min(os.cpu_count() or 1, 16)
+    # every core this process may run on (its CPU affinity), recorded beside the host's count
+    threads = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
     torch.set_num_threads(threads)
     state = {}
 
@@ -137,6 +138,9 @@ def cpu_baseline(torch, w, inp, budget_s):
         "seconds": round(sum(times), 2),
         "unit": "tokens/s",
         "cores": torch.get_num_threads(),
+        "host_cpu_count": os.cpu_count(),
+        "affinity_cpus": threads,
+        "omp_num_threads_env": os.environ.get("OMP_NUM_THREADS"),
         "kind": "port",
         "sample": (f"torch head (training/model.py:56-62, restated in oracle/) fwd+bwd autograd, "
                    f"{DTYPE_NAME[str(w.dtype)]}, {rows} of {w.B} batch rows ({rows * w.S} tokens), "
@@ -170,6 +174,42 @@ def time_main_kernel(torch, H, W, b, mask, reps_n):
         if i >= 3:
             times.append(ms.value)
     return statistics.mean(times)
+
+
+def mfma_ceiling(torch, dtype_name, target_ms=1.0):
+    """The MFMA rate all CUs sustain together on random 16-bit register operands, and their
+    shader clock (sparton_mfma_probe): under a full MFMA load the GPU is power-limited, so
+    this, not the nominal peak, is what the forward's main kernel can approach on this box."""
+    import ctypes
+    from sparton_amd import _lib
+    if dtype_name not in ("bf16", "fp16"):
+        return None
+    L = _lib.load()
+    dt = _lib.DTYPE_CODE[torch.bfloat16 if dtype_name == "bf16" else torch.float16]
+    grid = torch.cuda.get_device_properties(0).multi_processor_count
+    out = torch.empty(grid * 256, dtype=torch.float32, device="cuda")
+    clk = torch.empty(grid * 2, dtype=torch.int64, device="cuda")
+    stream = torch.cuda.current_stream().cuda_stream
+    flop_per_iter = grid * 4 * 16 * 2 * 32 * 32 * 16
+
+    def run(iters):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        _lib.check(L.sparton_mfma_probe(dt, grid, iters, out.data_ptr(), clk.data_ptr(), stream),
+                   "sparton_mfma_probe")
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1)
+
+    run(200)
+    iters = max(200, int(200 * target_ms / max(run(200), 1e-3)))
+    ms = run(iters)
+    c = clk.view(grid, 2).double()
+    mhz = float((c[:, 0] / (c[:, 1] / 100.0)).mean())  # s_memrealtime ticks at 100 MHz
+    return {"tflops": round(flop_per_iter * iters / (ms * 1e-3) / 1e12, 1), "clock_mhz": round(mhz),
+            "ms": round(ms, 3), "workgroups": grid,
+            "what": "sparton_mfma_probe: 4 waves per CU, independent v_mfma_f32_32x32x16 on random "
+                    "register operands, all CUs at once (power-limited rate); HIP events"}
 
 
 def time_device(torch, fn, reps):
@@ -509,6 +549,12 @@ def main():
                  + w.B * w.S * w.D * e + w.V * w.D * e + (w.V * e if has_bias else 0))
     bwd_gbs = bwd_bytes / (bwd_ms * 1e-3) / 1e9
     traffic, traffic_src = measured_traffic(args.config, FWD_KERNEL % KNAME[dname])
+    ceiling = mfma_ceiling(torch, dname)
+    # whole-step roofline: the forward at the MFMA peak plus the backward's
+    # compulsory bytes at HBM peak, over the measured step; useful flops only
+    t_step = elapsed / args.steps
+    t_roof = useful_flops / (peak_tf * 1e12) + bwd_bytes / (PEAK_HBM_GBS * 1e9)
+    step_flops = useful_flops + 4.0 * nnz * w.D
 
     out = {
         "metric": METRIC,
@@ -536,7 +582,15 @@ def main():
                                "(sparton_fwd_profile), mean of --kernel-reps launches",
                      "op_ms": round(fwd_ms, 4), "op_timing": "HIP events around the forward of each step of an untimed pass after the timed one",
                      "op_tflops": round(useful_flops / (fwd_ms * 1e-3) / 1e12, 2),
-                     "op_ms_back_to_back": round(fwd_b2b, 4)},
+                     "op_ms_back_to_back": round(fwd_b2b, 4),
+                     "frac_of_mfma_ceiling": (round(fwd_tflops / ceiling["tflops"], 4)
+                                              if ceiling else None)},
+        "step_roofline": {"frac": round(t_roof / t_step, 4), "roofline_ms": round(t_roof * 1e3, 4),
+                          "step_ms": round(t_step * 1e3, 4),
+                          "basis": "(useful F_fwd / MFMA peak + compulsory bwd bytes / 8 TB/s) / measured step"},
+        "step_tflops": round(step_flops / t_step / 1e12, 2),
+        "step_tflops_basis": "(2*D*V*valid_tokens + 4*nnz*D) / measured step",
+        "mfma_ceiling": ceiling,
         "bwd_roofline": {"bound": "hbm", "achieved": round(bwd_gbs, 1), "peak": PEAK_HBM_GBS,
                          "unit": "GB/s", "frac": round(bwd_gbs / PEAK_HBM_GBS, 4),
                          "bytes_per_call": bwd_bytes, "nnz": nnz, "U_W": u_w, "U_H": u_h,

@@ -230,6 +230,17 @@ int sparton_loss_bwd(const void* q, const void* d, const float* probs, const flo
                      int64_t Bq, int64_t Bd, int64_t V, float w_ce, float w_l1, float w_flops,
                      void* grad_q, void* grad_d, int dtype, void* stream);
 
+/*
+ * Measurement probe, no counterpart in the reference: `grid` workgroups (one per CU) of 4
+ * waves each run `iters` rounds of 16 independent v_mfma_f32_32x32x16_{bf16,f16} on random
+ * register operands (dtype SPARTON_BF16 or SPARTON_F16). clk[2*w] receives workgroup w's
+ * shader-clock cycles and clk[2*w+1] its 100 MHz real-time ticks over the loop; out[256*w+t]
+ * a sink value. It measures the MFMA rate all CUs sustain together on data-like operands
+ * (the GPU is power-limited under such a load), the ceiling the forward's main kernel runs
+ * against. `out` and `clk` are device pointers.
+ */
+int sparton_mfma_probe(int dtype, int grid, int iters, float* out, long long* clk, void* stream);
+
 /* Static, thread-safe description of a status code. */
 const char* sparton_strerror(int code);
 

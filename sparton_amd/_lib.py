@@ -45,6 +45,7 @@ EXPORTED_SYMBOLS = (
     "sparton_loss_fwd",
     "sparton_loss_bwd",
     "sparton_loss_workspace_bytes",
+    "sparton_mfma_probe",
     "sparton_strerror",
     "sparton_limits",
     "sparton_abi_version",
@@ -116,6 +117,8 @@ def load() -> ctypes.CDLL:
         L.sparton_loss_bwd.argtypes = [_vp, _vp, _vp, _vp, _i64, _i64, _i64, ctypes.c_float,
                                        ctypes.c_float, ctypes.c_float, _vp, _vp, ctypes.c_int, _vp]
         L.sparton_loss_bwd.restype = ctypes.c_int
+        L.sparton_mfma_probe.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, _vp, _vp, _vp]
+        L.sparton_mfma_probe.restype = ctypes.c_int
         L.sparton_strerror.argtypes = [ctypes.c_int]
         L.sparton_strerror.restype = ctypes.c_char_p
         L.sparton_limits.argtypes = [ctypes.POINTER(_i64), ctypes.POINTER(_i64)]

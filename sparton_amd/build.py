@@ -17,7 +17,7 @@ CSRC = os.path.join(HERE, "csrc")
 LIB_NAME = "libsparton_hip.so"
 LIB_PATH = os.path.join(HERE, LIB_NAME)
 SOURCES = ["sparton_fwd.hip", "sparton_bwd.hip", "sparton_transform.hip", "sparton_loss.hip",
-           "sparton_capi.cpp"]
+           "sparton_probe.hip", "sparton_capi.cpp"]
 ARCH = os.environ.get("SPARTON_OFFLOAD_ARCH", "gfx950")
 
 # Packed-fp32 VALU ops are disabled on purpose: hipcc would otherwise emit

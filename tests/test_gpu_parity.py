@@ -559,6 +559,27 @@ def test_backward_few_rows_split(case, device):
     check_bwd_isolated(H, W, b, m, G, reps32, idx, *outs[0])
 
 
+
+@pytest.mark.parametrize("dt", [1, 2])
+def test_mfma_probe_reports_cycles(dt, device):
+    """sparton_mfma_probe (the measurement kernel bench.py reports as mfma_ceiling) runs on
+    every CU and reports positive cycle and real-time counts at a plausible shader clock."""
+    say(f"mfma probe, dtype code {dt}")
+    L = _lib.load()
+    grid = torch.cuda.get_device_properties(0).multi_processor_count
+    out = torch.empty(grid * 256, dtype=torch.float32, device=device)
+    clk = torch.zeros(grid * 2, dtype=torch.int64, device=device)
+    rc = L.sparton_mfma_probe(dt, grid, 50, out.data_ptr(), clk.data_ptr(),
+                              torch.cuda.current_stream().cuda_stream)
+    assert rc == 0
+    torch.cuda.synchronize()
+    c = clk.view(grid, 2).double().cpu()
+    assert bool((c > 0).all())
+    mhz = c[:, 0] / (c[:, 1] / 100.0)
+    assert bool(((mhz > 300) & (mhz < 3500)).all()), mhz
+    assert bool(torch.isfinite(out).all())
+    assert L.sparton_mfma_probe(0, grid, 50, out.data_ptr(), clk.data_ptr(), None) == -1
+
 @pytest.mark.parametrize("cfg,use_bias", [(2, True), (3, False)])
 def test_reference_op_autograd(cfg, use_bias, device):
     """Backprop through torch.ops.sparton.fused_sparton_fwd, the route the reference's
