@@ -27,11 +27,13 @@ class _AutocastTrainFn(torch.autograd.Function):
     16 bits on the way."""
 
     @staticmethod
-    def forward(ctx, hidden, weight, bias, mask, dt, pad):
-        h, w = hidden.to(dt), weight.to(dt)
-        b = bias.to(dt) if bias is not None else None
+    def forward(ctx, hidden, weight, bias, mask, dt, pad, cast):
+        # cast(t): the compute-dtype (zero-padded) copy of a parameter, reused while unchanged
+        w = cast(weight, dt, pad, "weight")
+        b = cast(bias, dt, 0, "bias") if bias is not None else None
+        h = hidden.to(dt)
         if pad:
-            h, w = F.pad(h, (0, pad)), F.pad(w, (0, pad))
+            h = F.pad(h, (0, pad))
         reps, idx, reps32 = ops._fwd_impl(h, w, b, mask, True, True,
                                           "sparton::fused_sparton_fwd_train")
         ctx.save_for_backward(reps32, idx, h, w, b, mask)
@@ -45,7 +47,37 @@ class _AutocastTrainFn(torch.autograd.Function):
                                       "sparton::fused_sparton_bwd")
         if d_h.shape[-1] != ctx.D:  # drop the zero padding columns
             d_h, d_w = d_h[..., :ctx.D], d_w[:, :ctx.D]
-        return (d_h.to(ctx.hidden_dtype), d_w, d_b if ctx.has_bias else None, None, None, None)
+        return (d_h.to(ctx.hidden_dtype), d_w, d_b if ctx.has_bias else None, None, None, None, None)
+
+
+class _CastCache:
+    """Compute-dtype copies of fp32 parameters for the autocast path, reused while the
+    parameter is unchanged, so the head's calls between two optimizer steps (train.py calls
+    it for queries and for documents, training/train.py:165-172) share one cast of W.
+
+    A copy is keyed on the parameter's storage address, its version counter, dtype and
+    padding: an in-place update (an optimizer step, load(), copy_) bumps the version counter,
+    re-binding (tie_weights) changes the address, and either makes the next call cast again.
+    Writes through `param.data` are not versioned by torch and are not seen: update
+    parameters in place under torch.no_grad() instead."""
+
+    def __init__(self):
+        self._entries = {}
+
+    def __call__(self, t, dt, pad, slot):
+        key = (t.data_ptr(), t._version, tuple(t.shape), dt, pad)
+        hit = self._entries.get(slot)
+        if hit is not None and hit[0] == key:
+            return hit[1]
+        with torch.no_grad():
+            v = t.detach().to(dt)
+            if pad:
+                v = F.pad(v, (0, pad))
+        self._entries[slot] = (key, v)
+        return v
+
+    def clear(self):
+        self._entries.clear()
 
 
 class SpartonHead(nn.Module):
@@ -57,6 +89,7 @@ class SpartonHead(nn.Module):
         else:
             self.register_parameter("bias", None)
         self.init_parameters()
+        self._cast_cache = _CastCache()
 
     def tie_weights(self, decoder):
         """Share the MLM decoder's parameters (sparton_kernel.py:721-723)."""
@@ -93,9 +126,16 @@ class SpartonHead(nn.Module):
                     and (hidden.requires_grad or weight.requires_grad
                          or (bias is not None and bias.requires_grad))):
                 pad = (-hidden.shape[-1]) % (128 // torch.finfo(dt).bits)  # 16-byte chunks
-                return _AutocastTrainFn.apply(hidden, weight, bias, attention_mask, dt, pad)
-            hidden, weight = hidden.to(dt), weight.to(dt)
-            bias = bias.to(dt) if bias is not None else None
+                return _AutocastTrainFn.apply(hidden, weight, bias, attention_mask, dt, pad,
+                                              self._cast_cache)
+            if (weight.dtype == torch.float32 and not torch.compiler.is_compiling()
+                    and not (torch.is_grad_enabled() and weight.requires_grad)):
+                weight = self._cast_cache(weight, dt, 0, "weight")  # inference: reuse the cast copy
+                bias = self._cast_cache(bias, dt, 0, "bias") if bias is not None else None
+            else:
+                weight = weight.to(dt)
+                bias = bias.to(dt) if bias is not None else None
+            hidden = hidden.to(dt)
         elif weight.dtype != hidden.dtype:
             weight = weight.to(hidden.dtype)
             bias = bias.to(hidden.dtype) if bias is not None else None

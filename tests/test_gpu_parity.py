@@ -660,3 +660,41 @@ def test_bwd_accepts_reference_int64_index(device):
     bad[0, 0] = H.shape[1]
     with pytest.raises(ValueError, match="max_idx values"):
         torch.ops.sparton.fused_sparton_bwd(Gd, reps, bad, Hd, Wd, bd, md)
+
+
+
+def test_autocast_weight_cast_is_cached_until_updated(device):
+    """Under autocast over fp32 parameters the head casts W once and reuses the copy while W
+    is unchanged (two calls per training step share it); an optimizer step, which updates W
+    in place, makes the next call cast again, so its reps follow the new weights."""
+    say("autocast cast cache and optimizer step")
+    B, S, D, V = 3, 40, 64, 900
+    g = torch.Generator().manual_seed(9)
+    head = sparton.SpartonHead(V, D, use_bias=True).to(device)
+    H = torch.randn(B, S, D, generator=g).to(device).requires_grad_()
+    m = torch.ones(B, S, dtype=torch.long, device=device)
+    opt = torch.optim.SGD(head.parameters(), lr=0.5)
+
+    def run():
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            return head(H, m)
+
+    r1 = run()
+    w1 = head._cast_cache._entries["weight"][1]
+    r2 = run()
+    assert head._cast_cache._entries["weight"][1] is w1   # reused, not cast again
+    assert torch.equal(r1, r2)
+    (r1.float().sum() + r2.float().sum()).backward()
+    opt.step()
+    opt.zero_grad(set_to_none=True)
+    r3 = run()
+    assert head._cast_cache._entries["weight"][1] is not w1
+    ref = oracle.torch_head(H.detach().cpu().bfloat16().double(),
+                            head.weight.detach().cpu().bfloat16().double(),
+                            head.bias.detach().cpu().bfloat16().double(), m.cpu())
+    torch.testing.assert_close(r3.detach().cpu().double(), ref, **FWD_TOL)
+    assert not torch.equal(r3, r1)
+    with torch.no_grad():   # inference under autocast uses the same copy
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            r4 = head(H, m)
+    assert torch.equal(r4, r3.detach())
