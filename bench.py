@@ -239,7 +239,7 @@ def transform_timing(torch, w, dev, reps_n):
     row statistics)."""
     import torch.nn.functional as F
     from sparton_amd import _lib
-    from sparton_amd.transform import _TransformFn
+    from sparton_amd import _eager
     L = _lib.load()
     M, D, dt = w.B * w.S, w.D, w.dtype
     if D % 4 or D > 3072:
@@ -256,7 +256,7 @@ def transform_timing(torch, w, dev, reps_n):
         x.grad = W.grad = None
         for v in vec:
             v.grad = None
-        _TransformFn.apply(x, W, vec[0], vec[1], vec[2], eps).backward(dy)
+        _eager.load().mlm_transform(x, W, vec[0], vec[1], vec[2], eps).backward(dy)
 
     vl = [v.detach().to(dt).requires_grad_() for v in vec]
 

@@ -16,6 +16,8 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIB_NAME = "libsparton_hip.so"
 LIB_PATH = os.path.join(HERE, LIB_NAME)
+TORCH_LIB_NAME = "libsparton_torch.so"   # the eager torch ops (C++ autograd), on the C ABI above
+TORCH_LIB_PATH = os.path.join(HERE, TORCH_LIB_NAME)
 SOURCES = ["sparton_fwd.hip", "sparton_bwd.hip", "sparton_transform.hip", "sparton_loss.hip",
            "sparton_probe.hip", "sparton_capi.cpp"]
 ARCH = os.environ.get("SPARTON_OFFLOAD_ARCH", "gfx950")
@@ -59,7 +61,35 @@ def build_library(verbose: bool = False) -> str:
     os.replace(tmp, LIB_PATH)
     if verbose:
         print(f"built {LIB_PATH}")
+    build_torch_ops(verbose)
     return LIB_PATH
+
+
+def build_torch_ops(verbose: bool = False) -> str:
+    """libsparton_torch.so: the sparton_eager torch ops (csrc/sparton_torch.cpp), a host-only
+    C++ library compiled with g++ against libtorch and linked to libsparton_hip.so, which it
+    finds next to itself (rpath $ORIGIN)."""
+    import torch
+    tdir = os.path.dirname(torch.__file__)
+    cxx = os.environ.get("CXX", "g++")
+    tmp = TORCH_LIB_PATH + ".tmp"
+    cmd = [cxx, "-O2", "-std=c++17", "-fPIC", "-shared", "-fvisibility=hidden", "-Wall",
+           "-D__HIP_PLATFORM_AMD__", "-DUSE_ROCM",
+           f"-D_GLIBCXX_USE_CXX11_ABI={int(torch._C._GLIBCXX_USE_CXX11_ABI)}",
+           "-I", os.path.join(tdir, "include"),
+           "-I", os.path.join(tdir, "include", "torch", "csrc", "api", "include"),
+           "-I", "/opt/rocm/include",
+           os.path.join(CSRC, "sparton_torch.cpp"), "-o", tmp,
+           "-L", os.path.join(tdir, "lib"), "-ltorch", "-ltorch_cpu", "-lc10", "-lc10_hip",
+           "-ltorch_hip", "-L", HERE, "-lsparton_hip",
+           f"-Wl,-rpath,{os.path.join(tdir, 'lib')}", "-Wl,-rpath,$ORIGIN"]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"compile failed: {' '.join(cmd)}\n{res.stdout}\n{res.stderr}")
+    os.replace(tmp, TORCH_LIB_PATH)
+    if verbose:
+        print(f"built {TORCH_LIB_PATH}")
+    return TORCH_LIB_PATH
 
 
 if __name__ == "__main__":

@@ -13,41 +13,7 @@ import torch
 import torch.nn.functional as F
 from torch import nn
 
-from . import ops  # noqa: F401  (registers torch.ops.sparton.*)
-
-
-class _AutocastTrainFn(torch.autograd.Function):
-    """Training forward/backward under autocast with fp32 parameters (the usual
-    mixed-precision setup: fp32 master weights, bf16/fp16 compute).
-
-    The forward casts W, bias and H to the compute dtype and runs the training kernels on
-    them, as the plain path does. The backward writes dH, dW and dbias in fp32 straight from
-    the kernels' fp32 sums, so dW reaches the fp32 master without autograd's cast pass
-    (read a [V,D] 16-bit gradient, write it again as fp32) and without being rounded to
-    16 bits on the way."""
-
-    @staticmethod
-    def forward(ctx, hidden, weight, bias, mask, dt, pad, cast):
-        # cast(t): the compute-dtype (zero-padded) copy of a parameter, reused while unchanged
-        w = cast(weight, dt, pad, "weight")
-        b = cast(bias, dt, 0, "bias") if bias is not None else None
-        h = hidden.to(dt)
-        if pad:
-            h = F.pad(h, (0, pad))
-        reps, idx, reps32 = ops._fwd_impl(h, w, b, mask, True, True,
-                                          "sparton::fused_sparton_fwd_train")
-        ctx.save_for_backward(reps32, idx, h, w, b, mask)
-        ctx.hidden_dtype, ctx.D, ctx.has_bias = hidden.dtype, hidden.shape[-1], bias is not None
-        return reps
-
-    @staticmethod
-    def backward(ctx, grad_reps):
-        reps32, idx, h, w, b, mask = ctx.saved_tensors
-        d_h, d_w, d_b = ops._bwd_impl(grad_reps, reps32, idx, h, w, b, mask, torch.float32,
-                                      "sparton::fused_sparton_bwd")
-        if d_h.shape[-1] != ctx.D:  # drop the zero padding columns
-            d_h, d_w = d_h[..., :ctx.D], d_w[:, :ctx.D]
-        return (d_h.to(ctx.hidden_dtype), d_w, d_b if ctx.has_bias else None, None, None, None, None)
+from . import _eager, ops  # ops registers torch.ops.sparton.*
 
 
 class _CastCache:
@@ -116,18 +82,24 @@ class SpartonHead(nn.Module):
     def forward(self, hidden_states, attention_mask):
         hidden, weight, bias = hidden_states, self.weight, self.bias
         dev = hidden.device.type
+        eager = hidden.is_cuda and not torch.compiler.is_compiling()
         # The reference leaves autocast to leak into its torch.compile'd GEMM; the HIP
         # op does not see autocast, so apply the autocast dtype here explicitly.
         if dev in ("cuda", "cpu") and torch.is_autocast_enabled(dev):
             dt = torch.get_autocast_dtype(dev)
-            if (dt in (torch.bfloat16, torch.float16) and weight.dtype == torch.float32
+            if (eager and dt in (torch.bfloat16, torch.float16) and weight.dtype == torch.float32
                     and (bias is None or bias.dtype == torch.float32)
-                    and torch.is_grad_enabled() and not torch.compiler.is_compiling()
+                    and torch.is_grad_enabled()
                     and (hidden.requires_grad or weight.requires_grad
                          or (bias is not None and bias.requires_grad))):
+                # Mixed-precision training: the kernels run on the cached compute-dtype copies
+                # and write fp32 gradients straight to the masters (C++ autograd).
                 pad = (-hidden.shape[-1]) % (128 // torch.finfo(dt).bits)  # 16-byte chunks
-                return _AutocastTrainFn.apply(hidden, weight, bias, attention_mask, dt, pad,
-                                              self._cast_cache)
+                wc = self._cast_cache(weight, dt, pad, "weight")
+                bc = self._cast_cache(bias, dt, 0, "bias") if bias is not None else None
+                _check_autocast(hidden, weight, bias, attention_mask, wc)
+                return _eager.load().head_train_autocast(hidden, weight, bias, attention_mask,
+                                                         wc, bc, pad)
             if (weight.dtype == torch.float32 and not torch.compiler.is_compiling()
                     and not (torch.is_grad_enabled() and weight.requires_grad)):
                 weight = self._cast_cache(weight, dt, 0, "weight")  # inference: reuse the cast copy
@@ -146,8 +118,35 @@ class SpartonHead(nn.Module):
             hidden, weight = F.pad(hidden, (0, pad)), F.pad(weight, (0, pad))
         needs_grad = torch.is_grad_enabled() and (
             hidden.requires_grad or weight.requires_grad or (bias is not None and bias.requires_grad))
+        if eager:
+            # C++ ops (autograd in C++): the same kernels as the torch.library ops below
+            ops._validate(hidden, weight, bias, attention_mask, "SpartonHead")
+            E = _eager.load()
+            if needs_grad:
+                return E.head_train(hidden, weight, bias, attention_mask)
+            return E.head_encode(hidden, weight, bias, attention_mask)
         if needs_grad:
             scores, _idx, _scores32 = torch.ops.sparton.fused_sparton_fwd_train(
                 hidden, weight, bias, attention_mask)
             return scores
         return torch.ops.sparton.fused_sparton_encode(hidden, weight, bias, attention_mask)
+
+
+def _check_autocast(hidden, weight, bias, mask, weight_c):
+    """The checks of ops._validate for the mixed-precision path (fp32 hidden and masters,
+    16-bit padded weight copy)."""
+    op = "SpartonHead"
+    if hidden.dim() != 3 or weight.dim() != 2 or weight.shape[1] != hidden.shape[2]:
+        raise ValueError(f"{op}: hidden must be [B,S,D] and weight [V,D], got "
+                         f"{tuple(hidden.shape)} and {tuple(weight.shape)}")
+    B, S, _ = hidden.shape
+    V = weight.shape[0]
+    if bias is not None and tuple(bias.shape) != (V,):
+        raise ValueError(f"{op}: bias must be [V]=[{V}], got {tuple(bias.shape)}")
+    if tuple(mask.shape) != (B, S):
+        raise ValueError(f"{op}: mask must be [B,S]=[{B},{S}], got {tuple(mask.shape)}")
+    if mask.dtype not in ops._lib.MASK_CODE:
+        raise TypeError(f"{op}: mask dtype {mask.dtype} not supported")
+    for t in (weight, bias, mask, weight_c):
+        if t is not None and t.device != hidden.device:
+            raise ValueError(f"{op}: all tensors must be on {hidden.device}, got {t.device}")

@@ -26,7 +26,7 @@ from typing import NamedTuple, Optional, Tuple
 import torch
 from torch import Tensor
 
-from . import _lib
+from . import _eager, _lib
 
 MAX_ROWS = 128
 _FLOAT_DTYPES = tuple(_lib.DTYPE_CODE)
@@ -153,33 +153,16 @@ def _backward(ctx, g_out, _g_probs):
 splade_loss_fwd.register_autograd(_backward, setup_context=_setup_context)
 
 
-class _LossFn(torch.autograd.Function):
-    """The eager path: the same implementation as the custom ops, without the dispatcher
-    round trips of torch.library (used unless torch.compile is tracing)."""
-
-    @staticmethod
-    def forward(ctx, q, d, temperature, w_ce, w_l1, w_flops):
-        out, probs = _fwd_impl(q, d, temperature, w_ce, w_l1, w_flops)
-        ctx.has_d = d is not None
-        ctx.w = (w_ce, w_l1, w_flops)
-        ctx.save_for_backward(q, d if d is not None else q.new_empty(0), probs)
-        ctx.mark_non_differentiable(probs)
-        return out, probs
-
-    @staticmethod
-    def backward(ctx, g_out, _g_probs):
-        q, d, probs = ctx.saved_tensors
-        dq, dd = _bwd_impl(g_out, q, d if ctx.has_d else None, probs, *ctx.w)
-        return dq, (dd if ctx.has_d else None), None, None, None, None
-
-
 def _run(q: Tensor, d: Optional[Tensor], temperature: float, w_ce: float, w_l1: float,
          w_flops: float) -> Tensor:
-    if torch.compiler.is_compiling():
+    if torch.compiler.is_compiling() or not q.is_cuda:
         out, _ = torch.ops.sparton.splade_loss_fwd(q, d, temperature, w_ce, w_l1, w_flops)
-    else:
-        out, _ = _LossFn.apply(q, d, temperature, w_ce, w_l1, w_flops)
-    return out
+        return out
+    # eager: the C++ op (autograd in C++), the same implementation as the custom ops
+    _check(q, d, "splade_loss")
+    if d is not None and not temperature > 0.0:
+        raise ValueError(f"splade_loss: temperature must be > 0, got {temperature}")
+    return _eager.load().splade_loss(q, d, float(temperature), float(w_ce), float(w_l1), float(w_flops))
 
 
 def splade_loss(query_reps: Tensor, doc_reps: Optional[Tensor], temperature: float = 1.0,

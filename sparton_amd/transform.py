@@ -24,7 +24,7 @@ import torch
 import torch.nn.functional as F
 from torch import Tensor, nn
 
-from . import _lib
+from . import _eager, _lib
 
 _FLOAT_DTYPES = tuple(_lib.DTYPE_CODE)
 
@@ -181,24 +181,6 @@ def _backward(ctx, dy, _dz, _dmean, _drstd):
 mlm_transform_fwd.register_autograd(_backward, setup_context=_setup_context)
 
 
-class _TransformFn(torch.autograd.Function):
-    """The module's eager path: the same implementation as the custom ops, without the
-    dispatcher round trips of torch.library (roughly 90 us of host time per fwd+bwd on
-    one server core). Under torch.compile the module calls the custom op instead."""
-
-    @staticmethod
-    def forward(ctx, x, weight, dense_bias, ln_weight, ln_bias, eps):
-        y, z, mean, rstd = _fwd_impl(x, weight, dense_bias, ln_weight, ln_bias, eps)
-        ctx.save_for_backward(x, weight, z, dense_bias, ln_weight, mean, rstd)
-        return y
-
-    @staticmethod
-    def backward(ctx, dy):
-        x, weight, z, dense_bias, ln_weight, mean, rstd = ctx.saved_tensors
-        dx, dw, dbd, dg, dbt = _bwd_impl(dy, x, weight, z, dense_bias, ln_weight, mean, rstd)
-        return dx, dw, dbd, dg, dbt, None
-
-
 def _is_erf_gelu(act) -> bool:
     """torch's F.gelu / nn.GELU() without the tanh approximation, or transformers'
     GELUActivation (hidden_act "gelu" or "gelu_python", both the erf form)."""
@@ -247,6 +229,8 @@ class SpartonMLMTransform(nn.Module):
             weight = weight.to(x.dtype)
         args = (x, weight, self.dense.bias.float(), self.layer_norm.weight.float(),
                 self.layer_norm.bias.float(), float(self.layer_norm.eps))
-        if torch.compiler.is_compiling():  # the registered op: fake + autograd, no graph break
+        if torch.compiler.is_compiling() or not x.is_cuda:  # the registered op: fake + autograd
             return torch.ops.sparton.mlm_transform_fwd(*args)[0]
-        return _TransformFn.apply(*args)
+        # eager: the C++ op (autograd in C++), the same implementation as the custom ops
+        _check(args[0], args[1], args[2:5], "SpartonMLMTransform")
+        return _eager.load().mlm_transform(*args)

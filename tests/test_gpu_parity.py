@@ -698,3 +698,37 @@ def test_autocast_weight_cast_is_cached_until_updated(device):
         with torch.autocast("cuda", dtype=torch.bfloat16):
             r4 = head(H, m)
     assert torch.equal(r4, r3.detach())
+
+
+@pytest.mark.parametrize("use_bias", [True, False])
+def test_eager_cpp_head_equals_custom_ops(use_bias, device):
+    """SpartonHead's eager path (the C++ op sparton_eager::head_train, autograd in C++) gives
+    bitwise the reps and gradients of the torch.library training op with its Python autograd,
+    and inference (sparton_eager::head_encode) the reps of sparton::fused_sparton_encode."""
+    from sparton_amd import _eager
+    say(f"C++ eager head vs custom ops, bias={use_bias}")
+    H, W, b, m, G = make_case("bf16", 4, 150, 128, 2000, use_bias, "int64", seed=4)
+    Hd, Wd, md, Gd = H.to(device), W.to(device), m.to(device), G.to(device)
+    bd = b.to(device) if b is not None else None
+    outs = []
+    for path in ("eager", "op"):
+        h = Hd.clone().requires_grad_()
+        w = Wd.clone().requires_grad_()
+        bb = bd.clone().requires_grad_() if bd is not None else None
+        if path == "eager":
+            r = _eager.load().head_train(h, w, bb, md)
+        else:
+            r = torch.ops.sparton.fused_sparton_fwd_train(h, w, bb, md)[0]
+        r.backward(Gd)
+        outs.append([r.detach(), h.grad, w.grad] + ([bb.grad] if bb is not None else []))
+    torch.cuda.synchronize()
+    for a, c in zip(*outs):
+        assert torch.equal(a, c)
+    e = _eager.load().head_encode(Hd, Wd, bd, md)
+    assert torch.equal(e, torch.ops.sparton.fused_sparton_encode(Hd, Wd, bd, md))
+    head = sparton.SpartonHead(2000, 128, use_bias=use_bias).to(device).bfloat16()
+    with torch.no_grad():
+        head.weight.copy_(Wd)
+        if use_bias:
+            head.bias.copy_(bd)
+    assert torch.equal(head(Hd, md), e)  # no grad needed: the module takes head_encode
