@@ -3,6 +3,9 @@
 Two subcommands, each reading rocprofv3 CSV output (``--output-format csv``):
 
   stats    --kernel-trace --stats:  per-kernel calls and mean/min/max duration.
+  mfma     one --pmc pass of SQ_VALU_MFMA_BUSY_CYCLES, SQ_INSTS_MFMA and GRBM_GUI_ACTIVE:
+           per kernel, the medians per dispatch and the matrix pipes' busy fraction,
+           busy / (GPU cycles x 1024 SIMDs), GPU cycles = GRBM_GUI_ACTIVE / 8 XCDs.
   traffic  two --pmc passes (FETCH_SIZE, then WRITE_SIZE):  HBM bytes per dispatch
            of every SpartonHead kernel, scaled by what the same counters read for a
            plain device copy of known size (bench.py --copy-probe-mib N launches one
@@ -67,6 +70,26 @@ def counter_values(path, counter):
     return acc
 
 
+def mfma(path, simds=1024, xcds=8):
+    """{kernel: dict} of median MFMA counters per dispatch and the busy fraction."""
+    import statistics
+    busy = counter_values(path, "SQ_VALU_MFMA_BUSY_CYCLES")
+    insts = counter_values(path, "SQ_INSTS_MFMA")
+    grbm = counter_values(path, "GRBM_GUI_ACTIVE")
+    out = {}
+    for k, v in busy.items():
+        if k not in grbm or k not in insts:
+            continue
+        b, n, g = statistics.median(v), statistics.median(insts[k]), statistics.median(grbm[k])
+        if n <= 0:
+            continue
+        cyc = g / xcds
+        out[short_name(k)] = {"dispatches": len(v), "gpu_cycles": cyc, "mfma_busy_cycles": b,
+                              "mfma_insts": n, "busy_cycles_per_mfma": b / n,
+                              "mfma_busy_frac": b / (cyc * simds)}
+    return out
+
+
 def _probe(values):
     """(value, kernel) of the largest single copy dispatch: the copy probe."""
     return max(((max(v), k) for k, v in values.items() if "copy" in k.lower() and "sparton" not in k),
@@ -107,6 +130,8 @@ def main(argv=None):
     sub = ap.add_subparsers(dest="cmd", required=True)
     s = sub.add_parser("stats")
     s.add_argument("path")
+    m = sub.add_parser("mfma")
+    m.add_argument("path")
     t = sub.add_parser("traffic")
     t.add_argument("fetch_dir")
     t.add_argument("write_dir")
@@ -118,6 +143,11 @@ def main(argv=None):
         for r in kernel_stats(a.path):
             print(f"{r['kernel']:<60} {r['calls']:>6} {r['mean_us']:>9.1f} {r['min_us']:>9.1f} "
                   f"{r['max_us']:>9.1f} {r['pct']:>6.2f}")
+    elif a.cmd == "mfma":
+        for k, r in mfma(a.path).items():
+            print(f"{k}: {r['dispatches']} dispatches, {r['gpu_cycles'] / 1e3:.1f} K GPU cycles, "
+                  f"{r['mfma_insts'] / 1e6:.3f} M MFMA, {r['busy_cycles_per_mfma']:.1f} busy cycles "
+                  f"per MFMA, matrix pipes busy {100 * r['mfma_busy_frac']:.1f}%")
     else:
         res = traffic(a.fetch_dir, a.write_dir, a.copy_mib)
         print(json.dumps(res, indent=1))
