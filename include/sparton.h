@@ -244,7 +244,8 @@ int sparton_mfma_probe(int dtype, int grid, int iters, float* out, long long* cl
 /* Static, thread-safe description of a status code. */
 const char* sparton_strerror(int code);
 
-/* Supported ranges: writes max S and max B of the backward. */
+/* Supported ranges: writes max S and max B of the backward (each 2^31 - 1 since ABI 8;
+ * B * S and B * V must also stay below 2^31). */
 void sparton_limits(int64_t* max_bwd_seq, int64_t* max_bwd_batch);
 
 /* ABI version of this header (bumped on any signature change). */

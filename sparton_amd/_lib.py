@@ -15,7 +15,7 @@ import torch  # noqa: F401  (must be imported first: see module docstring)
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 DEFAULT_LIB = os.path.join(_HERE, "libsparton_hip.so")
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 # enum sparton_dtype / sparton_mask_dtype (include/sparton.h)
 DTYPE_CODE = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}

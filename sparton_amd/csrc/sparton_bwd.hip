@@ -40,8 +40,8 @@ namespace bwd {
 
 constexpr int CHW = 1024;          // vocab ids per wave chunk (16 rounds of 64 lanes)
 constexpr int ROUNDS = CHW / 64;
-constexpr int MAX_S = 16384;       // LDS: S mask floats + S counters per wave
-constexpr int MAX_B = 8192;
+constexpr int MAX_S = 16384;       // positions per dH window (LDS: S mask floats + S counters per wave)
+constexpr int MAX_B = 8192;        // batch rows per dH chunk
 constexpr int MAX_NP = 16;         // D up to 16 * 256 per register pass
 
 struct Layout {
@@ -67,14 +67,20 @@ static Layout layout(int64_t B, int64_t S, int64_t V) {
   return L;
 }
 
+// The workspace of one dH pass (at most MAX_B batch rows x MAX_S positions); the fused
+// path's layout (B <= DW_STAGE_B, S <= FUSE_MAX_S) is the same.
+static Layout pass_layout(int64_t B, int64_t S, int64_t V) {
+  return layout(std::min<int64_t>(B, MAX_B), std::min<int64_t>(S, MAX_S), V);
+}
+
 // Waves per block of the count/scatter kernels: LDS holds S mask floats plus S
 // counters per wave (at most 40 KB with 4 waves, 128 KB with one wave at MAX_S).
 static int waves_for(int64_t S) { return S <= 2048 ? 4 : 1; }
 
-// Stage mask row b as floats in LDS.
-__device__ __forceinline__ void stage_mask(float* maskf, const void* mask, int mdt, int64_t b,
+// Stage the S mask entries from element `off` on as floats in LDS.
+__device__ __forceinline__ void stage_mask(float* maskf, const void* mask, int mdt, int64_t off,
                                            int S) {
-  for (int s = threadIdx.x; s < S; s += blockDim.x) maskf[s] = load_mask(mask, mdt, b * S + s);
+  for (int s = threadIdx.x; s < S; s += blockDim.x) maskf[s] = load_mask(mask, mdt, off + s);
 }
 
 // Entry (b, v): whether it carries gradient, its coefficient g' and index s.
@@ -133,17 +139,21 @@ template <typename T, typename RT>
 __global__ __launch_bounds__(256) void bwd_count_kernel(
     const T* __restrict__ grad, const RT* __restrict__ reps, const int32_t* __restrict__ idx,
     const void* __restrict__ mask, int mdt, int S, int V, int nch, int* __restrict__ hist,
-    int2* __restrict__ comp, int* __restrict__ ccount) {
+    int2* __restrict__ comp, int* __restrict__ ccount, int s0, int64_t mrow0, int S_row) {
   float* maskf = (float*)sparton_bwd_smem;
   const int wpb = blockDim.x >> 6, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   int* h = (int*)(maskf + S) + wave * S;
   const int b = blockIdx.y, c = blockIdx.x * wpb + wave;
-  stage_mask(maskf, mask, mdt, b, S);
+  stage_mask(maskf, mask, mdt, (mrow0 + b) * S_row + s0, S);
   for (int s = lane; s < S; s += 64) h[s] = 0;
   __syncthreads();
   if (c < nch) {
     ChunkData<T, RT> d;
     d.load(grad, reps, idx, (int64_t)b * V, c * CHW, V, lane);
+    // Positions relative to the window (wrapping: an index outside it lands outside
+    // [0, S) and the entry is inactive).
+#pragma unroll
+    for (int j = 0; j < ROUNDS; ++j) d.s[j] = (int)((unsigned)d.s[j] - (unsigned)s0);
     // Active entries are also compacted, in v order, into the chunk's slice of comp.
     int2* cb = comp + ((int64_t)b * nch + c) * CHW;
     const uint64_t lt = (1ull << lane) - 1ull;
@@ -306,7 +316,8 @@ __global__ __launch_bounds__(SCAN_THREADS) void bwd_scan_parts_kernel(int* __res
 // program order), so each segment lists its vocab ids in ascending order.
 __global__ __launch_bounds__(256) void bwd_scatter_kernel(
     const int32_t* __restrict__ idx, int S, int V, int nch, const int* __restrict__ hist_base,
-    const int2* __restrict__ comp, const int* __restrict__ ccount, int2* __restrict__ list) {
+    const int2* __restrict__ comp, const int* __restrict__ ccount, int2* __restrict__ list,
+    int s0) {
   int* cur = (int*)sparton_bwd_smem + (threadIdx.x >> 6) * S;
   const int wpb = blockDim.x >> 6, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int b = blockIdx.y, c = blockIdx.x * wpb + wave;
@@ -322,7 +333,7 @@ __global__ __launch_bounds__(256) void bwd_scatter_kernel(
   for (int i0 = 0; i0 < n; i0 += 64) {
     const bool act = i0 + lane < n;
     const int2 e = cb[act ? i0 + lane : 0];
-    const int s = act ? ib[e.x] : 0;
+    const int s = act ? ib[e.x] - s0 : 0;  // compacted entries lie in the window
     const uint64_t act_mask = __ballot(act);
     uint64_t same = act_mask;
     for (int k = 0; k < sbits; ++k) {
@@ -391,7 +402,7 @@ template <typename T, int NP> struct DwPasses {
 template <typename T, typename O, int NP>
 __global__ __launch_bounds__(256) void bwd_dh_kernel(
     const T* __restrict__ W, const int2* __restrict__ list, const int* __restrict__ seg_start,
-    const int* __restrict__ seg_cnt, O* __restrict__ dH, int B, int S, int D, int V) {
+    const int* __restrict__ seg_cnt, O* __restrict__ dH, int B, int S, int D, int V, int S_row) {
   constexpr int U = Batch<NP>::U;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * 4 + wave;
@@ -430,7 +441,7 @@ __global__ __launch_bounds__(256) void bwd_dh_kernel(
           for (int p = 0; p < NP; ++p) acc[p] += g[u] * w[u][p].f();
       }
     }
-    O* out = dH + row * D;
+    O* out = dH + (b * S_row + (row - b * S)) * D;
 #pragma unroll
     for (int p = 0; p < NP; ++p) {
       const int d = d0 + p * 256 + lane * 4;
@@ -452,7 +463,7 @@ template <int NP> struct SplitRW<NP, 1> { static constexpr int value = 1; };
 template <typename T, typename O, int NP, int RW>
 __global__ __launch_bounds__(64 * RW) void bwd_dh_split_kernel(
     const T* __restrict__ W, const int2* __restrict__ list, const int* __restrict__ seg_start,
-    const int* __restrict__ seg_cnt, O* __restrict__ dH, int B, int S, int D, int V) {
+    const int* __restrict__ seg_cnt, O* __restrict__ dH, int B, int S, int D, int V, int S_row) {
   constexpr int U = Batch<NP>::U;
   __shared__ __attribute__((aligned(16))) float red[RW][SplitLds<NP>::floats];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -495,7 +506,7 @@ __global__ __launch_bounds__(64 * RW) void bwd_dh_split_kernel(
     for (int p = 0; p < NP; ++p) *(f32x4*)&red[wave][p * 256 + lane * 4] = acc[p];
     __syncthreads();
     if (wave == 0) {
-      O* out = dH + row * D;
+      O* out = dH + (b * S_row + (row - b * S)) * D;
 #pragma unroll
       for (int p = 0; p < NP; ++p) {
         f32x4 t = *(const f32x4*)&red[0][p * 256 + lane * 4];
@@ -982,44 +993,61 @@ static void launch_rows(const T* g, const RT* r, const int32_t* idx, const void*
     return;
   }
   if (dH != nullptr && B * S > 0 && D > 0) {
-    const Layout L = layout(B, S, V);
+    // Batch rows in chunks of at most MAX_B and positions in windows of at most MAX_S:
+    // each pass runs count -> scan -> scatter -> dH over rows [b0, b0 + nb) and
+    // positions [s0, s0 + sw), with entries whose index lies outside the window
+    // inactive, so every dH row is written by exactly one pass. The workspace holds
+    // one pass; the passes reuse it in stream order.
+    const int64_t Bc = std::min<int64_t>(B, MAX_B), Sc = std::min<int64_t>(S, MAX_S);
+    const Layout L = layout(Bc, Sc, V);
     int* hist = (int*)((char*)ws + L.hist);
     int* seg_start = (int*)((char*)ws + L.seg_start);
     int* seg_cnt = (int*)((char*)ws + L.seg_cnt);
     int2* list = (int2*)((char*)ws + L.list);
     int2* comp = (int2*)((char*)ws + L.comp);
     int* ccount = (int*)((char*)ws + L.ccount);
-    const int wpb = waves_for(S);
-    const dim3 cgrid((unsigned)cdiv(L.nch, wpb), (unsigned)B);
-    const size_t cl = (size_t)S * 4 * (1 + wpb);
-    if (L.nch > 0)
-      hipLaunchKernelGGL((bwd_count_kernel<T, RT>), cgrid, dim3(64 * wpb), cl, st, g, r, idx,
-                         mask, mdt, (int)S, (int)V, (int)L.nch, hist, comp, ccount);
-    if (S <= SCAN_THREADS / 2)
-      hipLaunchKernelGGL(bwd_scan_parts_kernel, dim3((unsigned)B), dim3(SCAN_THREADS), 0, st, hist,
-                         seg_start, seg_cnt, (int)S, (int)L.nch, (int)round_up(S, 64));
-    else
-      hipLaunchKernelGGL(bwd_scan_kernel, dim3((unsigned)B),
-                         dim3((unsigned)std::min<int64_t>(SCAN_THREADS, round_up(S, 64))), 0, st, hist,
-                         seg_start, seg_cnt, (int)S, (int)L.nch);
-    if (L.nch > 0)
-      hipLaunchKernelGGL(bwd_scatter_kernel, cgrid, dim3(64 * wpb), (size_t)S * 4 * wpb, st, idx,
-                         (int)S, (int)V, (int)L.nch, (const int*)hist, (const int2*)comp,
-                         (const int*)ccount, list);
-    const int rw = dh_row_waves(B * S, NP);
-#define DH_SPLIT(RW)                                                                            \
-  hipLaunchKernelGGL((bwd_dh_split_kernel<T, O, NP, SplitRW<NP, RW>::value>), dim3((unsigned)(B * S)), \
-                     dim3(64 * SplitRW<NP, RW>::value), 0,                                           \
-                     st, W, (const int2*)list, (const int*)seg_start, (const int*)seg_cnt, dH,   \
-                     (int)B, (int)S, (int)D, (int)V)
-    if (rw >= 8) DH_SPLIT(8);
-    else if (rw >= 4) DH_SPLIT(4);
-    else if (rw >= 2) DH_SPLIT(2);
-    else
-      hipLaunchKernelGGL((bwd_dh_kernel<T, O, NP>), dim3((unsigned)cdiv(B * S, 4)), dim3(256), 0,
-                         st, W, (const int2*)list, (const int*)seg_start, (const int*)seg_cnt, dH,
-                         (int)B, (int)S, (int)D, (int)V);
+    for (int64_t b0 = 0; b0 < B; b0 += Bc) {
+      const int64_t nb = std::min(Bc, B - b0);
+      const T* gb = g + b0 * V;
+      const RT* rb = r + b0 * V;
+      const int32_t* ib = idx + b0 * V;
+      for (int64_t s0 = 0; s0 < S; s0 += Sc) {
+        const int64_t sw = std::min(Sc, S - s0);
+        O* dhb = dH + (b0 * S + s0) * D;
+        const int wpb = waves_for(sw);
+        const dim3 cgrid((unsigned)cdiv(L.nch, wpb), (unsigned)nb);
+        const size_t cl = (size_t)sw * 4 * (1 + wpb);
+        if (L.nch > 0)
+          hipLaunchKernelGGL((bwd_count_kernel<T, RT>), cgrid, dim3(64 * wpb), cl, st, gb, rb, ib,
+                             mask, mdt, (int)sw, (int)V, (int)L.nch, hist, comp, ccount, (int)s0,
+                             b0, (int)S);
+        if (sw <= SCAN_THREADS / 2)
+          hipLaunchKernelGGL(bwd_scan_parts_kernel, dim3((unsigned)nb), dim3(SCAN_THREADS), 0, st,
+                             hist, seg_start, seg_cnt, (int)sw, (int)L.nch, (int)round_up(sw, 64));
+        else
+          hipLaunchKernelGGL(bwd_scan_kernel, dim3((unsigned)nb),
+                             dim3((unsigned)std::min<int64_t>(SCAN_THREADS, round_up(sw, 64))), 0, st,
+                             hist, seg_start, seg_cnt, (int)sw, (int)L.nch);
+        if (L.nch > 0)
+          hipLaunchKernelGGL(bwd_scatter_kernel, cgrid, dim3(64 * wpb), (size_t)sw * 4 * wpb, st, ib,
+                             (int)sw, (int)V, (int)L.nch, (const int*)hist, (const int2*)comp,
+                             (const int*)ccount, list, (int)s0);
+        const int rw = dh_row_waves(nb * sw, NP);
+#define DH_SPLIT(RW)                                                                             \
+  hipLaunchKernelGGL((bwd_dh_split_kernel<T, O, NP, SplitRW<NP, RW>::value>),                    \
+                     dim3((unsigned)(nb * sw)), dim3(64 * SplitRW<NP, RW>::value), 0, st, W,     \
+                     (const int2*)list, (const int*)seg_start, (const int*)seg_cnt, dhb, (int)nb, \
+                     (int)sw, (int)D, (int)V, (int)S)
+        if (rw >= 8) DH_SPLIT(8);
+        else if (rw >= 4) DH_SPLIT(4);
+        else if (rw >= 2) DH_SPLIT(2);
+        else
+          hipLaunchKernelGGL((bwd_dh_kernel<T, O, NP>), dim3((unsigned)cdiv(nb * sw, 4)), dim3(256), 0,
+                             st, W, (const int2*)list, (const int*)seg_start, (const int*)seg_cnt, dhb,
+                             (int)nb, (int)sw, (int)D, (int)V, (int)S);
 #undef DH_SPLIT
+      }
+    }
   }
   if ((dW != nullptr || dbias != nullptr) && V > 0) {
     if (B <= DW_STAGE_B)
@@ -1069,7 +1097,7 @@ using namespace sparton;
 extern "C" __attribute__((visibility("default"))) size_t sparton_bwd_workspace_bytes(
     int64_t B, int64_t S, int64_t D, int64_t V) {
   if (B <= 0 || S <= 0 || D <= 0 || V < 0) return 0;
-  return bwd::layout(B, S, V).total;
+  return bwd::pass_layout(B, S, V).total;
 }
 
 extern "C" __attribute__((visibility("default"))) int sparton_bwd(
@@ -1094,12 +1122,11 @@ extern "C" __attribute__((visibility("default"))) int sparton_bwd(
   // Outputs are written 4 elements at a time: 16 bytes (fp32) or 8 bytes (16-bit).
   const uintptr_t oalign = grad_dtype == SPARTON_F32 ? 16 : 8;
   if (((uintptr_t)d_hidden | (uintptr_t)d_weight) % oalign != 0) return SPARTON_EALIGN;
-  if (B > bwd::MAX_B || S > bwd::MAX_S) return SPARTON_EUNSUPPORTED;
   if (D > INT32_MAX || V > INT32_MAX || B * S > INT32_MAX || B * V > INT32_MAX)
     return SPARTON_EUNSUPPORTED;
   if (need_dh) {
     if (workspace == nullptr) return SPARTON_EWORKSPACE;
-    if (workspace_bytes < bwd::layout(B, S, V).total) return SPARTON_EWORKSPACE;
+    if (workspace_bytes < bwd::pass_layout(B, S, V).total) return SPARTON_EWORKSPACE;
     if ((uintptr_t)workspace % 256 != 0) return SPARTON_EALIGN;
   }
   if (!need_dh && !need_dw) return SPARTON_OK;

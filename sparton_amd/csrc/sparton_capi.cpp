@@ -4,9 +4,11 @@
 #define SPARTON_EXPORT extern "C" __attribute__((visibility("default")))
 
 namespace {
-constexpr int kAbiVersion = 7;
-constexpr int64_t kMaxBwdSeq = 16384;   // must match bwd::MAX_S in sparton_bwd.hip
-constexpr int64_t kMaxBwdBatch = 8192;  // must match bwd::MAX_B in sparton_bwd.hip
+constexpr int kAbiVersion = 8;
+// The backward takes any S and B with B * S and B * V below 2^31 (it runs its dH passes
+// over windows of positions and chunks of batch rows).
+constexpr int64_t kMaxBwdSeq = INT32_MAX;
+constexpr int64_t kMaxBwdBatch = INT32_MAX;
 }  // namespace
 
 SPARTON_EXPORT const char* sparton_strerror(int code) {

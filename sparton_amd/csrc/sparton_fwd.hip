@@ -79,7 +79,6 @@ constexpr int A_LOADS = BM / ROWS_PER_LOAD / COPY_WAVES;  // wave-wide copies pe
 constexpr int B_LOADS = BN / ROWS_PER_LOAD / COPY_WAVES;  // and for B (8)
 // The copy threads handle one tile row / one column each.
 static_assert(BM == COPY_THREADS && BN == COPY_THREADS, "one copy thread per row and column");
-constexpr int MAX_S = 16384;         // positions per batch row (1024 groups)
 constexpr int PLAN_THREADS = 1024;
 
 // ---- workspace ------------------------------------------------------------------
@@ -1216,10 +1215,14 @@ static int launch(const void* H, const void* W, const void* bias, const void* ma
   return e == hipSuccess ? SPARTON_OK : (int)e;
 }
 
-// Batch rows per launch: byte offsets into H inside a launch stay below 2^31.
+// Batch rows per launch: byte offsets into H inside a launch stay below 2^31 (which also
+// keeps every group code b * ngrp + j and tile-row index an int), and the fixup grid's
+// y dimension (one per batch row) stays within 32768.
+constexpr int64_t MAX_ROWS_PER_LAUNCH = 32768;
 static int64_t rows_per_launch(int64_t B, int64_t S, int64_t D, int64_t esz) {
   const int64_t per_row = std::max<int64_t>(1, S * D * esz);
-  return std::max<int64_t>(1, std::min<int64_t>(B, ((int64_t)1 << 31) / per_row));
+  const int64_t cap = std::min<int64_t>(MAX_ROWS_PER_LAUNCH, ((int64_t)1 << 31) / per_row);
+  return std::max<int64_t>(1, std::min<int64_t>(B, cap));
 }
 
 static int64_t mask_elem_bytes(int mask_dtype) {
@@ -1262,7 +1265,7 @@ static int fwd_run(const void* hidden, const void* weight, const void* bias, con
   const int64_t esz = dtype == SPARTON_F32 ? 4 : 2;
   if ((D * esz) % 16 != 0) return SPARTON_EINVAL;
   if (((uintptr_t)hidden | (uintptr_t)weight) % 16 != 0) return SPARTON_EALIGN;
-  if (S > fwd::MAX_S || B > INT32_MAX || V > INT32_MAX) return SPARTON_EUNSUPPORTED;
+  if (B > INT32_MAX || V > INT32_MAX) return SPARTON_EUNSUPPORTED;
   if (S * D * esz >= ((int64_t)1 << 31) || (int64_t)fwd::BN * D * esz >= ((int64_t)1 << 31))
     return SPARTON_EUNSUPPORTED;
   const size_t need = sparton_fwd_workspace_bytes(B, S, D, V, dtype);

@@ -41,7 +41,7 @@ def test_host_side_entry_points():
     for code in (-1, -2, -3, -4, -5, 7, -99):
         assert len(L.sparton_strerror(code)) > 0
     max_s, max_b = _lib.limits()
-    assert max_s >= 4096 and max_b >= 1024
+    assert max_s == max_b == 2**31 - 1
     ws = L.sparton_bwd_workspace_bytes(32, 256, 768, 30522)
     assert ws % 256 == 0 and ws >= 32 * 30522 * 8 + 2 * 32 * 256 * 4
     assert L.sparton_bwd_workspace_bytes(0, 256, 768, 30522) == 0
@@ -74,7 +74,9 @@ def bwd(**kw):
     (dict(B=-1), -1), (dict(dtype=3), -1), (dict(mask_dtype=6), -1), (dict(hidden=None), -1),
     (dict(D=60), -1), (dict(D=4, dtype=1), -1), (dict(hidden=P + 8), -2), (dict(weight=P + 4), -2),
     (dict(B=0), 0), (dict(V=0), 0), (dict(ws=None), -4), (dict(ws_bytes=16), -4),
-    (dict(ws=P + 16), -2), (dict(S=20000), -3),
+    (dict(ws=P + 16), -2),
+    (dict(S=1 << 24), -3),                # a batch row of H reaches 2^31 bytes
+    (dict(S=20000, ws_bytes=16), -4),     # S > 16384 is accepted (stops at the workspace)
 ])
 def test_fwd_argument_validation(kw, code):
     assert fwd(**kw) == code
@@ -87,7 +89,9 @@ def test_fwd_argument_validation(kw, code):
     (dict(dW=P + 8, grad_dtype=0, ws=P, ws_bytes=1 << 30), -2),
     (dict(weight=None), -1),
     (dict(D=12), -1), (dict(dH=P + 4), -2), (dict(ws=None), -4), (dict(ws=P, ws_bytes=16), -4),
-    (dict(S=1 << 20), -3), (dict(B=1 << 20), -3), (dict(dH=None, dW=None, db=None), 0),
+    (dict(S=1 << 30), -3), (dict(B=1 << 28), -3),   # B * S or B * V reaches 2^31
+    (dict(S=20000), -4), (dict(B=9000), -4),         # accepted (dH passes over windows / chunks)
+    (dict(dH=None, dW=None, db=None), 0),
 ])
 def test_bwd_argument_validation(kw, code):
     assert bwd(**kw) == code

@@ -560,6 +560,25 @@ def test_backward_few_rows_split(case, device):
 
 
 
+@pytest.mark.parametrize("case", [
+    ("bf16", 2, 20000, 64, 320, True, "holes"),     # S > 16384: two dH windows
+    ("fp32", 1, 40000, 32, 200, False, "int64"),    # three windows, the last partial
+    ("fp16", 20, 20000, 32, 64, True, "gaps"),      # 25000 groups: the three-kernel plan
+    ("bf16", 9000, 3, 32, 64, True, "int64"),       # B > 8192: two dH batch chunks
+    ("bf16", 33000, 1, 8, 16, True, "holes"),       # B > 32768: two forward launches
+], ids=lambda c: "-".join(map(str, c)))
+def test_long_sequences_and_many_rows(case, device):
+    """Shapes past one pass of the kernels: the forward takes any S (and splits B over
+    launches of at most 32768 rows); the backward's dH passes run over windows of 16384
+    positions and chunks of 8192 batch rows. Against the oracle."""
+    say(f"long / many rows, case {case}")
+    H, W, b, m, G = make_case(*case)
+    reps, idx, reps32, dH, dW, db = run_fwd_bwd(H, W, b, m, G, device)
+    n, bad = check_fwd(H, W, b, m, reps, idx)
+    say(f"  checked {n} entries, {bad} near-tie argmax differences")
+    check_bwd_isolated(H, W, b, m, G, reps32, idx, dH, dW, db)
+
+
 @pytest.mark.parametrize("dt", [1, 2])
 def test_mfma_probe_reports_cycles(dt, device):
     """sparton_mfma_probe (the measurement kernel bench.py reports as mfma_ceiling) runs on
