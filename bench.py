@@ -71,6 +71,16 @@ def cpu_model():
 
 FWD_KERNEL = "sparton::fwd::sparton_fwd_kernel<%s>"
 KNAME = {"bf16": "bf16", "fp16": "f16", "fp32": "f32"}
+# fp32 batches of at most 128 rows (B * S) run one kernel, one wave per 32 vocab columns.
+SMALL_MAX_ROWS = 128
+SMALL_KERNEL = "sparton::fwd::fwd_small_kernel<%s, %d>"
+SMALL_TNAME = {"bf16": "__bf16", "fp16": "_Float16", "fp32": "float"}
+
+
+def fwd_kernel_name(w, dname):
+    if dname == "fp32" and w.B * w.S <= SMALL_MAX_ROWS:
+        return SMALL_KERNEL % (SMALL_TNAME[dname], min(4, -(-w.B * w.S // 32)))
+    return FWD_KERNEL % KNAME[dname]
 
 
 def measured_traffic(config, kernel):
@@ -554,7 +564,8 @@ def main():
     bwd_bytes = (w.B * w.V * (e + 4 + 4) + u_w * w.D * e + u_h * w.D * e
                  + w.B * w.S * w.D * e + w.V * w.D * e + (w.V * e if has_bias else 0))
     bwd_gbs = bwd_bytes / (bwd_ms * 1e-3) / 1e9
-    traffic, traffic_src = measured_traffic(args.config, FWD_KERNEL % KNAME[dname])
+    kname = fwd_kernel_name(w, dname)
+    traffic, traffic_src = measured_traffic(args.config, kname)
     ceiling = mfma_ceiling(torch, dname)
     # whole-step roofline: the forward at the MFMA peak plus the backward's
     # compulsory bytes at HBM peak, over the measured step; useful flops only
@@ -578,7 +589,7 @@ def main():
         "config": {"workload": f"{w.name} SpartonHead fwd+bwd", "B": w.B, "S": w.S, "D": w.D, "V": w.V,
                    "global_batch": w.B, "seq_len": w.S, "use_bias": has_bias,
                    "valid_tokens": valid_tokens, "parallelism": "none (1 GPU)"},
-        "roofline": {"bound": "mfma", "kernel": FWD_KERNEL % KNAME[dname], "achieved": round(fwd_tflops, 2),
+        "roofline": {"bound": "mfma", "kernel": kname, "achieved": round(fwd_tflops, 2),
                      "peak": peak_tf, "unit": "TFLOP/s", "frac": round(fwd_tflops / peak_tf, 4),
                      "traffic": traffic, "traffic_source": traffic_src, "flops_per_launch": useful_flops,
                      "flops_basis": "useful: 2*D*V*valid_tokens (fully masked 32-row blocks are skipped)",

@@ -46,6 +46,7 @@
 // added when D fits in one), which keeps the two-stage stream uniform.
 
 #include <stdlib.h>
+#include <string.h>
 
 #include <algorithm>
 #include <mutex>
@@ -1150,6 +1151,205 @@ __global__ __launch_bounds__(256) void fwd_fixup_kernel(int V, const int* __rest
   }
 }
 
+// ---- small batches --------------------------------------------------------------
+//
+// fp32 with B * S <= SMALL_MAX_ROWS: one kernel, no plan or fixup. fp32 MFMAs are 16x
+// slower than bf16 ones, so a small batch is bound by MFMA issue, and the 256-column
+// unit gives only cdiv(V, 256) units to 256 CUs (config 1: 120). Here every wave owns
+// 32 vocab columns and all the batch's rows (RB blocks of 32): cdiv(V, 32) waves, about
+// one per SIMD, and W is read once. Each wave loads its operands straight from global
+// memory into registers, one 128-byte K slab per row per window, one window in flight
+// while the other is multiplied; lane (l32, h) holds bytes 64h .. 64h + 63 of each slab
+// in four 16-byte steps, the same K order the main kernel's LDS fragments have, and the
+// accumulators also start at the bias: every logit is summed exactly as the main kernel
+// sums it. (For bf16/fp16 the main kernel is faster: every wave here re-reads all of
+// H, and its loads fetch each 128-byte line in four pieces, where the main kernel
+// shares H through LDS and copies whole lines; measured at B x S of 64 .. 128 rows.) Bytes past D are
+// zero (loaded from inside the row, then cleared), and rows past B * S repeat the last
+// row and are never reduced.
+// Epilogue: x = acc * mask[row] goes to LDS, and lane pairs (batch row b, column) scan
+// the b's S positions in order keeping the largest x with its 5 lowest mantissa bits
+// cleared and, on ties, the lowest s -- the main kernel's key order.
+constexpr int SMALL_MAX_ROWS = 128;
+constexpr int SMALL_WAVES = 4;
+constexpr int SMALL_SLABS = 1;  // 128-byte K slabs per window (2 measured slower)
+
+// One window: NS consecutive 128-byte K slabs of the lane's W row and H rows, four
+// 16-byte steps per slab (lane half h: bytes 64h + 16p of each slab).
+template <typename T, int RB, int NS>
+struct SmallFrag {
+  u32x4 b[NS][4];
+  u32x4 a[NS][RB][4];
+};
+
+template <int RB>
+struct SmallRows {
+  const char* w;      // this lane's W row
+  const char* a[RB];  // this lane's H row in each 32-row block
+};
+
+// Loads of the NS slabs from slab k0 on. TAIL: a slab that ends past D; offsets are
+// clamped into the row.
+template <typename T, int RB, int NS, bool TAIL>
+__device__ __forceinline__ void small_load(SmallFrag<T, RB, NS>& f, const SmallRows<RB>& rp,
+                                           int k0, int h, int row_bytes) {
+#pragma unroll
+  for (int q = 0; q < NS; ++q)
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      int o = (k0 + q) * 128 + h * 64 + p * 16;
+      if (TAIL) o = min(o, row_bytes - 16);
+      f.b[q][p] = *(const u32x4*)(rp.w + o);
+#pragma unroll
+      for (int r = 0; r < RB; ++r) f.a[q][r][p] = *(const u32x4*)(rp.a[r] + o);
+    }
+}
+
+// The MFMAs of the NS slabs from slab k0 on, in K order. TAIL: chunks past D enter as
+// zeros (a select at use: registers with loads in flight are never overwritten).
+template <typename T, int RB, int NS, bool TAIL>
+__device__ __forceinline__ void small_mfma(const SmallFrag<T, RB, NS>& f, f32x16 (&acc)[RB],
+                                           int k0, int h, int row_bytes) {
+#pragma unroll
+  for (int q = 0; q < NS; ++q)
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      const bool ok = !TAIL || (k0 + q) * 128 + h * 64 + p * 16 < row_bytes;
+      const u32x4 z = u32x4{0u, 0u, 0u, 0u};
+      const u32x4 bq = ok ? f.b[q][p] : z;
+#pragma unroll
+      for (int r = 0; r < RB; ++r) Mfma<T>::run(ok ? f.a[q][r][p] : z, bq, acc[r]);
+    }
+}
+
+template <typename T, int RB>
+__global__ __launch_bounds__(64 * SMALL_WAVES) void fwd_small_kernel(
+    const T* __restrict__ H, const T* __restrict__ W, const T* __restrict__ bias,
+    const void* __restrict__ mask, int mask_dtype, T* __restrict__ reps,
+    int32_t* __restrict__ argmax, float* __restrict__ reps_f32, int B, int S, int D, int V) {
+  __shared__ float mk[RB * 32];
+  __shared__ float xs[SMALL_WAVES][RB * 32][33];  // per wave: x[row][column] (+1: no conflicts)
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int l32 = lane & 31, h = lane >> 5;
+  const int rows = B * S;
+  if ((int)threadIdx.x < RB * 32)
+    mk[threadIdx.x] = (int)threadIdx.x < rows ? load_mask(mask, mask_dtype, threadIdx.x) : 0.0f;
+  const int v0 = (blockIdx.x * SMALL_WAVES + wave) * 32;
+  const bool live = v0 < V;  // waves past V only join the barrier
+  const int row_bytes = D * (int)sizeof(T);
+  f32x16 acc[RB];
+  if (live) {
+    const float bv = bias != nullptr ? to_f32(bias[min(v0 + l32, V - 1)]) : 0.0f;
+#pragma unroll
+    for (int r = 0; r < RB; ++r)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) acc[r][i] = bv;
+    SmallRows<RB> rp;
+    rp.w = (const char*)(W + (int64_t)min(v0 + l32, V - 1) * D);
+#pragma unroll
+    for (int r = 0; r < RB; ++r) rp.a[r] = (const char*)(H + (int64_t)min(r * 32 + l32, rows - 1) * D);
+    // Windows of SMALL_SLABS full slabs through a ring of three: two in flight while
+    // one is multiplied. Then the full slabs left over, and the partial slab past the
+    // last full one, if any. Loads past the last window re-read it (unused), so every
+    // window issues the same loads; the scheduling barriers keep each window's loads
+    // together and in issue order, so the wait before a window's MFMAs counts only its
+    // own loads.
+    constexpr int NS = SMALL_SLABS;
+    const int nks = row_bytes >> 7;  // full slabs
+    const int nkw = nks / NS;        // full windows
+    SmallFrag<T, RB, NS> f0, f1, f2;
+    int k = 0;
+    if (nkw > 0) {
+      small_load<T, RB, NS, false>(f0, rp, 0, h, row_bytes);
+      small_load<T, RB, NS, false>(f1, rp, min(1, nkw - 1) * NS, h, row_bytes);
+      for (; k + 2 < nkw; k += 3) {
+        small_load<T, RB, NS, false>(f2, rp, (k + 2) * NS, h, row_bytes);
+        __builtin_amdgcn_sched_barrier(0);
+        small_mfma<T, RB, NS, false>(f0, acc, k * NS, h, row_bytes);
+        __builtin_amdgcn_sched_barrier(0);
+        small_load<T, RB, NS, false>(f0, rp, min(k + 3, nkw - 1) * NS, h, row_bytes);
+        __builtin_amdgcn_sched_barrier(0);
+        small_mfma<T, RB, NS, false>(f1, acc, (k + 1) * NS, h, row_bytes);
+        __builtin_amdgcn_sched_barrier(0);
+        small_load<T, RB, NS, false>(f1, rp, min(k + 4, nkw - 1) * NS, h, row_bytes);
+        __builtin_amdgcn_sched_barrier(0);
+        small_mfma<T, RB, NS, false>(f2, acc, (k + 2) * NS, h, row_bytes);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      // f0, f1 hold windows k, k + 1 (loads clamped to the last window)
+      if (k < nkw) small_mfma<T, RB, NS, false>(f0, acc, k * NS, h, row_bytes);
+      if (k + 1 < nkw) small_mfma<T, RB, NS, false>(f1, acc, (k + 1) * NS, h, row_bytes);
+      k = nkw;
+    }
+    for (int ks = nkw * NS; ks < nks; ++ks) {
+      SmallFrag<T, RB, 1> g;
+      small_load<T, RB, 1, false>(g, rp, ks, h, row_bytes);
+      small_mfma<T, RB, 1, false>(g, acc, ks, h, row_bytes);
+    }
+    if (row_bytes & 127) {
+      SmallFrag<T, RB, 1> g;
+      small_load<T, RB, 1, true>(g, rp, nks, h, row_bytes);
+      small_mfma<T, RB, 1, true>(g, acc, nks, h, row_bytes);
+    }
+  }
+  __syncthreads();  // mk is staged
+  if (live) {
+    // 32x32 accumulator layout: lane holds column l32, register 4q + e row 8q + 4h + e.
+#pragma unroll
+    for (int r = 0; r < RB; ++r)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int row = r * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
+        xs[wave][row][l32] = acc[r][i] * mk[row];
+      }
+  }
+  __syncthreads();
+  if (!live) return;
+  for (int t = lane; t < B * 32; t += 64) {
+    const int b = t >> 5, c = t & 31, v = v0 + c;
+    if (v >= V) continue;
+    float bvx = 0.0f;
+    int bi = 0;
+    for (int s = 0; s < S; ++s) {
+      const float x = __int_as_float(__float_as_int(xs[wave][b * S + s][c]) & ~31);
+      if (x > bvx) {  // strict: the lowest s keeps a tie
+        bvx = x;
+        bi = s;
+      }
+    }
+    const int64_t o = (int64_t)b * V + v;
+    const float rv = log1pf(bvx);
+    reps[o] = from_f32<T>(rv);
+    if (argmax != nullptr) argmax[o] = bi;
+    if (reps_f32 != nullptr) reps_f32[o] = rv;
+  }
+}
+
+// SPARTON_FWD_PATH=main sends small batches through the plan / main / fixup kernels too
+// (tests compare the two paths).
+static bool small_path_enabled() {
+  const char* e = getenv("SPARTON_FWD_PATH");
+  return e == nullptr || strcmp(e, "main") != 0;
+}
+
+template <typename T>
+static void launch_small(const void* H, const void* W, const void* bias, const void* mask,
+                         int mask_dtype, void* reps, int32_t* argmax, float* reps_f32, int64_t B,
+                         int64_t S, int64_t D, int64_t V, hipStream_t stream) {
+  const dim3 grid((unsigned)cdiv(cdiv(V, 32), SMALL_WAVES)), block(64 * SMALL_WAVES);
+#define SMALL(RB)                                                                                   \
+  hipLaunchKernelGGL((fwd_small_kernel<T, RB>), grid, block, 0, stream, (const T*)H, (const T*)W,  \
+                     (const T*)bias, mask, mask_dtype, (T*)reps, argmax, reps_f32, (int)B, (int)S, \
+                     (int)D, (int)V)
+  switch (cdiv(B * S, 32)) {
+    case 1: SMALL(1); break;
+    case 2: SMALL(2); break;
+    case 3: SMALL(3); break;
+    default: SMALL(4); break;
+  }
+#undef SMALL
+}
+
 // Persistent grid: one workgroup per CU (the kernel's LDS allows one per CU), or
 // fewer when there are fewer units. SPARTON_FWD_GRID overrides the workgroup count
 // (tests use it to give each workgroup many units).
@@ -1182,6 +1382,13 @@ static int launch(const void* H, const void* W, const void* bias, const void* ma
   const int64_t n_mt_max = cdiv(B * ngrp, NGRP);
   // Unit numbers (and one round past them) must fit in int.
   if (n_mt_max * n_vt > INT32_MAX / 2) return SPARTON_EUNSUPPORTED;
+  if (sizeof(T) == 4 && B * S > 0 && B * S <= SMALL_MAX_ROWS && small_path_enabled()) {
+    if (ev_main != nullptr) (void)hipEventRecord(ev_main[0], stream);
+    launch_small<T>(H, W, bias, mask, mask_dtype, reps, argmax, reps_f32, B, S, D, V, stream);
+    if (ev_main != nullptr) (void)hipEventRecord(ev_main[1], stream);
+    const hipError_t e = hipGetLastError();
+    return e == hipSuccess ? SPARTON_OK : (int)e;
+  }
   const int64_t grid = persistent_grid(n_mt_max * n_vt);
   if (B * S <= PLAN_TINY_POS && B * ngrp <= PLAN_THREADS) {
     hipLaunchKernelGGL(fwd_plan_tiny_kernel, dim3(1), dim3(PLAN_THREADS), 0, stream, mask,

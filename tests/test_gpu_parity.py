@@ -579,6 +579,34 @@ def test_long_sequences_and_many_rows(case, device):
     check_bwd_isolated(H, W, b, m, G, reps32, idx, dH, dW, db)
 
 
+@pytest.mark.parametrize("case", [
+    ("fp32", 2, 32, 768, 30522, True, "int64"),     # config 1: 64 rows
+    ("fp32", 3, 40, 256, 1000, True, "holes"),      # 120 rows: four 32-row blocks
+    ("fp32", 1, 7, 12, 100, False, "frac"),         # one block, D in one partial slab
+    ("fp32", 5, 20, 132, 333, True, "int64"),       # 100 rows, a 16-byte tail slab
+    ("fp32", 128, 1, 72, 5000, True, "bool"),       # S = 1: every row its own batch row
+    ("fp32", 2, 48, 2048, 2000, False, "int64"),    # 64 full slabs
+    ("bf16", 2, 32, 256, 1000, True, "int64"),      # 16-bit: the main path either way
+], ids=lambda c: "-".join(map(str, c)))
+def test_small_batch_path_equals_main_path(case, device, monkeypatch):
+    """fp32 batches of B * S <= 128 rows take one kernel (one wave per 32 vocab columns,
+    all rows, W read once). It sums every logit in the main kernel's order and applies
+    the same key order, so reps, argmax and the fp32 reps equal the plan / main / fixup
+    path's bitwise; and both match the oracle."""
+    say(f"small-batch path vs main path, case {case}")
+    H, W, b, m, G = make_case(*case)
+    Hd, Wd, md = H.to(device), W.to(device), m.to(device)
+    bd = None if b is None else b.to(device)
+    small = [t.clone() for t in torch.ops.sparton.fused_sparton_fwd_train(Hd, Wd, bd, md)]
+    monkeypatch.setenv("SPARTON_FWD_PATH", "main")
+    main = torch.ops.sparton.fused_sparton_fwd_train(Hd, Wd, bd, md)
+    torch.cuda.synchronize()
+    for a, c in zip(small, main):
+        assert torch.equal(a, c)
+    n, bad = check_fwd(H, W, b, m, small[0], small[1])
+    say(f"  checked {n} entries, {bad} near-tie argmax differences")
+
+
 @pytest.mark.parametrize("dt", [1, 2])
 def test_mfma_probe_reports_cycles(dt, device):
     """sparton_mfma_probe (the measurement kernel bench.py reports as mfma_ceiling) runs on
