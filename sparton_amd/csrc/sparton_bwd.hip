@@ -381,11 +381,13 @@ template <> struct Raw4<f16> {
 // Rows gathered per batch: all their loads are in flight together (about 24 per lane).
 template <int NP> struct Batch { static constexpr int U = NP <= 3 ? 8 : NP <= 6 ? 4 : NP <= 8 ? 3 : 2; };
 
-// The staged dW kernel gathers the rows of IDC of a wave's ids together; their
-// accumulators and U rows of loads fit its 128 VGPRs.
+// The staged dW kernel gathers the rows of IDC of a wave's ids together, U rows at a
+// time. For 16-bit rows of up to 768 elements one id and 4 rows keep it within 64 VGPRs:
+// two 16-wave workgroups per CU, so config 2's 477 workgroups run in one round instead
+// of two (measured: 4 ids x 6 rows at 128 VGPRs, 55.0 us for the backward; 1 x 4, 49.8).
 template <typename T, int NP> struct DwBatch {
-  static constexpr int IDC = NP > 3 ? 1 : sizeof(T) == 2 ? 4 : 2;
-  static constexpr int U = IDC > 1 ? 6 : Batch<NP>::U;
+  static constexpr int IDC = sizeof(T) == 2 ? 1 : NP > 3 ? 1 : 2;
+  static constexpr int U = sizeof(T) == 2 && NP <= 3 ? 4 : IDC > 1 ? 6 : Batch<NP>::U;
 };
 // Register passes of the staged dW kernel: at most 8 (16-bit) or 4 (fp32), so that one
 // id's accumulators and a batch of rows fit 128 VGPRs; longer rows loop over D.
@@ -629,9 +631,9 @@ constexpr int DW_STAGE_B = 128;
 // register pass): an entry packs v and s into one int.
 constexpr int FUSE_V_BITS = 18;
 constexpr int FUSE_MAX_S = 1024;
-constexpr int FUSE_MAX_NVB = (1 << FUSE_V_BITS) / 64;  // 64-id blocks
 constexpr int FUSE_ROWS = 16;                          // rows per range (one workgroup)
 constexpr int FUSE_V_FAST = 1 << 16;    // above this the five-kernel path is faster
+constexpr int FUSE_MAX_NVB = FUSE_V_FAST / 64;         // 64-id blocks the fused path takes
 constexpr int FUSE_MIN_RANGES = 64;     // below this too (too few workgroups)
 constexpr int FUSE_MAX_NR = FUSE_MAX_S / FUSE_ROWS;    // ranges (<= 64: one lane each)
 
@@ -797,25 +799,29 @@ __global__ __launch_bounds__(64 * DW_WAVES) void bwd_dw_staged_kernel(
 }
 
 // ---- 4b. dH from the staged dW kernel's compacted entries (the fused path) -------------
-// Two workgroups per (b, range of FUSE_ROWS consecutive rows); wave w of half h owns row
-// s = FUSE_ROWS * range + FUSE_WAVES * h + w. Each 64-id block of row b lists its active
+// FUSE_HALVES workgroups per (b, range of FUSE_ROWS consecutive rows); wave w of
+// workgroup h owns row s = FUSE_ROWS * range + FUSE_WAVES * h + w. Each 64-id block of row b lists its active
 // entries sorted by row range, then v, so a range's entries are one contiguous run per
 // block: thread t copies the t-th of them into LDS (its block found by binary search over
 // the runs' prefix sums), 64 * FUSE_WAVES per round, in block (= v) order. Each wave
 // appends the entries of its row to its own list, keeping v order, and gathers their W
 // rows U at a time, summing in v order exactly as bwd_dh_kernel does over its segment.
 // With the compaction in the dW kernel this replaces the count, scan and scatter passes.
-constexpr int FUSE_CAP = 256;  // a wave's list; gathered before it could overflow
-constexpr int FUSE_WAVES = 8;  // rows per workgroup: two workgroups per range, so that three
-                               // fit a CU (24 waves) at the dH gathers' ~80 VGPRs
-static_assert(FUSE_ROWS == 2 * FUSE_WAVES, "two workgroups per row range");
-// Register passes the fused path takes (a batch of rows and the accumulators in ~80 VGPRs).
+constexpr int FUSE_CAP = 128;  // a wave's list; gathered before it could overflow
+constexpr int FUSE_WAVES = 8;  // rows per workgroup (one 16-wave workgroup per range measured
+                               // slower: 56.5 vs 49.4 us at config 2)
+constexpr int FUSE_HALVES = FUSE_ROWS / FUSE_WAVES;  // workgroups per row range
+static_assert(FUSE_ROWS % FUSE_WAVES == 0, "whole workgroups per row range");
+// Register passes the fused path takes (a batch of rows and the accumulators in ~64 VGPRs).
 template <typename T> struct FuseMaxNp { static constexpr int value = sizeof(T) == 2 ? 6 : 3; };
+// W rows gathered per batch by the fused dH kernel: fewer than the five-kernel path's, so
+// that the kernel stays within 64 VGPRs (8 waves per SIMD: four workgroups per CU).
+template <int NP> struct FuseBatch { static constexpr int U = NP <= 3 ? 4 : 2; };
 
 template <typename T, int NP>
 __device__ __forceinline__ void gather_rows(const T* __restrict__ W, const int2* list, int n,
                                             int D, int lane, f32x4* acc) {
-  constexpr int U = Batch<NP>::U;
+  constexpr int U = FuseBatch<NP>::U;
   constexpr int VMASK = (1 << FUSE_V_BITS) - 1;
   for (int e0 = 0; e0 < n; e0 += 64) {
     const int2 ent = e0 + lane < n ? list[e0 + lane] : make_int2(0, 0);
@@ -844,22 +850,23 @@ __device__ __forceinline__ void gather_rows(const T* __restrict__ W, const int2*
   }
 }
 
-template <typename T, typename O, int NP>
+// PER: 64-id blocks per thread in the prefix (nvb <= PER * 64 * FUSE_WAVES).
+template <typename T, typename O, int NP, int PER>
 __global__ __launch_bounds__(64 * FUSE_WAVES) void bwd_dh_fused_kernel(
     const T* __restrict__ W, const int2* __restrict__ comp, const int* __restrict__ cnt,
     const int* __restrict__ offs, O* __restrict__ dH, int S, int D, int nvb) {
   constexpr int NT = 64 * FUSE_WAVES;
-  constexpr int PER = FUSE_MAX_NVB / NT;  // blocks per thread in the prefix
-  __shared__ int pre[FUSE_MAX_NVB + 1];   // prefix of the runs' lengths
-  __shared__ int lo_of[FUSE_MAX_NVB];     // each run's first rank in its block
+  static_assert(PER * NT <= FUSE_MAX_NVB, "prefix arrays");
+  __shared__ int pre[PER * NT];    // prefix of the runs' lengths
+  __shared__ int lo_of[PER * NT];  // each run's first rank in its block
   __shared__ int2 stage[NT];
   __shared__ int2 lst[FUSE_WAVES][FUSE_CAP];
   __shared__ int wsum[FUSE_WAVES];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int64_t b = blockIdx.y;
-  const int k = blockIdx.x >> 1, nr = (S + FUSE_ROWS - 1) / FUSE_ROWS;
+  const int k = blockIdx.x / FUSE_HALVES, nr = (S + FUSE_ROWS - 1) / FUSE_ROWS;
   // >= S: no row (the wave still keeps the barriers)
-  const int s = k * FUSE_ROWS + (blockIdx.x & 1) * FUSE_WAVES + wave;
+  const int s = k * FUSE_ROWS + (blockIdx.x % FUSE_HALVES) * FUSE_WAVES + wave;
   // Run of block `blk`: ranks [offs[k], offs[k+1]) (the last range ends at the count).
   int c[PER], sum = 0;
   {
@@ -899,7 +906,6 @@ __global__ __launch_bounds__(64 * FUSE_WAVES) void bwd_dh_fused_kernel(
     pre[PER * tid + q] = run;
     run += c[q];
   }
-  if (tid == 0) pre[FUSE_MAX_NVB] = total;
   __syncthreads();
   f32x4 acc[NP];
 #pragma unroll
@@ -986,10 +992,14 @@ static void launch_rows(const T* g, const RT* r, const int32_t* idx, const void*
     hipLaunchKernelGGL((bwd_dw_staged_kernel<T, O, DwPasses<T, NP>::value, RT>), dim3((unsigned)nvb),
                        dim3(64 * DW_WAVES), 0, st, g, r, idx, mask, mdt, H, dW, dbias, (int)B,
                        (int)S, (int)D, (int)V, comp, cnt, offs);
-    hipLaunchKernelGGL((bwd_dh_fused_kernel<T, O, FNP>),
-                       dim3((unsigned)(2 * cdiv(S, FUSE_ROWS)), (unsigned)B), dim3(64 * FUSE_WAVES), 0, st,
-                       W, (const int2*)comp, (const int*)cnt, (const int*)offs, dH, (int)S, (int)D,
-                       nvb);
+    const dim3 hgrid((unsigned)(FUSE_HALVES * cdiv(S, FUSE_ROWS)), (unsigned)B);
+    if (nvb <= 64 * FUSE_WAVES)
+      hipLaunchKernelGGL((bwd_dh_fused_kernel<T, O, FNP, 1>), hgrid, dim3(64 * FUSE_WAVES), 0, st, W,
+                         (const int2*)comp, (const int*)cnt, (const int*)offs, dH, (int)S, (int)D, nvb);
+    else
+      hipLaunchKernelGGL((bwd_dh_fused_kernel<T, O, FNP, FUSE_MAX_NVB / (64 * FUSE_WAVES)>), hgrid,
+                         dim3(64 * FUSE_WAVES), 0, st, W,
+                         (const int2*)comp, (const int*)cnt, (const int*)offs, dH, (int)S, (int)D, nvb);
     return;
   }
   if (dH != nullptr && B * S > 0 && D > 0) {
