@@ -19,9 +19,14 @@
 //                   its vocab ids in ascending order (a stable counting sort).
 //       4. dh:      one wave per (b,s) row sums g' * W[v,:] over its segment,
 //                   gathering several W rows per batch before accumulating.
-//   dW / dbias for B <= 128 (bwd_dw_staged_kernel): a workgroup stages g' and I of all
-//   batch rows for 64 consecutive vocab ids in LDS (coalesced loads), then each wave
-//   gathers the H rows of one id at a time.
+//   dW / dbias for B <= 128 and S <= 65536 (bwd_dw_staged_kernel): a workgroup stages g'
+//   and I of all batch rows for 64 consecutive vocab ids in LDS (coalesced loads), then
+//   each wave gathers the H rows of one id at a time.
+//   The fused path (B <= 128, S <= 1024, V <= 65536; configs 2 and 3) is two launches:
+//   bwd_compact_kernel lists each (b, 64-id block)'s active entries sorted by 16-row
+//   range, and bwd_fused_kernel runs the dH workgroups (one per (b, 8 rows), which
+//   gather the entries of their rows from every block) and the staged dW workgroups
+//   side by side.
 // The only atomics are integer counts in LDS, which are order-independent.
 //
 // Gradients are written as fp32 (what the reference returns) or in the input dtype
@@ -637,71 +642,49 @@ constexpr int FUSE_MAX_NVB = FUSE_V_FAST / 64;         // 64-id blocks the fused
 constexpr int FUSE_MIN_RANGES = 64;     // below this too (too few workgroups)
 constexpr int FUSE_MAX_NR = FUSE_MAX_S / FUSE_ROWS;    // ranges (<= 64: one lane each)
 
-// A workgroup of 16 waves owns 64 consecutive vocab ids. It loads G, reps and I of all
-// batch rows for them (each load instruction reads 64 consecutive elements of one row)
-// and keeps g' (0 = inactive) and I in LDS; then wave w handles ids 4w .. 4w+3
-// together: lanes scan the batch rows, ballots list the active ones, and their H rows
-// are gathered up to U at a time and accumulated, each id in ascending b.
+// The staged dW: a workgroup of NW waves owns NIDS consecutive vocab ids (NIDS / NW per
+// wave). It loads G, reps and I of all batch rows for them (each load instruction reads
+// NIDS consecutive elements of 64 / NIDS rows) and keeps g' (0 = inactive) and I in LDS;
+// then each wave handles its ids: lanes scan the batch rows, ballots list the active
+// ones, and their H rows are gathered up to U at a time and accumulated, each id in
+// ascending b. I is kept as 16 bits: the staged kernels take S <= DW_STAGE_S.
 constexpr int DW_WAVES = 16;
-template <typename T, typename O, int NP, typename RT>
-__global__ __launch_bounds__(64 * DW_WAVES) void bwd_dw_staged_kernel(
-    const T* __restrict__ grad, const RT* __restrict__ reps,
-    const int32_t* __restrict__ idx, const void* __restrict__ mask, int mdt,
-    const T* __restrict__ H, O* __restrict__ dW, O* __restrict__ dbias, int B, int S, int D,
-    int V, int2* __restrict__ comp, int* __restrict__ cnt, int* __restrict__ offs) {
-  constexpr int LD = DW_STAGE_B + 1;  // odd row stride: conflict-free column and row access
-  __shared__ float gl[64 * LD];
-  __shared__ uint16_t sl[64 * LD];
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int v0 = blockIdx.x * 64;
-  // Batch rows b = wave + 16 i, two per batch (their loads in flight together).
-  for (int i0 = 0; wave + i0 * DW_WAVES < B; i0 += 2) {
-    const int bs[2] = {wave + i0 * DW_WAVES, wave + (i0 + 1) * DW_WAVES};
+constexpr int DW_LD = DW_STAGE_B + 1;  // odd row stride: conflict-free column and row access
+constexpr int DW_STAGE_S = 1 << 16;
+
+template <typename T, typename RT, int NIDS, int NW>
+__device__ __forceinline__ void dw_stage(float* gl, uint16_t* sl, const T* __restrict__ grad,
+                                         const RT* __restrict__ reps,
+                                         const int32_t* __restrict__ idx,
+                                         const void* __restrict__ mask, int mdt, int B, int S,
+                                         int V, int v0, int wave, int lane) {
+  constexpr int RPL = 64 / NIDS;  // batch rows per load instruction
+  const int idl = lane % NIDS, rsub = lane / NIDS;
+  // Each wave takes 2 * RPL batch rows at a time, their loads in flight together.
+  for (int b0 = wave * 2 * RPL; b0 < B; b0 += NW * 2 * RPL) {
+    const int bs[2] = {b0 + rsub, b0 + RPL + rsub};
     float g[2];
     int s[2];
-    entries_n<T, RT, 2>(grad, reps, idx, mask, mdt, bs, v0 + lane, B, S, V, g, s);
+    entries_n<T, RT, 2>(grad, reps, idx, mask, mdt, bs, v0 + idl, B, S, V, g, s);
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       if (bs[i] < B) {
-        gl[lane * LD + bs[i]] = g[i];
-        sl[lane * LD + bs[i]] = (uint16_t)s[i];
+        gl[idl * DW_LD + bs[i]] = g[i];
+        sl[idl * DW_LD + bs[i]] = (uint16_t)s[i];
       }
     }
   }
-  __syncthreads();
-  if (comp != nullptr) {
-    // For the fused dH kernel: row b's active entries among these 64 ids, sorted by row
-    // range k = s / FUSE_ROWS and then by v, as (v | s << FUSE_V_BITS, g') at
-    // comp[(b * nvb + block) * 64 + rank]; their number, and the first rank of each range
-    // (offs[(b * nvb + block) * nr + k], lane k). Ranks come from one pass over the
-    // active lanes (a handful per block).
-    const int nvb = gridDim.x, nr = (S + FUSE_ROWS - 1) / FUSE_ROWS;
-    for (int b = wave; b < B; b += DW_WAVES) {
-      const float g = gl[lane * LD + b];  // 0 for inactive entries and ids past V
-      const int sv = (int)sl[lane * LD + b];
-      const bool on = g != 0.0f;
-      const int k = sv / FUSE_ROWS;
-      const uint64_t bal = __ballot(on);  // outside any branch: every lane votes
-      uint64_t act = bal;
-      const int64_t base = (int64_t)b * nvb + blockIdx.x;
-      int rank = 0, first = 0;  // this entry's rank; the first rank of range `lane`
-      while (act) {
-        const int j = __ffsll((unsigned long long)act) - 1;
-        act &= act - 1;
-        const int kj = __builtin_amdgcn_readlane(k, j);
-        rank += (kj < k || (kj == k && j < lane)) ? 1 : 0;
-        first += kj < lane ? 1 : 0;
-      }
-      if (on)
-        comp[base * 64 + rank] = make_int2((v0 + lane) | (sv << FUSE_V_BITS), __float_as_int(g));
-      if (lane < nr) offs[base * nr + lane] = first;
-      if (lane == 0) cnt[base] = __popcll(bal);
-    }
-  }
+}
+
+template <typename T, typename O, int NP, typename RT, int NIDS, int NW>
+__device__ __forceinline__ void dw_gather(const float* gl, const uint16_t* sl,
+                                          const T* __restrict__ H, O* __restrict__ dW,
+                                          O* __restrict__ dbias, int B, int S, int D, int V,
+                                          int v0, int wave, int lane) {
   // IDC of the wave's ids at a time are gathered together: batches of U rows are taken
   // from their active (id, b) pairs in (id, b) order, so each id still sums its rows in
   // ascending b.
-  constexpr int IDS = 64 / DW_WAVES;
+  constexpr int IDS = NIDS / NW;  // ids per wave
   constexpr int IDC = DwBatch<T, NP>::IDC;
   constexpr int U = DwBatch<T, NP>::U;
   static_assert(IDS % IDC == 0, "ids per wave");
@@ -727,8 +710,8 @@ __global__ __launch_bounds__(64 * DW_WAVES) void bwd_dw_staged_kernel(
         for (int i = 0; i < IDC; ++i) {
           const int vl = wave * IDS + i0 + i;
           const bool in = bb < B && v0 + vl < V;
-          g[i] = in ? gl[vl * LD + bb] : 0.0f;
-          s[i] = in ? (int)sl[vl * LD + bb] : 0;
+          g[i] = in ? gl[vl * DW_LD + bb] : 0.0f;
+          s[i] = in ? (int)sl[vl * DW_LD + bb] : 0;
           pend[i] = __ballot(g[i] != 0.0f);
           left += __popcll(pend[i]);
         }
@@ -798,6 +781,62 @@ __global__ __launch_bounds__(64 * DW_WAVES) void bwd_dw_staged_kernel(
   }
 }
 
+// dW / dbias for B <= DW_STAGE_B and S <= DW_STAGE_S (the five-kernel path's).
+template <typename T, typename O, int NP, typename RT>
+__global__ __launch_bounds__(64 * DW_WAVES) void bwd_dw_staged_kernel(
+    const T* __restrict__ grad, const RT* __restrict__ reps,
+    const int32_t* __restrict__ idx, const void* __restrict__ mask, int mdt,
+    const T* __restrict__ H, O* __restrict__ dW, O* __restrict__ dbias, int B, int S, int D,
+    int V) {
+  __shared__ float gl[64 * DW_LD];
+  __shared__ uint16_t sl[64 * DW_LD];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int v0 = blockIdx.x * 64;
+  dw_stage<T, RT, 64, DW_WAVES>(gl, sl, grad, reps, idx, mask, mdt, B, S, V, v0, wave, lane);
+  __syncthreads();
+  dw_gather<T, O, NP, RT, 64, DW_WAVES>(gl, sl, H, dW, dbias, B, S, D, V, v0, wave, lane);
+}
+
+// The fused path's compaction, for the dH workgroups: for batch row b and 64-id block
+// blk, the active entries sorted by row range k = s / FUSE_ROWS and then by v, as
+// (v | s << FUSE_V_BITS, g') at comp[(b * nvb + blk) * 64 + rank]; their number
+// cnt[b * nvb + blk], and the first rank of each range (offs[(b * nvb + blk) * nr + k],
+// lane k). Ranks come from one pass over the active lanes (a handful per block). One
+// wave per (block, two batch rows b, b + 4).
+template <typename T, typename RT>
+__global__ __launch_bounds__(256) void bwd_compact_kernel(
+    const T* __restrict__ grad, const RT* __restrict__ reps, const int32_t* __restrict__ idx,
+    const void* __restrict__ mask, int mdt, int B, int S, int V, int2* __restrict__ comp,
+    int* __restrict__ cnt, int* __restrict__ offs) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int nvb = gridDim.x, blk = blockIdx.x, v0 = blk * 64;
+  const int nr = (S + FUSE_ROWS - 1) / FUSE_ROWS;
+  const int bs[2] = {(int)blockIdx.y * 8 + wave, (int)blockIdx.y * 8 + 4 + wave};
+  float g[2];
+  int sv[2];
+  entries_n<T, RT, 2>(grad, reps, idx, mask, mdt, bs, v0 + lane, B, S, V, g, sv);
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    if (bs[i] >= B) break;  // wave-uniform
+    const bool on = g[i] != 0.0f;
+    const int k = sv[i] / FUSE_ROWS;
+    const uint64_t bal = __ballot(on);
+    uint64_t act = bal;
+    const int64_t base = (int64_t)bs[i] * nvb + blk;
+    int rank = 0, first = 0;  // this entry's rank; the first rank of range `lane`
+    while (act) {
+      const int j = __ffsll((unsigned long long)act) - 1;
+      act &= act - 1;
+      const int kj = __builtin_amdgcn_readlane(k, j);
+      rank += (kj < k || (kj == k && j < lane)) ? 1 : 0;
+      first += kj < lane ? 1 : 0;
+    }
+    if (on) comp[base * 64 + rank] = make_int2((v0 + lane) | (sv[i] << FUSE_V_BITS), __float_as_int(g[i]));
+    if (lane < nr) offs[base * nr + lane] = first;
+    if (lane == 0) cnt[base] = __popcll(bal);
+  }
+}
+
 // ---- 4b. dH from the staged dW kernel's compacted entries (the fused path) -------------
 // FUSE_HALVES workgroups per (b, range of FUSE_ROWS consecutive rows); wave w of
 // workgroup h owns row s = FUSE_ROWS * range + FUSE_WAVES * h + w. Each 64-id block of row b lists its active
@@ -851,22 +890,34 @@ __device__ __forceinline__ void gather_rows(const T* __restrict__ W, const int2*
 }
 
 // PER: 64-id blocks per thread in the prefix (nvb <= PER * 64 * FUSE_WAVES).
-template <typename T, typename O, int NP, int PER>
-__global__ __launch_bounds__(64 * FUSE_WAVES) void bwd_dh_fused_kernel(
-    const T* __restrict__ W, const int2* __restrict__ comp, const int* __restrict__ cnt,
-    const int* __restrict__ offs, O* __restrict__ dH, int S, int D, int nvb) {
-  constexpr int NT = 64 * FUSE_WAVES;
+template <int PER>
+struct DhSmem {
+  static constexpr int NT = 64 * FUSE_WAVES;
   static_assert(PER * NT <= FUSE_MAX_NVB, "prefix arrays");
-  __shared__ int pre[PER * NT];    // prefix of the runs' lengths
-  __shared__ int lo_of[PER * NT];  // each run's first rank in its block
-  __shared__ int2 stage[NT];
-  __shared__ int2 lst[FUSE_WAVES][FUSE_CAP];
-  __shared__ int wsum[FUSE_WAVES];
+  int pre[PER * NT];    // prefix of the runs' lengths
+  int lo_of[PER * NT];  // each run's first rank in its block
+  int2 stage[NT];
+  int2 lst[FUSE_WAVES][FUSE_CAP];
+  int wsum[FUSE_WAVES];
+};
+
+// The workgroup for batch row b and xb = FUSE_HALVES * range + half.
+template <typename T, typename O, int NP, int PER>
+__device__ __forceinline__ void dh_fused_body(DhSmem<PER>& sm, const T* __restrict__ W,
+                                              const int2* __restrict__ comp,
+                                              const int* __restrict__ cnt,
+                                              const int* __restrict__ offs, O* __restrict__ dH,
+                                              int S, int D, int nvb, int64_t b, int xb) {
+  constexpr int NT = DhSmem<PER>::NT;
+  int* pre = sm.pre;
+  int* lo_of = sm.lo_of;
+  int2* stage = sm.stage;
+  int* wsum = sm.wsum;
+  auto& lst = sm.lst;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int64_t b = blockIdx.y;
-  const int k = blockIdx.x / FUSE_HALVES, nr = (S + FUSE_ROWS - 1) / FUSE_ROWS;
+  const int k = xb / FUSE_HALVES, nr = (S + FUSE_ROWS - 1) / FUSE_ROWS;
   // >= S: no row (the wave still keeps the barriers)
-  const int s = k * FUSE_ROWS + (blockIdx.x % FUSE_HALVES) * FUSE_WAVES + wave;
+  const int s = k * FUSE_ROWS + (xb % FUSE_HALVES) * FUSE_WAVES + wave;
   // Run of block `blk`: ranks [offs[k], offs[k+1]) (the last range ends at the count).
   int c[PER], sum = 0;
   {
@@ -949,6 +1000,42 @@ __global__ __launch_bounds__(64 * FUSE_WAVES) void bwd_dh_fused_kernel(
   }
 }
 
+// The fused path after the compaction: the dH workgroups (the first n_dh_x * B; the
+// long rows start first) and the staged dW workgroups (FUSE_DW_IDS ids each) in one
+// launch. The two read only the compaction and the inputs, so the dW work fills the
+// CUs while the dH workgroups with long rows finish.
+constexpr int FUSE_DW_IDS = 4 * FUSE_WAVES;
+template <typename T, typename O, int NP, typename RT, int PER>
+__global__ __launch_bounds__(64 * FUSE_WAVES) void bwd_fused_kernel(
+    const T* __restrict__ grad, const RT* __restrict__ reps, const int32_t* __restrict__ idx,
+    const void* __restrict__ mask, int mdt, const T* __restrict__ H, const T* __restrict__ W,
+    const int2* __restrict__ comp, const int* __restrict__ cnt, const int* __restrict__ offs,
+    O* __restrict__ dH, O* __restrict__ dW, O* __restrict__ dbias, int B, int S, int D, int V,
+    int nvb, int n_dh_x) {
+  struct DwSmem {
+    float gl[FUSE_DW_IDS * DW_LD];
+    uint16_t sl[FUSE_DW_IDS * DW_LD];
+  };
+  union Smem {
+    DhSmem<PER> h;
+    DwSmem w;
+  };
+  __shared__ Smem sm;
+  const int n_dh = n_dh_x * B;
+  if ((int)blockIdx.x < n_dh) {  // workgroup-uniform
+    dh_fused_body<T, O, NP, PER>(sm.h, W, comp, cnt, offs, dH, S, D, nvb, blockIdx.x / n_dh_x,
+                                 blockIdx.x % n_dh_x);
+  } else {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int v0 = ((int)blockIdx.x - n_dh) * FUSE_DW_IDS;
+    dw_stage<T, RT, FUSE_DW_IDS, FUSE_WAVES>(sm.w.gl, sm.w.sl, grad, reps, idx, mask, mdt, B, S,
+                                             V, v0, wave, lane);
+    __syncthreads();
+    dw_gather<T, O, NP, RT, FUSE_DW_IDS, FUSE_WAVES>(sm.w.gl, sm.w.sl, H, dW, dbias, B, S, D, V,
+                                                     v0, wave, lane);
+  }
+}
+
 // Register passes for a row of D elements (4 per lane, 256 per pass), capped at MAX_NP
 // (longer rows loop over D in chunks of MAX_NP * 256).
 static int passes_for(int64_t D) {
@@ -989,17 +1076,17 @@ static void launch_rows(const T* g, const RT* r, const int32_t* idx, const void*
     int* cnt = (int*)((char*)ws + L.cnt64);
     int* offs = (int*)((char*)ws + L.off64);
     const int nvb = (int)cdiv(V, 64);
-    hipLaunchKernelGGL((bwd_dw_staged_kernel<T, O, DwPasses<T, NP>::value, RT>), dim3((unsigned)nvb),
-                       dim3(64 * DW_WAVES), 0, st, g, r, idx, mask, mdt, H, dW, dbias, (int)B,
-                       (int)S, (int)D, (int)V, comp, cnt, offs);
-    const dim3 hgrid((unsigned)(FUSE_HALVES * cdiv(S, FUSE_ROWS)), (unsigned)B);
-    if (nvb <= 64 * FUSE_WAVES)
-      hipLaunchKernelGGL((bwd_dh_fused_kernel<T, O, FNP, 1>), hgrid, dim3(64 * FUSE_WAVES), 0, st, W,
-                         (const int2*)comp, (const int*)cnt, (const int*)offs, dH, (int)S, (int)D, nvb);
-    else
-      hipLaunchKernelGGL((bwd_dh_fused_kernel<T, O, FNP, FUSE_MAX_NVB / (64 * FUSE_WAVES)>), hgrid,
-                         dim3(64 * FUSE_WAVES), 0, st, W,
-                         (const int2*)comp, (const int*)cnt, (const int*)offs, dH, (int)S, (int)D, nvb);
+    hipLaunchKernelGGL((bwd_compact_kernel<T, RT>), dim3((unsigned)nvb, (unsigned)cdiv(B, 8)), dim3(256),
+                       0, st, g, r, idx, mask, mdt, (int)B, (int)S, (int)V, comp, cnt, offs);
+    const int n_dh_x = (int)(FUSE_HALVES * cdiv(S, FUSE_ROWS));
+    const dim3 grid((unsigned)(n_dh_x * B + cdiv(V, FUSE_DW_IDS)));
+#define FUSED(PER)                                                                                  \
+  hipLaunchKernelGGL((bwd_fused_kernel<T, O, FNP, RT, PER>), grid, dim3(64 * FUSE_WAVES), 0, st, g,  \
+                     r, idx, mask, mdt, H, W, (const int2*)comp, (const int*)cnt, (const int*)offs, \
+                     dH, dW, dbias, (int)B, (int)S, (int)D, (int)V, nvb, n_dh_x)
+    if (nvb <= 64 * FUSE_WAVES) FUSED(1);
+    else FUSED(FUSE_MAX_NVB / (64 * FUSE_WAVES));
+#undef FUSED
     return;
   }
   if (dH != nullptr && B * S > 0 && D > 0) {
@@ -1060,11 +1147,10 @@ static void launch_rows(const T* g, const RT* r, const int32_t* idx, const void*
     }
   }
   if ((dW != nullptr || dbias != nullptr) && V > 0) {
-    if (B <= DW_STAGE_B)
+    if (B <= DW_STAGE_B && S <= DW_STAGE_S)
       hipLaunchKernelGGL((bwd_dw_staged_kernel<T, O, DwPasses<T, NP>::value, RT>),
                          dim3((unsigned)cdiv(V, 64)), dim3(64 * DW_WAVES), 0,
-                         st, g, r, idx, mask, mdt, H, dW, dbias, (int)B, (int)S, (int)D, (int)V,
-                         (int2*)nullptr, (int*)nullptr, (int*)nullptr);
+                         st, g, r, idx, mask, mdt, H, dW, dbias, (int)B, (int)S, (int)D, (int)V);
     else
       hipLaunchKernelGGL((bwd_dw_kernel<T, O, NP, RT>), dim3((unsigned)cdiv(V, 4)), dim3(256), 0, st,
                          g, r, idx, mask, mdt, H, dW, dbias, (int)B, (int)S, (int)D, (int)V);

@@ -566,6 +566,7 @@ def test_backward_few_rows_split(case, device):
     ("fp16", 20, 20000, 32, 64, True, "gaps"),      # 25000 groups: the three-kernel plan
     ("bf16", 9000, 3, 32, 64, True, "int64"),       # B > 8192: two dH batch chunks
     ("bf16", 33000, 1, 8, 16, True, "holes"),       # B > 32768: two forward launches
+    ("bf16", 1, 70000, 16, 64, True, "int64"),      # S > 65536: dW without the 16-bit staging
 ], ids=lambda c: "-".join(map(str, c)))
 def test_long_sequences_and_many_rows(case, device):
     """Shapes past one pass of the kernels: the forward takes any S (and splits B over
