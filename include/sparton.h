@@ -231,6 +231,19 @@ int sparton_loss_bwd(const void* q, const void* d, const float* probs, const flo
                      void* grad_q, void* grad_d, int dtype, void* stream);
 
 /*
+ * The same backward with the six upstream gradients given separately: grad_terms is a host
+ * array of six device pointers to fp32 scalars, in sparton_loss_fwd's output order, each
+ * possibly NULL for a zero gradient. It serves callers that hand the six terms out as
+ * separate tensors (a training loop that backpropagates `total` alone passes one pointer)
+ * and so never have to assemble a six-element gradient. No counterpart in the reference,
+ * whose loss is plain torch (training/train.py:178-197).
+ */
+int sparton_loss_bwd_terms(const void* q, const void* d, const float* probs,
+                           const float* const* grad_terms, int64_t Bq, int64_t Bd, int64_t V,
+                           float w_ce, float w_l1, float w_flops, void* grad_q, void* grad_d,
+                           int dtype, void* stream);
+
+/*
  * Measurement probe, no counterpart in the reference: `grid` workgroups (one per CU) of 4
  * waves each run `iters` rounds of 16 independent v_mfma_f32_32x32x16_{bf16,f16} on random
  * register operands (dtype SPARTON_BF16 or SPARTON_F16). clk[2*w] receives workgroup w's

@@ -15,7 +15,7 @@ import torch  # noqa: F401  (must be imported first: see module docstring)
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 DEFAULT_LIB = os.path.join(_HERE, "libsparton_hip.so")
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 # enum sparton_dtype / sparton_mask_dtype (include/sparton.h)
 DTYPE_CODE = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
@@ -44,6 +44,7 @@ EXPORTED_SYMBOLS = (
     "sparton_transform_chunk_sum",
     "sparton_loss_fwd",
     "sparton_loss_bwd",
+    "sparton_loss_bwd_terms",
     "sparton_loss_workspace_bytes",
     "sparton_mfma_probe",
     "sparton_strerror",
@@ -117,6 +118,10 @@ def load() -> ctypes.CDLL:
         L.sparton_loss_bwd.argtypes = [_vp, _vp, _vp, _vp, _i64, _i64, _i64, ctypes.c_float,
                                        ctypes.c_float, ctypes.c_float, _vp, _vp, ctypes.c_int, _vp]
         L.sparton_loss_bwd.restype = ctypes.c_int
+        L.sparton_loss_bwd_terms.argtypes = [_vp, _vp, _vp, ctypes.POINTER(_vp), _i64, _i64, _i64,
+                                             ctypes.c_float, ctypes.c_float, ctypes.c_float, _vp, _vp,
+                                             ctypes.c_int, _vp]
+        L.sparton_loss_bwd_terms.restype = ctypes.c_int
         L.sparton_mfma_probe.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, _vp, _vp, _vp]
         L.sparton_mfma_probe.restype = ctypes.c_int
         L.sparton_strerror.argtypes = [ctypes.c_int]

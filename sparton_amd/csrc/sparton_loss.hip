@@ -223,12 +223,20 @@ __global__ __launch_bounds__(NT) void loss_final_kernel(const float* __restrict_
   }
 }
 
+// The upstream gradients of the six outputs: each a device fp32 scalar, or NULL for 0.
+struct Grads6 {
+  const float* p[6];
+};
+__device__ __forceinline__ float grad_of(const Grads6& g, int k) {
+  return g.p[k] != nullptr ? *g.p[k] : 0.0f;
+}
+
 // One workgroup per slice: stages Q, R and P, the slice's column sums, then 4x4 tiles of
 // dQ (rows i0..i0+3 x 4 columns) and dR (rows j0..j0+3 x 4 columns), each thread a tile.
 template <typename T, int MB>
 __global__ __launch_bounds__(NT) void loss_bwd_kernel(const T* __restrict__ Q, const T* __restrict__ R,
                                                       const float* __restrict__ P,
-                                                      const float* __restrict__ g, int Bq, int Bd,
+                                                      const Grads6 g, int Bq, int Bd,
                                                       int V, float w_ce, float w_l1, float w_fl,
                                                       T* __restrict__ GQ, T* __restrict__ GR) {
   constexpr int PLD = MB + 4;
@@ -264,12 +272,12 @@ __global__ __launch_bounds__(NT) void loss_bwd_kernel(const T* __restrict__ Q, c
     colsum[wave][lane] = cs;
   }
   __syncthreads();
-  const float g0 = g[0];
-  const float c_ce = g0 * w_ce + g[1];
-  const float c_sq = (g0 * w_l1 + g[2]) / (float)Bq;
-  const float c_sd = Bd > 0 ? (g0 * w_l1 + g[3]) / (float)Bd : 0.0f;
-  const float c_fq = 2.0f * (g0 * w_fl + g[4]) / (float)V;
-  const float c_fd = 2.0f * (g0 * w_fl + g[5]) / (float)V;
+  const float g0 = grad_of(g, 0);
+  const float c_ce = g0 * w_ce + grad_of(g, 1);
+  const float c_sq = (g0 * w_l1 + grad_of(g, 2)) / (float)Bq;
+  const float c_sd = Bd > 0 ? (g0 * w_l1 + grad_of(g, 3)) / (float)Bd : 0.0f;
+  const float c_fq = 2.0f * (g0 * w_fl + grad_of(g, 4)) / (float)V;
+  const float c_fd = 2.0f * (g0 * w_fl + grad_of(g, 5)) / (float)V;
   const int nbi = Bqp / 4, nbj = Bdp / 4;
   constexpr int CT = SLICE / 4;  // column tiles per slice
   for (int t = threadIdx.x; t < (nbi + nbj) * CT; t += NT) {
@@ -338,7 +346,7 @@ static void launch_fwd(const void* q, const void* d, int Bq, int Bd, int V, floa
                        (const T*)d, Bq, Bd, V, part, K);
 }
 template <typename T, int MB>
-static void launch_bwd(const void* q, const void* d, const float* P, const float* g, int Bq, int Bd,
+static void launch_bwd(const void* q, const void* d, const float* P, const Grads6& g, int Bq, int Bd,
                        int V, float w_ce, float w_l1, float w_fl, void* gq, void* gd, hipStream_t st) {
   hipLaunchKernelGGL((loss_bwd_kernel<T, MB>), dim3((unsigned)slices(V)), dim3(NT), 0, st,
                      (const T*)q, (const T*)d, P, g, Bq, Bd, V, w_ce, w_l1, w_fl, (T*)gq, (T*)gd);
@@ -353,7 +361,7 @@ static void fwd_partial(const void* q, const void* d, int Bq, int Bd, int V, flo
   else launch_fwd<T, 128>(q, d, Bq, Bd, V, part, K, st);
 }
 template <typename T>
-static void bwd_all(const void* q, const void* d, const float* P, const float* g, int Bq, int Bd,
+static void bwd_all(const void* q, const void* d, const float* P, const Grads6& g, int Bq, int Bd,
                     int V, float w_ce, float w_l1, float w_fl, void* gq, void* gd, hipStream_t st) {
   const int mb = Bq > Bd ? Bq : Bd;
   if (mb <= 32) launch_bwd<T, 32>(q, d, P, g, Bq, Bd, V, w_ce, w_l1, w_fl, gq, gd, st);
@@ -411,13 +419,12 @@ extern "C" __attribute__((visibility("default"))) int sparton_loss_fwd(
   return e == hipSuccess ? SPARTON_OK : (int)e;
 }
 
-extern "C" __attribute__((visibility("default"))) int sparton_loss_bwd(
-    const void* q, const void* d, const float* probs, const float* grad_out, int64_t Bq, int64_t Bd,
-    int64_t V, float w_ce, float w_l1, float w_flops, void* grad_q, void* grad_d, int dtype,
-    void* stream) {
+static int loss_bwd_run(const void* q, const void* d, const float* probs, const loss::Grads6& grad_out,
+                        int64_t Bq, int64_t Bd, int64_t V, float w_ce, float w_l1, float w_flops,
+                        void* grad_q, void* grad_d, int dtype, void* stream) {
   const int rc = loss_check(Bq, Bd, V, dtype);
   if (rc != SPARTON_OK) return rc;
-  if (q == nullptr || grad_out == nullptr || grad_q == nullptr ||
+  if (q == nullptr || grad_q == nullptr ||
       (Bd > 0 && (d == nullptr || probs == nullptr || grad_d == nullptr)))
     return SPARTON_EINVAL;
   hipStream_t st = (hipStream_t)stream;
@@ -437,4 +444,23 @@ extern "C" __attribute__((visibility("default"))) int sparton_loss_bwd(
   }
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? SPARTON_OK : (int)e;
+}
+
+extern "C" __attribute__((visibility("default"))) int sparton_loss_bwd(
+    const void* q, const void* d, const float* probs, const float* grad_out, int64_t Bq, int64_t Bd,
+    int64_t V, float w_ce, float w_l1, float w_flops, void* grad_q, void* grad_d, int dtype,
+    void* stream) {
+  if (grad_out == nullptr) return SPARTON_EINVAL;
+  const loss::Grads6 g{{grad_out, grad_out + 1, grad_out + 2, grad_out + 3, grad_out + 4, grad_out + 5}};
+  return loss_bwd_run(q, d, probs, g, Bq, Bd, V, w_ce, w_l1, w_flops, grad_q, grad_d, dtype, stream);
+}
+
+extern "C" __attribute__((visibility("default"))) int sparton_loss_bwd_terms(
+    const void* q, const void* d, const float* probs, const float* const* grad_terms, int64_t Bq,
+    int64_t Bd, int64_t V, float w_ce, float w_l1, float w_flops, void* grad_q, void* grad_d,
+    int dtype, void* stream) {
+  if (grad_terms == nullptr) return SPARTON_EINVAL;
+  loss::Grads6 g;
+  for (int k = 0; k < 6; ++k) g.p[k] = grad_terms[k];
+  return loss_bwd_run(q, d, probs, g, Bq, Bd, V, w_ce, w_l1, w_flops, grad_q, grad_d, dtype, stream);
 }

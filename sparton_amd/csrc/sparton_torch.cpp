@@ -340,9 +340,19 @@ std::tuple<Tensor, Tensor> loss_fwd(const Tensor& q, const Tensor& d, double T, 
   return {out, probs};
 }
 
+// The six terms (total, CE, L1(q), L1(d), FL(q), FL(d)) as separate scalars (views of the
+// kernel's one output buffer), so that a caller backpropagating some of them (usually
+// `total`) hands the backward only those gradients: the others stay undefined (no
+// materialised zeros, no stack of six) and reach the kernel as NULL pointers.
+using Loss6 = std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor, Tensor>;
+Loss6 split6(const Tensor& out) {
+  return {out.select(0, 0), out.select(0, 1), out.select(0, 2), out.select(0, 3), out.select(0, 4),
+          out.select(0, 5)};
+}
+
 struct LossFn : public torch::autograd::Function<LossFn> {
-  static Tensor forward(AutogradContext* ctx, const Tensor& q_in, const Tensor& d_in, bool has_d,
-                        double T, double w_ce, double w_l1, double w_flops) {
+  static variable_list forward(AutogradContext* ctx, const Tensor& q_in, const Tensor& d_in, bool has_d,
+                               double T, double w_ce, double w_l1, double w_flops) {
     at::AutoDispatchBelowADInplaceOrView below;
     c10::OptionalDeviceGuard guard(q_in.device());
     Tensor q = q_in.contiguous(), d = has_d ? d_in.contiguous() : Tensor();
@@ -351,37 +361,50 @@ struct LossFn : public torch::autograd::Function<LossFn> {
     ctx->saved_data["w_ce"] = w_ce;
     ctx->saved_data["w_l1"] = w_l1;
     ctx->saved_data["w_flops"] = w_flops;
-    return out;
+    ctx->set_materialize_grads(false);
+    auto t = split6(out);
+    return {std::get<0>(t), std::get<1>(t), std::get<2>(t), std::get<3>(t), std::get<4>(t), std::get<5>(t)};
   }
   static variable_list backward(AutogradContext* ctx, variable_list grads) {
-    if (!grads[0].defined()) return variable_list(7);
+    const float* gp[6];
+    std::vector<Tensor> keep;
+    bool any = false;
+    for (int k = 0; k < 6; ++k) {
+      gp[k] = nullptr;
+      if (grads[k].defined()) {
+        keep.push_back(grads[k].to(at::kFloat).contiguous());
+        gp[k] = keep.back().data_ptr<float>();
+        any = true;
+      }
+    }
+    if (!any) return variable_list(7);
     auto s = ctx->get_saved_variables();
     const Tensor &q = s[0], &d = s[1], &probs = s[2];
     c10::OptionalDeviceGuard guard(q.device());
     const int64_t Bq = q.size(0), V = q.size(1), Bd = d.defined() ? d.size(0) : 0;
-    Tensor g = grads[0].to(at::kFloat).contiguous();
     Tensor dq = at::empty_like(q);
     Tensor dd = d.defined() ? at::empty_like(d) : Tensor();
-    check(sparton_loss_bwd(q.data_ptr(), ptr(d), Bd ? probs.data_ptr<float>() : nullptr, g.data_ptr<float>(),
-                           Bq, Bd, V, (float)ctx->saved_data["w_ce"].toDouble(),
-                           (float)ctx->saved_data["w_l1"].toDouble(),
-                           (float)ctx->saved_data["w_flops"].toDouble(), dq.data_ptr(), mptr(dd),
-                           dtype_code(q.scalar_type()), stream_of(q)),
-          "sparton_loss_bwd");
+    check(sparton_loss_bwd_terms(q.data_ptr(), ptr(d), Bd ? probs.data_ptr<float>() : nullptr, gp, Bq, Bd,
+                                 V, (float)ctx->saved_data["w_ce"].toDouble(),
+                                 (float)ctx->saved_data["w_l1"].toDouble(),
+                                 (float)ctx->saved_data["w_flops"].toDouble(), dq.data_ptr(), mptr(dd),
+                                 dtype_code(q.scalar_type()), stream_of(q)),
+          "sparton_loss_bwd_terms");
     return {dq, dd, Tensor(), Tensor(), Tensor(), Tensor(), Tensor()};
   }
 };
 
-Tensor loss_autograd(const Tensor& q, const c10::optional<Tensor>& d, double T, double w_ce, double w_l1,
-                     double w_flops) {
-  return LossFn::apply(q, present(d, q), d.has_value(), T, w_ce, w_l1, w_flops);
+Loss6 loss_autograd(const Tensor& q, const c10::optional<Tensor>& d, double T, double w_ce, double w_l1,
+                    double w_flops) {
+  auto o = LossFn::apply(q, present(d, q), d.has_value(), T, w_ce, w_l1, w_flops);
+  return {o[0], o[1], o[2], o[3], o[4], o[5]};
 }
 
-Tensor loss_cuda(const Tensor& q, const c10::optional<Tensor>& d, double T, double w_ce, double w_l1,
-                 double w_flops) {
+Loss6 loss_cuda(const Tensor& q, const c10::optional<Tensor>& d, double T, double w_ce, double w_l1,
+                double w_flops) {
   c10::OptionalDeviceGuard guard(q.device());
   Tensor dd = d.has_value() ? d->contiguous() : Tensor();
-  return std::get<0>(loss_fwd(q.contiguous(), dd, T, w_ce, w_l1, w_flops));
+  return split6(std::get<0>(loss_fwd(q.contiguous(), dd, T, w_ce, w_l1, w_flops)));
 }
 
 // CPU tensors: the same refusal as the reference's `assert hidden.is_cuda`
@@ -400,7 +423,7 @@ TORCH_LIBRARY(sparton_eager, m) {
   m.def("mlm_transform(Tensor x, Tensor weight, Tensor dense_bias, Tensor ln_weight, "
         "Tensor ln_bias, float eps) -> Tensor");
   m.def("splade_loss(Tensor q, Tensor? d, float temperature, float w_ce, float w_l1, "
-        "float w_flops) -> Tensor");
+        "float w_flops) -> (Tensor, Tensor, Tensor, Tensor, Tensor, Tensor)");
 }
 
 TORCH_LIBRARY_IMPL(sparton_eager, CUDA, m) {
@@ -431,5 +454,5 @@ TORCH_LIBRARY_IMPL(sparton_eager, CPU, m) {
   m.impl("mlm_transform", [](const Tensor&, const Tensor&, const Tensor&, const Tensor&, const Tensor&,
                              double) -> Tensor { cpu_refused("sparton_eager::mlm_transform"); });
   m.impl("splade_loss", [](const Tensor&, const c10::optional<Tensor>&, double, double, double,
-                           double) -> Tensor { cpu_refused("sparton_eager::splade_loss"); });
+                           double) -> Loss6 { cpu_refused("sparton_eager::splade_loss"); });
 }

@@ -154,11 +154,14 @@ splade_loss_fwd.register_autograd(_backward, setup_context=_setup_context)
 
 
 def _run(q: Tensor, d: Optional[Tensor], temperature: float, w_ce: float, w_l1: float,
-         w_flops: float) -> Tensor:
+         w_flops: float) -> Tuple[Tensor, ...]:
+    """The six terms (total, CE, L1(q), L1(d), FL(q), FL(d)) as separate scalars."""
     if torch.compiler.is_compiling() or not q.is_cuda:
         out, _ = torch.ops.sparton.splade_loss_fwd(q, d, temperature, w_ce, w_l1, w_flops)
-        return out
-    # eager: the C++ op (autograd in C++), the same implementation as the custom ops
+        return out.unbind(0)
+    # eager: the C++ op (autograd in C++), the same implementation as the custom ops; its six
+    # outputs are separate, so backpropagating one term materialises no gradients of the
+    # others
     _check(q, d, "splade_loss")
     if d is not None and not temperature > 0.0:
         raise ValueError(f"splade_loss: temperature must be > 0, got {temperature}")
@@ -169,8 +172,7 @@ def splade_loss(query_reps: Tensor, doc_reps: Optional[Tensor], temperature: flo
                 lambda_l1: float = 0.0, lambda_flops: float = 0.0) -> SpladeLossOutput:
     """InfoNCE + weighted L1 and FLOPS regularisers of both sides in one fused pass
     (train.py:178-197 with the weights already warmed up, see get_reg_weight)."""
-    out = _run(query_reps, doc_reps, temperature, 1.0, lambda_l1, lambda_flops)
-    return SpladeLossOutput(*out.unbind(0))
+    return SpladeLossOutput(*_run(query_reps, doc_reps, temperature, 1.0, lambda_l1, lambda_flops))
 
 
 def info_nce_loss(query_reps: Tensor, doc_reps: Tensor, temperature: float = 1.0) -> Tensor:

@@ -317,6 +317,23 @@ def test_loss_bwd_argument_validation(kw, code):
     assert loss_bwd(**kw) == code
 
 
+def loss_bwd_terms(**kw):
+    import ctypes
+    terms = (ctypes.c_void_p * 6)(P, None, None, None, None, None)
+    a = dict(q=P, d=P, probs=P, terms=terms, Bq=4, Bd=8, V=100, w_ce=1.0, w_l1=0.0, w_fl=0.0, gq=P,
+             gd=P, dtype=1, stream=None)
+    a.update(kw)
+    return _lib.load().sparton_loss_bwd_terms(*a.values())
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(terms=None), -1), (dict(Bq=0), -1), (dict(gq=None), -1), (dict(gd=None), -1),
+    (dict(probs=None), -1), (dict(Bq=9), -1), (dict(Bd=129), -3), (dict(dtype=-1), -1),
+])
+def test_loss_bwd_terms_argument_validation(kw, code):
+    assert loss_bwd_terms(**kw) == code
+
+
 def test_loss_workspace_size():
     L = _lib.load()
     # fp32 partials per 64-column slice plus their sums: Bq*Bd scores, Bq + Bd row sums of

@@ -130,6 +130,33 @@ def test_loss_deterministic_and_modes_agree(device):
     assert torch.equal(out.detach(), runs[0][0]) and torch.equal(qs.grad, runs[0][1])
 
 
+@pytest.mark.parametrize("dt,Bq,Bd,V", [("bf16", 32, 32, 30522), ("fp32", 5, 9, 333), ("fp16", 3, 0, 100)])
+def test_loss_terms_backward_equals_six_vector_backward(dt, Bq, Bd, V, device):
+    """The eager op returns the six terms as separate tensors and passes the backward only
+    the gradients of the terms used (NULL for the others); the custom op returns one
+    six-vector whose gradient autograd assembles. Any combination of terms must give the
+    same gradients, bitwise."""
+    say(f"loss terms backward {dt} {Bq}x{Bd}x{V}")
+    q = reps_like(Bq, V, dt, seed=11).to(device)
+    d = reps_like(Bd, V, dt, seed=12).to(device) if Bd else None
+    wts = [1.0, 0.5, 0.0, 2.0, 1.0, 0.0] if Bd else [1.0, 0.0, 0.25, 0.0, 3.0, 0.0]
+    grads = []
+    for path in ("terms", "vector"):
+        qs = q.clone().requires_grad_()
+        ds = d.clone().requires_grad_() if Bd else None
+        if path == "terms":
+            res = list(sl.splade_loss(qs, ds, 0.7, 0.1, 0.2))
+        else:
+            out, _ = torch.ops.sparton.splade_loss_fwd(qs, ds, 0.7, 1.0, 0.1, 0.2)
+            res = list(out.unbind(0))
+        sum(w * t for w, t in zip(wts, res) if w != 0.0).backward()
+        grads.append((qs.grad.clone(), ds.grad.clone() if Bd else None))
+    torch.cuda.synchronize()
+    assert torch.equal(grads[0][0], grads[1][0])
+    if Bd:
+        assert torch.equal(grads[0][1], grads[1][1])
+
+
 def test_head_then_loss_trains(device):
     """SpartonHead reps of queries and documents -> splade_training_loss -> backward."""
     torch.manual_seed(0)
