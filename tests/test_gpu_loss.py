@@ -81,6 +81,35 @@ def test_loss_matches_oracle(dt, Bq, Bd, V, T, w_l1, w_fl, device):
     say(f"  total {out[0].item():.6f} (oracle {want[0]:.6f})")
 
 
+@pytest.mark.parametrize("dt,Bq,Bd,V", [("fp32", 200, 200, 700), ("bf16", 150, 300, 2000),
+                                         ("fp16", 129, 0, 500)])
+def test_loss_large_batches_match_oracle(dt, Bq, Bd, V, device):
+    """More than 128 rows: splade_loss and the single-term functions take the batch through
+    torch's GPU operations in fp32 (train.py's formulas). Values and gradients against the
+    float64 oracle, weighting the six terms as the kernel test does."""
+    say(f"loss large batch {dt} Bq={Bq} Bd={Bd} V={V}")
+    T, w_l1, w_fl = 0.5, 1e-2, 1e-3
+    q = reps_like(Bq, V, dt, seed=Bq + V)
+    d = reps_like(Bd, V, dt, seed=Bd + 2 * V) if Bd else None
+    qd = q.to(device).requires_grad_()
+    dd = d.to(device).requires_grad_() if d is not None else None
+    res = sl.splade_loss(qd, dd, T, w_l1, w_fl)
+    g = [1.0, 0.3, -0.5, 0.25, 2.0, -1.5] if Bd else [1.0, 0.0, -0.5, 0.0, 2.0, 0.0]
+    sum(w * t for w, t in zip(g, res) if w != 0.0).backward()
+    torch.cuda.synchronize()
+    qn = q.double().numpy()
+    dn = d.double().numpy() if d is not None else None
+    want = loss_ref.splade_loss(qn, dn, T, 1.0, w_l1, w_fl)
+    np.testing.assert_allclose(torch.stack(list(res)).detach().double().cpu().numpy(), want, **OUT_TOL)
+    gq, gd = loss_ref.splade_loss_grad(qn, dn, np.array(g), T, 1.0, w_l1, w_fl)
+    assert qd.grad.dtype == q.dtype
+    close_rel(qd.grad, gq, GRAD_TOL[dt], "dq")
+    if d is not None:
+        close_rel(dd.grad, gd, GRAD_TOL[dt], "dd")
+    np.testing.assert_allclose(sl.l1_regularization(qd).item(), want[2], rtol=1e-4)
+    np.testing.assert_allclose(sl.flops_regularization(qd).item(), want[4], rtol=1e-4)
+
+
 def test_loss_matches_torch_formulas_fp32(device):
     """Against train.py's own expressions (F.cross_entropy etc.) in fp32 autograd."""
     q = reps_like(16, 4000, "fp32", seed=1).to(device)
