@@ -1157,69 +1157,65 @@ __global__ __launch_bounds__(256) void fwd_fixup_kernel(int V, const int* __rest
 // slower than bf16 ones, so a small batch is bound by MFMA issue, and the 256-column
 // unit gives only cdiv(V, 256) units to 256 CUs (config 1: 120). Here every wave owns
 // 32 vocab columns and all the batch's rows (RB blocks of 32): cdiv(V, 32) waves, about
-// one per SIMD, and W is read once. Each wave loads its operands straight from global
-// memory into registers, one 128-byte K slab per row per window, one window in flight
-// while the other is multiplied; lane (l32, h) holds bytes 64h .. 64h + 63 of each slab
-// in four 16-byte steps, the same K order the main kernel's LDS fragments have, and the
-// accumulators also start at the bias: every logit is summed exactly as the main kernel
-// sums it. (For bf16/fp16 the main kernel is faster: every wave here re-reads all of
-// H, and its loads fetch each 128-byte line in four pieces, where the main kernel
-// shares H through LDS and copies whole lines; measured at B x S of 64 .. 128 rows.) Bytes past D are
-// zero (loaded from inside the row, then cleared), and rows past B * S repeat the last
-// row and are never reduced.
+// one per SIMD, and W is read once.
+// K runs in 128-byte slabs. Each wave loads its W rows straight into registers through
+// a ring of four slabs (three in flight while one is multiplied). The workgroup's four
+// waves share the H rows: each slab of them is copied once into LDS (double-buffered,
+// the main kernel's swizzled layout, one barrier per slab), so H is read from L2 once
+// per workgroup instead of once per wave. Lane (l32, h) takes bytes 64h + 16p of each
+// slab in step p, the main kernel's K order, and the accumulators start at the bias:
+// every logit is summed exactly as the main kernel sums it. Bytes past D enter as
+// zeros, and rows past B * S repeat the last row and are never reduced.
+// (For bf16/fp16 the main kernel is faster; measured with this kernel's earlier form,
+// which read H per wave, at B x S of 64 .. 128 rows.)
 // Epilogue: x = acc * mask[row] goes to LDS, and lane pairs (batch row b, column) scan
 // the b's S positions in order keeping the largest x with its 5 lowest mantissa bits
 // cleared and, on ties, the lowest s -- the main kernel's key order.
 constexpr int SMALL_MAX_ROWS = 128;
 constexpr int SMALL_WAVES = 4;
-constexpr int SMALL_SLABS = 1;  // 128-byte K slabs per window (2 measured slower)
 
-// One window: NS consecutive 128-byte K slabs of the lane's W row and H rows, four
-// 16-byte steps per slab (lane half h: bytes 64h + 16p of each slab).
-template <typename T, int RB, int NS>
-struct SmallFrag {
-  u32x4 b[NS][4];
-  u32x4 a[NS][RB][4];
-};
-
-template <int RB>
-struct SmallRows {
-  const char* w;      // this lane's W row
-  const char* a[RB];  // this lane's H row in each 32-row block
-};
-
-// Loads of the NS slabs from slab k0 on. TAIL: a slab that ends past D; offsets are
-// clamped into the row.
-template <typename T, int RB, int NS, bool TAIL>
-__device__ __forceinline__ void small_load(SmallFrag<T, RB, NS>& f, const SmallRows<RB>& rp,
-                                           int k0, int h, int row_bytes) {
+// The lane's W row, slab k: four 16-byte chunks (lane half h: bytes 64h + 16p), the
+// offsets clamped into the row (chunks past D are cleared at use).
+__device__ __forceinline__ void small_w_load(u32x4 (&f)[4], const char* wrow, int k, int h,
+                                             int row_bytes) {
 #pragma unroll
-  for (int q = 0; q < NS; ++q)
-#pragma unroll
-    for (int p = 0; p < 4; ++p) {
-      int o = (k0 + q) * 128 + h * 64 + p * 16;
-      if (TAIL) o = min(o, row_bytes - 16);
-      f.b[q][p] = *(const u32x4*)(rp.w + o);
-#pragma unroll
-      for (int r = 0; r < RB; ++r) f.a[q][r][p] = *(const u32x4*)(rp.a[r] + o);
-    }
+  for (int p = 0; p < 4; ++p) f[p] = *(const u32x4*)(wrow + min(k * 128 + h * 64 + p * 16, row_bytes - 16));
 }
 
-// The MFMAs of the NS slabs from slab k0 on, in K order. TAIL: chunks past D enter as
-// zeros (a select at use: registers with loads in flight are never overwritten).
-template <typename T, int RB, int NS, bool TAIL>
-__device__ __forceinline__ void small_mfma(const SmallFrag<T, RB, NS>& f, f32x16 (&acc)[RB],
-                                           int k0, int h, int row_bytes) {
+// This thread's RB chunks of the H slab k (thread t: row 32 r + t / 8, chunk t % 8),
+// the offset clamped into the row.
+template <int RB>
+__device__ __forceinline__ void small_h_load(u32x4 (&hv)[RB], const char* const (&hrow)[RB], int k,
+                                             int hc, int row_bytes) {
+  const int off = min(k * 128 + hc * 16, row_bytes - 16);
 #pragma unroll
-  for (int q = 0; q < NS; ++q)
+  for (int r = 0; r < RB; ++r) hv[r] = *(const u32x4*)(hrow[r] + off);
+}
+
+// Into LDS, chunks past D as zeros. (The select sits here, after the slab's MFMAs, so
+// that the wait for these loads does not hold the MFMAs back.)
+template <int RB>
+__device__ __forceinline__ void small_h_store(u32x4* buf, const u32x4 (&hv)[RB], int k, int hr, int hc,
+                                              int row_bytes) {
+  const bool ok = k * 128 + hc * 16 < row_bytes;
 #pragma unroll
-    for (int p = 0; p < 4; ++p) {
-      const bool ok = !TAIL || (k0 + q) * 128 + h * 64 + p * 16 < row_bytes;
-      const u32x4 z = u32x4{0u, 0u, 0u, 0u};
-      const u32x4 bq = ok ? f.b[q][p] : z;
+  for (int r = 0; r < RB; ++r)
+    buf[(r * 32 + hr) * CHUNKS + (hc ^ swz_key(hr))] = ok ? hv[r] : u32x4{0u, 0u, 0u, 0u};
+}
+
+// The MFMAs of slab k: A from the LDS slab, B from the W registers.
+template <typename T, int RB>
+__device__ __forceinline__ void small_slab(const u32x4* buf, const u32x4 (&f)[4], f32x16 (&acc)[RB],
+                                           int k, int l32, int h, int row_bytes) {
+  const int kx = swz_key(l32);
 #pragma unroll
-      for (int r = 0; r < RB; ++r) Mfma<T>::run(ok ? f.a[q][r][p] : z, bq, acc[r]);
-    }
+  for (int p = 0; p < 4; ++p) {
+    const bool ok = k * 128 + h * 64 + p * 16 < row_bytes;
+    const u32x4 bq = ok ? f[p] : u32x4{0u, 0u, 0u, 0u};
+    const int c = (h * 4 + p) ^ kx;
+#pragma unroll
+    for (int r = 0; r < RB; ++r) Mfma<T>::run(buf[(r * 32 + l32) * CHUNKS + c], bq, acc[r]);
+  }
 }
 
 template <typename T, int RB>
@@ -1227,72 +1223,67 @@ __global__ __launch_bounds__(64 * SMALL_WAVES) void fwd_small_kernel(
     const T* __restrict__ H, const T* __restrict__ W, const T* __restrict__ bias,
     const void* __restrict__ mask, int mask_dtype, T* __restrict__ reps,
     int32_t* __restrict__ argmax, float* __restrict__ reps_f32, int B, int S, int D, int V) {
+  static_assert(SMALL_WAVES * 64 == 32 * CHUNKS, "one thread per 16-byte chunk of 32 H rows");
+  union Smem {
+    u32x4 h[2][RB * 32 * CHUNKS];             // H slabs k and k + 1
+    float xs[SMALL_WAVES][RB * 32][33];      // epilogue, per wave: x[row][column] (+1: no conflicts)
+  };
+  __shared__ Smem sm;
   __shared__ float mk[RB * 32];
-  __shared__ float xs[SMALL_WAVES][RB * 32][33];  // per wave: x[row][column] (+1: no conflicts)
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int l32 = lane & 31, h = lane >> 5;
   const int rows = B * S;
-  if ((int)threadIdx.x < RB * 32)
-    mk[threadIdx.x] = (int)threadIdx.x < rows ? load_mask(mask, mask_dtype, threadIdx.x) : 0.0f;
+  if (tid < RB * 32) mk[tid] = tid < rows ? load_mask(mask, mask_dtype, tid) : 0.0f;
   const int v0 = (blockIdx.x * SMALL_WAVES + wave) * 32;
-  const bool live = v0 < V;  // waves past V only join the barrier
+  const bool live = v0 < V;  // waves past V stage H and keep the barriers
   const int row_bytes = D * (int)sizeof(T);
+  const int nk = (row_bytes + 127) >> 7;  // slabs (the last may be partial)
   f32x16 acc[RB];
-  if (live) {
-    const float bv = bias != nullptr ? to_f32(bias[min(v0 + l32, V - 1)]) : 0.0f;
+  const float bv = bias != nullptr ? to_f32(bias[min(v0 + l32, V - 1)]) : 0.0f;
 #pragma unroll
-    for (int r = 0; r < RB; ++r)
+  for (int r = 0; r < RB; ++r)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) acc[r][i] = bv;
-    SmallRows<RB> rp;
-    rp.w = (const char*)(W + (int64_t)min(v0 + l32, V - 1) * D);
+    for (int i = 0; i < 16; ++i) acc[r][i] = bv;
+  const char* wrow = (const char*)(W + (int64_t)min(v0 + l32, V - 1) * D);
+  const int hr = tid / CHUNKS, hc = tid % CHUNKS;
+  const char* hrow[RB];
 #pragma unroll
-    for (int r = 0; r < RB; ++r) rp.a[r] = (const char*)(H + (int64_t)min(r * 32 + l32, rows - 1) * D);
-    // Windows of SMALL_SLABS full slabs through a ring of three: two in flight while
-    // one is multiplied. Then the full slabs left over, and the partial slab past the
-    // last full one, if any. Loads past the last window re-read it (unused), so every
-    // window issues the same loads; the scheduling barriers keep each window's loads
-    // together and in issue order, so the wait before a window's MFMAs counts only its
-    // own loads.
-    constexpr int NS = SMALL_SLABS;
-    const int nks = row_bytes >> 7;  // full slabs
-    const int nkw = nks / NS;        // full windows
-    SmallFrag<T, RB, NS> f0, f1, f2;
+  for (int r = 0; r < RB; ++r) hrow[r] = (const char*)(H + (int64_t)min(r * 32 + hr, rows - 1) * D);
+  if (nk > 0) {
+    // Slab j: W from ring slot j % 4 (three slabs in flight while one is multiplied), H
+    // from LDS buffer j % 2. Loads past the last slab re-read it (unused), so every step
+    // issues the same loads; the scheduling barriers keep the loads in issue order (H's
+    // first), so each wait counts only what it needs.
+    u32x4 f0[4], f1[4], f2[4], f3[4], hv[RB];
+    small_h_load<RB>(hv, hrow, 0, hc, row_bytes);
+    small_w_load(f0, wrow, 0, h, row_bytes);
+    small_w_load(f1, wrow, min(1, nk - 1), h, row_bytes);
+    small_w_load(f2, wrow, min(2, nk - 1), h, row_bytes);
+    small_h_store<RB>(sm.h[0], hv, 0, hr, hc, row_bytes);
+    __syncthreads();
+    auto step = [&](int j, const u32x4 (&fc)[4], u32x4 (&fn)[4]) {
+      small_h_load<RB>(hv, hrow, min(j + 1, nk - 1), hc, row_bytes);
+      small_w_load(fn, wrow, min(j + 3, nk - 1), h, row_bytes);
+      __builtin_amdgcn_sched_barrier(0);
+      small_slab<T, RB>(sm.h[j & 1], fc, acc, j, l32, h, row_bytes);
+      __builtin_amdgcn_sched_barrier(0);
+      small_h_store<RB>(sm.h[(j + 1) & 1], hv, min(j + 1, nk - 1), hr, hc, row_bytes);
+      __syncthreads();
+    };
     int k = 0;
-    if (nkw > 0) {
-      small_load<T, RB, NS, false>(f0, rp, 0, h, row_bytes);
-      small_load<T, RB, NS, false>(f1, rp, min(1, nkw - 1) * NS, h, row_bytes);
-      for (; k + 2 < nkw; k += 3) {
-        small_load<T, RB, NS, false>(f2, rp, (k + 2) * NS, h, row_bytes);
-        __builtin_amdgcn_sched_barrier(0);
-        small_mfma<T, RB, NS, false>(f0, acc, k * NS, h, row_bytes);
-        __builtin_amdgcn_sched_barrier(0);
-        small_load<T, RB, NS, false>(f0, rp, min(k + 3, nkw - 1) * NS, h, row_bytes);
-        __builtin_amdgcn_sched_barrier(0);
-        small_mfma<T, RB, NS, false>(f1, acc, (k + 1) * NS, h, row_bytes);
-        __builtin_amdgcn_sched_barrier(0);
-        small_load<T, RB, NS, false>(f1, rp, min(k + 4, nkw - 1) * NS, h, row_bytes);
-        __builtin_amdgcn_sched_barrier(0);
-        small_mfma<T, RB, NS, false>(f2, acc, (k + 2) * NS, h, row_bytes);
-        __builtin_amdgcn_sched_barrier(0);
-      }
-      // f0, f1 hold windows k, k + 1 (loads clamped to the last window)
-      if (k < nkw) small_mfma<T, RB, NS, false>(f0, acc, k * NS, h, row_bytes);
-      if (k + 1 < nkw) small_mfma<T, RB, NS, false>(f1, acc, (k + 1) * NS, h, row_bytes);
-      k = nkw;
+    for (; k + 3 < nk; k += 4) {
+      step(k, f0, f3);
+      step(k + 1, f1, f0);
+      step(k + 2, f2, f1);
+      step(k + 3, f3, f2);
     }
-    for (int ks = nkw * NS; ks < nks; ++ks) {
-      SmallFrag<T, RB, 1> g;
-      small_load<T, RB, 1, false>(g, rp, ks, h, row_bytes);
-      small_mfma<T, RB, 1, false>(g, acc, ks, h, row_bytes);
-    }
-    if (row_bytes & 127) {
-      SmallFrag<T, RB, 1> g;
-      small_load<T, RB, 1, true>(g, rp, nks, h, row_bytes);
-      small_mfma<T, RB, 1, true>(g, acc, nks, h, row_bytes);
-    }
+    // f0, f1, f2 hold slabs k, k + 1, k + 2 (loads clamped to the last slab)
+    if (k < nk) step(k, f0, f3);
+    if (k + 1 < nk) step(k + 1, f1, f0);
+    if (k + 2 < nk) step(k + 2, f2, f1);
   }
-  __syncthreads();  // mk is staged
+  // (the last step's barrier: every wave is done with the H slabs, sm.xs may be written)
+  __syncthreads();  // mk is staged (also when nk == 0)
   if (live) {
     // 32x32 accumulator layout: lane holds column l32, register 4q + e row 8q + 4h + e.
 #pragma unroll
@@ -1300,7 +1291,7 @@ __global__ __launch_bounds__(64 * SMALL_WAVES) void fwd_small_kernel(
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         const int row = r * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
-        xs[wave][row][l32] = acc[r][i] * mk[row];
+        sm.xs[wave][row][l32] = acc[r][i] * mk[row];
       }
   }
   __syncthreads();
@@ -1311,7 +1302,7 @@ __global__ __launch_bounds__(64 * SMALL_WAVES) void fwd_small_kernel(
     float bvx = 0.0f;
     int bi = 0;
     for (int s = 0; s < S; ++s) {
-      const float x = __int_as_float(__float_as_int(xs[wave][b * S + s][c]) & ~31);
+      const float x = __int_as_float(__float_as_int(sm.xs[wave][b * S + s][c]) & ~31);
       if (x > bvx) {  // strict: the lowest s keeps a tie
         bvx = x;
         bi = s;
