@@ -71,14 +71,15 @@ def cpu_model():
 
 FWD_KERNEL = "sparton::fwd::sparton_fwd_kernel<%s>"
 KNAME = {"bf16": "bf16", "fp16": "f16", "fp32": "f32"}
-# fp32 batches of at most 128 rows (B * S) run one kernel, one wave per 32 vocab columns.
+# Batches of at most 128 rows (B * S) run one kernel, one wave per 32 vocab columns: fp32
+# always, 16-bit up to B * S * V = 2^24.
 SMALL_MAX_ROWS = 128
 SMALL_KERNEL = "sparton::fwd::fwd_small_kernel<%s, %d>"
 SMALL_TNAME = {"bf16": "__bf16", "fp16": "_Float16", "fp32": "float"}
 
 
 def fwd_kernel_name(w, dname):
-    if dname == "fp32" and w.B * w.S <= SMALL_MAX_ROWS:
+    if w.B * w.S <= SMALL_MAX_ROWS and (dname == "fp32" or w.B * w.S * w.V <= 1 << 24):
         return SMALL_KERNEL % (SMALL_TNAME[dname], min(4, -(-w.B * w.S // 32)))
     return FWD_KERNEL % KNAME[dname]
 

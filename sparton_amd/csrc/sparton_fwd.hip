@@ -1153,9 +1153,10 @@ __global__ __launch_bounds__(256) void fwd_fixup_kernel(int V, const int* __rest
 
 // ---- small batches --------------------------------------------------------------
 //
-// fp32 with B * S <= SMALL_MAX_ROWS: one kernel, no plan or fixup. fp32 MFMAs are 16x
-// slower than bf16 ones, so a small batch is bound by MFMA issue, and the 256-column
-// unit gives only cdiv(V, 256) units to 256 CUs (config 1: 120). Here every wave owns
+// B * S <= SMALL_MAX_ROWS: one kernel, no plan or fixup. The 256-column unit gives only
+// cdiv(V, 256) units to 256 CUs (config 1: 120) and leaves most of its 256 rows empty;
+// an fp32 batch is then bound by MFMA issue (fp32 MFMAs are 16x slower than bf16 ones)
+// and a 16-bit one by the latency of its few units' W streams. Here every wave owns
 // 32 vocab columns and all the batch's rows (RB blocks of 32): cdiv(V, 32) waves, about
 // one per SIMD, and W is read once.
 // K runs in 128-byte slabs. Each wave loads its W rows straight into registers through
@@ -1166,13 +1167,15 @@ __global__ __launch_bounds__(256) void fwd_fixup_kernel(int V, const int* __rest
 // slab in step p, the main kernel's K order, and the accumulators start at the bias:
 // every logit is summed exactly as the main kernel sums it. Bytes past D enter as
 // zeros, and rows past B * S repeat the last row and are never reduced.
-// (For bf16/fp16 the main kernel is faster; measured with this kernel's earlier form,
-// which read H per wave, at B x S of 64 .. 128 rows.)
 // Epilogue: x = acc * mask[row] goes to LDS, and lane pairs (batch row b, column) scan
 // the b's S positions in order keeping the largest x with its 5 lowest mantissa bits
 // cleared and, on ties, the lowest s -- the main kernel's key order.
 constexpr int SMALL_MAX_ROWS = 128;
 constexpr int SMALL_WAVES = 4;
+// 16-bit batches take this kernel up to B * S * V = 2^24 (measured against the main path:
+// 64-128 rows at V = 30522 and 32 rows at V = 128256 win by 7-36%, 128 rows at V = 250002
+// loses by 15%); fp32 ones always (1.8-2x faster at every measured shape).
+constexpr int64_t SMALL_MAX_WORK_16 = (int64_t)1 << 24;
 
 // The lane's W row, slab k: four 16-byte chunks (lane half h: bytes 64h + 16p), the
 // offsets clamped into the row (chunks past D are cleared at use).
@@ -1316,11 +1319,15 @@ __global__ __launch_bounds__(64 * SMALL_WAVES) void fwd_small_kernel(
   }
 }
 
-// SPARTON_FWD_PATH=main sends small batches through the plan / main / fixup kernels too
-// (tests compare the two paths).
-static bool small_path_enabled() {
+// SPARTON_FWD_PATH=main sends small fp32 batches through the plan / main / fixup kernels
+// too, and SPARTON_FWD_PATH=small sends small 16-bit batches through the small-batch kernel
+// (tests compare the paths; measurements).
+static int fwd_path_override() {
   const char* e = getenv("SPARTON_FWD_PATH");
-  return e == nullptr || strcmp(e, "main") != 0;
+  if (e == nullptr) return 0;
+  if (strcmp(e, "main") == 0) return 1;
+  if (strcmp(e, "small") == 0) return 2;
+  return 0;
 }
 
 template <typename T>
@@ -1373,7 +1380,9 @@ static int launch(const void* H, const void* W, const void* bias, const void* ma
   const int64_t n_mt_max = cdiv(B * ngrp, NGRP);
   // Unit numbers (and one round past them) must fit in int.
   if (n_mt_max * n_vt > INT32_MAX / 2) return SPARTON_EUNSUPPORTED;
-  if (sizeof(T) == 4 && B * S > 0 && B * S <= SMALL_MAX_ROWS && small_path_enabled()) {
+  const int ovr = fwd_path_override();
+  if (B * S > 0 && B * S <= SMALL_MAX_ROWS && ovr != 1 &&
+      (sizeof(T) == 4 || B * S * V <= SMALL_MAX_WORK_16 || ovr == 2)) {
     if (ev_main != nullptr) (void)hipEventRecord(ev_main[0], stream);
     launch_small<T>(H, W, bias, mask, mask_dtype, reps, argmax, reps_f32, B, S, D, V, stream);
     if (ev_main != nullptr) (void)hipEventRecord(ev_main[1], stream);

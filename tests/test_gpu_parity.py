@@ -587,13 +587,17 @@ def test_long_sequences_and_many_rows(case, device):
     ("fp32", 5, 20, 132, 333, True, "int64"),       # 100 rows, a 16-byte tail slab
     ("fp32", 128, 1, 72, 5000, True, "bool"),       # S = 1: every row its own batch row
     ("fp32", 2, 48, 2048, 2000, False, "int64"),    # 64 full slabs
-    ("bf16", 2, 32, 256, 1000, True, "int64"),      # 16-bit: the main path either way
+    ("bf16", 2, 32, 768, 30522, True, "int64"),     # 16-bit, config 2's widths
+    ("bf16", 3, 40, 256, 1000, True, "holes"),      # 120 rows: four 32-row blocks
+    ("fp16", 1, 7, 24, 100, False, "frac"),         # one block, D in one partial slab
+    ("bf16", 128, 1, 72, 5000, True, "bool"),       # S = 1, a 16-byte tail slab
+    ("bf16", 2, 48, 4096, 2000, False, "int64"),    # 64 full slabs
 ], ids=lambda c: "-".join(map(str, c)))
 def test_small_batch_path_equals_main_path(case, device, monkeypatch):
-    """fp32 batches of B * S <= 128 rows take one kernel (one wave per 32 vocab columns,
-    all rows, W read once). It sums every logit in the main kernel's order and applies
-    the same key order, so reps, argmax and the fp32 reps equal the plan / main / fixup
-    path's bitwise; and both match the oracle."""
+    """Batches of B * S <= 128 rows (16-bit ones up to B * S * V = 2^24) take one kernel
+    (one wave per 32 vocab columns, all rows, W read once). It sums every logit in the
+    main kernel's order and applies the same key order, so reps, argmax and the fp32 reps
+    equal the plan / main / fixup path's bitwise; and both match the oracle."""
     say(f"small-batch path vs main path, case {case}")
     H, W, b, m, G = make_case(*case)
     Hd, Wd, md = H.to(device), W.to(device), m.to(device)
