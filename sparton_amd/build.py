@@ -81,7 +81,7 @@ def build_torch_ops(verbose: bool = False) -> str:
            "-I", "/opt/rocm/include",
            os.path.join(CSRC, "sparton_torch.cpp"), "-o", tmp,
            "-L", os.path.join(tdir, "lib"), "-ltorch", "-ltorch_cpu", "-lc10", "-lc10_hip",
-           "-ltorch_hip", "-L", HERE, "-lsparton_hip",
+           "-ltorch_hip", "-lhipblaslt", "-L", HERE, "-lsparton_hip",
            f"-Wl,-rpath,{os.path.join(tdir, 'lib')}", "-Wl,-rpath,$ORIGIN"]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:

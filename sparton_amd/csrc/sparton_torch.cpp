@@ -27,7 +27,12 @@
 #include <torch/csrc/autograd/custom_function.h>
 #include <torch/library.h>
 
+#include <hipblaslt/hipblaslt.h>
+
 #include <algorithm>
+#include <cstring>
+#include <mutex>
+#include <unordered_map>
 
 #include "../../include/sparton.h"
 
@@ -230,6 +235,141 @@ Tensor head_train_autocast_cuda(const Tensor& hidden, const Tensor& weight,
   return head_fwd(dense(h), dense(weight_c), dense(opt(bias_c)), dense(mask), false, false).reps;
 }
 
+// ---- cached hipBLASLt GEMMs (the transform's, 16-bit) ------------------------------------
+//
+// Column-major D[m x n] = op(A)[m x k] op(B)[k x n], fp32 accumulation, optionally a strided
+// batch. torch's GEMM path asks hipBLASLt's heuristic for an algorithm on every call (~20 us of
+// host time per GEMM); here the descriptors and the heuristic's first algorithm are made once
+// per shape and device and kept, so a call is one hipblasLtMatmul. The library is the one
+// torch loads (same soname), so the process holds one hipBLASLt.
+struct GemmKey {
+  int device, in_type, out_type, ta, tb, batch;
+  int64_t m, n, k, lda, ldb, ldd, sa, sb, sd;
+};
+bool operator==(const GemmKey& x, const GemmKey& y) { return std::memcmp(&x, &y, sizeof(GemmKey)) == 0; }
+struct GemmKeyHash {
+  size_t operator()(const GemmKey& key) const {
+    const unsigned char* p = reinterpret_cast<const unsigned char*>(&key);
+    uint64_t h = 1469598103934665603ull;  // FNV-1a over the (zero-initialised) key bytes
+    for (size_t i = 0; i < sizeof(GemmKey); ++i) h = (h ^ p[i]) * 1099511628211ull;
+    return (size_t)h;
+  }
+};
+struct GemmPlan {
+  hipblasLtMatmulDesc_t op = nullptr;
+  hipblasLtMatrixLayout_t a = nullptr, b = nullptr, d = nullptr;
+  hipblasLtMatmulAlgo_t algo;
+  size_t ws = 0;
+};
+constexpr int kMaxGemmDevices = 64;
+constexpr uint64_t kGemmMaxWorkspace = (uint64_t)32 << 20;
+std::mutex g_lt_mu;
+hipblasLtHandle_t g_lt[kMaxGemmDevices] = {};
+std::unordered_map<GemmKey, GemmPlan, GemmKeyHash> g_plans;
+
+void lt_check(hipblasStatus_t st, const char* what) {
+  TORCH_CHECK(st == HIPBLAS_STATUS_SUCCESS, "sparton: hipBLASLt ", what, " failed (status ", (int)st, ")");
+}
+
+GemmKey gemm_key(int device, hipDataType in, hipDataType out, bool ta, bool tb, int64_t m, int64_t n,
+                 int64_t k, int64_t lda, int64_t ldb, int64_t ldd, int batch = 1, int64_t sa = 0,
+                 int64_t sb = 0, int64_t sd = 0) {
+  GemmKey key;
+  std::memset(&key, 0, sizeof(key));  // the padding bytes take part in == and the hash
+  key.device = device;
+  key.in_type = (int)in;
+  key.out_type = (int)out;
+  key.ta = ta;
+  key.tb = tb;
+  key.batch = batch;
+  key.m = m;
+  key.n = n;
+  key.k = k;
+  key.lda = lda;
+  key.ldb = ldb;
+  key.ldd = ldd;
+  key.sa = sa;
+  key.sb = sb;
+  key.sd = sd;
+  return key;
+}
+
+// Called with the key's device current. The returned reference stays valid: the map only grows.
+const GemmPlan& gemm_plan(const GemmKey& key, hipblasLtHandle_t* handle) {
+  TORCH_CHECK(key.device >= 0 && key.device < kMaxGemmDevices, "sparton: device index out of range");
+  std::lock_guard<std::mutex> lock(g_lt_mu);
+  if (g_lt[key.device] == nullptr) lt_check(hipblasLtCreate(&g_lt[key.device]), "handle creation");
+  *handle = g_lt[key.device];
+  auto it = g_plans.find(key);
+  if (it != g_plans.end()) return it->second;
+  GemmPlan p;
+  lt_check(hipblasLtMatmulDescCreate(&p.op, HIPBLAS_COMPUTE_32F, HIP_R_32F), "descriptor");
+  const hipblasOperation_t ta = key.ta ? HIPBLAS_OP_T : HIPBLAS_OP_N;
+  const hipblasOperation_t tb = key.tb ? HIPBLAS_OP_T : HIPBLAS_OP_N;
+  lt_check(hipblasLtMatmulDescSetAttribute(p.op, HIPBLASLT_MATMUL_DESC_TRANSA, &ta, sizeof(ta)), "transA");
+  lt_check(hipblasLtMatmulDescSetAttribute(p.op, HIPBLASLT_MATMUL_DESC_TRANSB, &tb, sizeof(tb)), "transB");
+  const hipDataType in = (hipDataType)key.in_type, out = (hipDataType)key.out_type;
+  lt_check(hipblasLtMatrixLayoutCreate(&p.a, in, key.ta ? key.k : key.m, key.ta ? key.m : key.k, key.lda), "layout A");
+  lt_check(hipblasLtMatrixLayoutCreate(&p.b, in, key.tb ? key.n : key.k, key.tb ? key.k : key.n, key.ldb), "layout B");
+  lt_check(hipblasLtMatrixLayoutCreate(&p.d, out, key.m, key.n, key.ldd), "layout D");
+  if (key.batch > 1) {
+    const int32_t bc = key.batch;
+    const hipblasLtMatrixLayout_t lay[3] = {p.a, p.b, p.d};
+    const int64_t str[3] = {key.sa, key.sb, key.sd};
+    for (int i = 0; i < 3; ++i) {
+      lt_check(hipblasLtMatrixLayoutSetAttribute(lay[i], HIPBLASLT_MATRIX_LAYOUT_BATCH_COUNT, &bc, sizeof(bc)), "batch");
+      lt_check(hipblasLtMatrixLayoutSetAttribute(lay[i], HIPBLASLT_MATRIX_LAYOUT_STRIDED_BATCH_OFFSET, &str[i],
+                                                 sizeof(str[i])), "batch stride");
+    }
+  }
+  hipblasLtMatmulPreference_t pref = nullptr;
+  lt_check(hipblasLtMatmulPreferenceCreate(&pref), "preference");
+  lt_check(hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &kGemmMaxWorkspace,
+                                                 sizeof(kGemmMaxWorkspace)), "workspace preference");
+  hipblasLtMatmulHeuristicResult_t res[1];
+  int got = 0;
+  const hipblasStatus_t hs = hipblasLtMatmulAlgoGetHeuristic(*handle, p.op, p.a, p.b, p.d, p.d, pref, 1, res, &got);
+  hipblasLtMatmulPreferenceDestroy(pref);
+  lt_check(hs, "heuristic");
+  TORCH_CHECK(got > 0, "sparton: hipBLASLt found no algorithm for a ", key.m, " x ", key.n, " x ", key.k, " GEMM");
+  p.algo = res[0].algo;
+  p.ws = res[0].workspaceSize;
+  return g_plans.emplace(key, p).first->second;
+}
+
+void lt_gemm(const GemmKey& key, const void* A, const void* B, void* D, const Tensor& like) {
+  hipblasLtHandle_t handle = nullptr;
+  const GemmPlan& p = gemm_plan(key, &handle);
+  Tensor ws = workspace(p.ws, like);
+  const float alpha = 1.0f, beta = 0.0f;
+  lt_check(hipblasLtMatmul(handle, p.op, &alpha, A, p.a, B, p.b, &beta, D, p.d, D, p.d, &p.algo,
+                           p.ws ? ws.data_ptr() : nullptr, p.ws, (hipStream_t)stream_of(like)),
+           "matmul");
+}
+
+hipDataType lt_type(at::ScalarType t) { return t == at::kBFloat16 ? HIP_R_16BF : HIP_R_16F; }
+bool lt_gemm_ok(const Tensor& t) { return t.scalar_type() == at::kBFloat16 || t.scalar_type() == at::kHalf; }
+
+// z[M, Dout] = x2[M, Din] W[Dout, Din]^T (column-major: z^T = op_T(W) x2^T).
+Tensor lt_linear(const Tensor& x2, const Tensor& w) {
+  const int64_t M = x2.size(0), Din = x2.size(1), Dout = w.size(0);
+  Tensor z = at::empty({M, Dout}, x2.options());
+  lt_gemm(gemm_key(x2.get_device(), lt_type(x2.scalar_type()), lt_type(x2.scalar_type()), true, false, Dout, M, Din,
+                   Din, Din, Dout),
+          w.data_ptr(), x2.data_ptr(), z.data_ptr(), x2);
+  return z;
+}
+
+// dx[M, Din] = dz[M, Dout] W[Dout, Din] (column-major: dx^T = W^T dz^T, both as stored).
+Tensor lt_dgrad(const Tensor& dz, const Tensor& w) {
+  const int64_t M = dz.size(0), Dout = dz.size(1), Din = w.size(1);
+  Tensor dx = at::empty({M, Din}, dz.options());
+  lt_gemm(gemm_key(dz.get_device(), lt_type(dz.scalar_type()), lt_type(dz.scalar_type()), false, false, Din, M, Dout,
+                   Din, Dout, Din),
+          w.data_ptr(), dz.data_ptr(), dx.data_ptr(), dz);
+  return dx;
+}
+
 // ---- the MLM transform -------------------------------------------------------------------
 
 // Row chunks of the transform's batched weight-gradient GEMM, or 0 for one plain GEMM (the same
@@ -242,15 +382,26 @@ int64_t wgrad_chunks(int64_t M, int64_t D, at::ScalarType dt) {
 
 // dW = dz^T x2: row chunks transposed by HIP, one batched GEMM with fp32 outputs, the chunk
 // products summed in order and rounded once by HIP (transform.py's _weight_grad).
+// For 16-bit, the chunks go to hipBLASLt as one strided batch over row chunks of dz and x2 as
+// they lie (dz transposed by the GEMM's op flag, so no transpose kernel): chunk i's fp32
+// product is column-major (Din x Dout), i.e. row-major dW [Dout][Din].
 Tensor transform_weight_grad(const Tensor& dz, const Tensor& x2, int64_t M, int64_t D) {
   const int64_t C = wgrad_chunks(M, D, dz.scalar_type());
-  if (C == 0) return at::mm(dz.t(), x2);
+  if (C == 0) {
+    if (!lt_gemm_ok(dz)) return at::mm(dz.t(), x2);
+    Tensor dw = at::empty({D, D}, dz.options());  // column-major dW^T = x2^T dz
+    lt_gemm(gemm_key(dz.get_device(), lt_type(dz.scalar_type()), lt_type(dz.scalar_type()), false, true, D, D, M,
+                     D, D, D),
+            x2.data_ptr(), dz.data_ptr(), dw.data_ptr(), dz);
+    return dw;
+  }
   const int code = dtype_code(dz.scalar_type());
   void* st = stream_of(dz);
-  Tensor dzt = at::empty({C, D, M / C}, dz.options());
-  check(sparton_transform_dz_chunks(dz.data_ptr(), dzt.data_ptr(), M, D, C, code, st),
-        "sparton_transform_dz_chunks");
-  Tensor part = at::bmm(dzt, x2.contiguous().view({C, M / C, D}), at::kFloat);
+  const int64_t Mc = M / C;
+  Tensor part = at::empty({C, D, D}, dz.options().dtype(at::kFloat));
+  lt_gemm(gemm_key(dz.get_device(), lt_type(dz.scalar_type()), HIP_R_32F, false, true, D, D, Mc, D, D, D, (int)C,
+                   Mc * D, Mc * D, D * D),
+          x2.data_ptr(), dz.data_ptr(), part.data_ptr(), dz);
   Tensor dw = at::empty({D, D}, dz.options());
   check(sparton_transform_chunk_sum(part.data_ptr<float>(), dw.data_ptr(), C, D * D, code, st),
         "sparton_transform_chunk_sum");
@@ -265,7 +416,8 @@ struct TransformFn : public torch::autograd::Function<TransformFn> {
     c10::OptionalDeviceGuard guard(x.device());
     const int64_t D = x.size(-1);
     Tensor x2 = x.reshape({-1, D});
-    Tensor z = at::linear(x2, weight);  // hipBLASLt, as F.linear
+    // hipBLASLt: cached plans for 16-bit, torch's F.linear otherwise
+    Tensor z = lt_gemm_ok(x2) ? lt_linear(dense(x2), dense(weight)) : at::linear(x2, weight);
     const int64_t M = z.size(0);
     Tensor y = at::empty_like(z);
     Tensor mean = at::empty({M}, x.options().dtype(at::kFloat));
@@ -297,8 +449,8 @@ struct TransformFn : public torch::autograd::Function<TransformFn> {
                                 dg.data_ptr<float>(), dbt.data_ptr<float>(), dbd.data_ptr<float>(),
                                 ws.data_ptr(), ws_bytes, M, D, dtype_code(x.scalar_type()), stream_of(x)),
           "sparton_transform_bwd");
-    Tensor dx = at::mm(dz, weight);  // hipBLASLt
-    Tensor dw = transform_weight_grad(dz, x2, M, D);
+    Tensor dx = lt_gemm_ok(dz) ? lt_dgrad(dz, dense(weight)) : at::mm(dz, weight);
+    Tensor dw = transform_weight_grad(dz, lt_gemm_ok(dz) ? dense(x2) : x2, M, D);
     return {dx.view(x.sizes()), dw, dbd, dg, dbt, Tensor()};
   }
 };
@@ -312,7 +464,8 @@ Tensor transform_cuda(const Tensor& x, const Tensor& weight, const Tensor& dense
                       const Tensor& ln_weight, const Tensor& ln_bias, double eps) {
   c10::OptionalDeviceGuard guard(x.device());
   const int64_t D = x.size(-1);
-  Tensor z = at::linear(x.reshape({-1, D}), weight);
+  Tensor x2 = x.reshape({-1, D});
+  Tensor z = lt_gemm_ok(x2) ? lt_linear(dense(x2), dense(weight)) : at::linear(x2, weight);
   const int64_t M = z.size(0);
   Tensor y = at::empty_like(z);
   Tensor mean = at::empty({M}, x.options().dtype(at::kFloat)), rstd = at::empty_like(mean);
