@@ -83,6 +83,7 @@ CASES = [
     ("bf16", 8, 3000, 64, 700, True, "gaps"),   # B*S > 16384: plan with the mask in global memory
     ("fp16", 1100, 8, 16, 200, True, "int64"),  # more groups than plan threads
     ("bf16", 600, 500, 16, 300, True, "holes"),  # > 16384 groups: the three-kernel plan
+    ("fp16", 6, 70, 32, 333, False, "bf16"),    # bf16 mask
 ]
 
 # Cases run again with several vocab tiles per workgroup (the unit stream then crosses
@@ -128,6 +129,8 @@ def make_case(dt, B, S, D, V, bias, mk, seed=0):
         m = torch.randint(0, 3, (B, S), generator=g).float() * 0.5
     elif mk == "f16":
         m = pad.half()
+    elif mk == "bf16":
+        m = pad.bfloat16()
     G = torch.rand(B, V, generator=g).to(dtype) * (torch.rand(B, V, generator=g) < 0.3)
     return H, W, b, m, G
 
