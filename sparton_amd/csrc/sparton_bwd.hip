@@ -383,8 +383,29 @@ template <> struct Raw4<f16> {
   __device__ __forceinline__ f32x4 f() const { return f32x4{(float)v[0], (float)v[1], (float)v[2], (float)v[3]}; }
 };
 
+// The order every dH kernel (except the few-rows split kernel) sums a row in: the row's
+// entries, in v order, are taken DH_BATCH at a time (the last batch may hold fewer); a
+// batch's partial is P = fma(g_u, W[v_u], P) over its entries from P = 0, and the row is
+// ((0 + P_0) + P_1) + ... So the fused path, whose waves share one workgroup's batches,
+// and the five-kernel path agree bitwise.
+constexpr int DH_BATCH = 4;
+
 // Rows gathered per batch: all their loads are in flight together (about 24 per lane).
 template <int NP> struct Batch { static constexpr int U = NP <= 3 ? 8 : NP <= 6 ? 4 : NP <= 8 ? 3 : 2; };
+// bwd_dh_kernel takes at most DH_MAX_NP register passes (wider rows loop over D) and
+// whole DH_BATCH-entry batches per load group.
+constexpr int DH_MAX_NP = 8;
+template <int NP> struct DhPasses { static constexpr int value = NP < DH_MAX_NP ? NP : DH_MAX_NP; };
+template <int NP> struct DhBatch { static constexpr int U = NP <= 3 ? 8 : 4; };
+static_assert(DhBatch<1>::U % DH_BATCH == 0 && DhBatch<DH_MAX_NP>::U % DH_BATCH == 0, "whole batches");
+
+// P = fma(g, w, P) per element, written out so that every dH kernel rounds the same way.
+__device__ __forceinline__ void fma4(f32x4& P, float g, const f32x4& w) {
+  P[0] = __builtin_fmaf(g, w[0], P[0]);
+  P[1] = __builtin_fmaf(g, w[1], P[1]);
+  P[2] = __builtin_fmaf(g, w[2], P[2]);
+  P[3] = __builtin_fmaf(g, w[3], P[3]);
+}
 
 // The staged dW kernel gathers the rows of IDC of a wave's ids together, U rows at a
 // time. For 16-bit rows of up to 768 elements one id and 4 rows keep it within 64 VGPRs:
@@ -410,7 +431,8 @@ template <typename T, typename O, int NP>
 __global__ __launch_bounds__(256) void bwd_dh_kernel(
     const T* __restrict__ W, const int2* __restrict__ list, const int* __restrict__ seg_start,
     const int* __restrict__ seg_cnt, O* __restrict__ dH, int B, int S, int D, int V, int S_row) {
-  constexpr int U = Batch<NP>::U;
+  constexpr int U = DhBatch<NP>::U;
+  static_assert(NP <= DH_MAX_NP, "register passes");
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * 4 + wave;
   if (row >= (int64_t)B * S) return;
@@ -442,10 +464,21 @@ __global__ __launch_bounds__(256) void bwd_dh_kernel(
             else w[u][p].zero();
           }
         }
+        // Whole batches (chunks of 64 and j are multiples of DH_BATCH), one pass at a
+        // time, so only one pass of a partial is held in registers.
 #pragma unroll
-        for (int u = 0; u < U; ++u)
+        for (int p = 0; p < NP; ++p) {
 #pragma unroll
-          for (int p = 0; p < NP; ++p) acc[p] += g[u] * w[u][p].f();
+          for (int a = 0; a < U; a += DH_BATCH) {
+            if (j + a < n) {  // uniform: the batch exists
+              f32x4 P = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+              for (int u = a; u < a + DH_BATCH; ++u)
+                if (j + u < n) fma4(P, g[u], w[u][p].f());
+              acc[p] += P;
+            }
+          }
+        }
       }
     }
     O* out = dH + (b * S_row + (row - b * S)) * D;
@@ -843,72 +876,154 @@ __global__ __launch_bounds__(256) void bwd_compact_kernel(
 // entries sorted by row range, then v, so a range's entries are one contiguous run per
 // block: thread t copies the t-th of them into LDS (its block found by binary search over
 // the runs' prefix sums), 64 * FUSE_WAVES per round, in block (= v) order. Each wave
-// appends the entries of its row to its own list, keeping v order, and gathers their W
-// rows U at a time, summing in v order exactly as bwd_dh_kernel does over its segment.
+// appends the entries of its row to its own list, keeping v order.
+// The workgroup's waves then share the gathering: the rows' DH_BATCH-entry batches, in
+// (row, batch) order, are taken FUSE_SLOTS at a time, one per wave; each wave gathers its
+// batch's W rows and writes the batch partial to LDS, and each row's own wave adds its
+// rows' partials in batch order. A row with many entries is gathered by all the waves of
+// its workgroup, and the sums are exactly those of bwd_dh_kernel.
 // With the compaction in the dW kernel this replaces the count, scan and scatter passes.
-constexpr int FUSE_CAP = 128;  // a wave's list; gathered before it could overflow
+constexpr int FUSE_CAP = 120;  // a wave's list; the lists are gathered before one could overflow
 constexpr int FUSE_WAVES = 8;  // rows per workgroup (one 16-wave workgroup per range measured
                                // slower: 56.5 vs 49.4 us at config 2)
 constexpr int FUSE_HALVES = FUSE_ROWS / FUSE_WAVES;  // workgroups per row range
 static_assert(FUSE_ROWS % FUSE_WAVES == 0, "whole workgroups per row range");
 // Register passes the fused path takes (a batch of rows and the accumulators in ~64 VGPRs).
 template <typename T> struct FuseMaxNp { static constexpr int value = sizeof(T) == 2 ? 6 : 3; };
-// W rows gathered per batch by the fused dH kernel: fewer than the five-kernel path's, so
-// that the kernel stays within 64 VGPRs (8 waves per SIMD: four workgroups per CU).
+// W rows loaded at a time by the fused dH gather (a divisor of DH_BATCH): fewer for wide
+// rows, so that the kernel stays near 64 VGPRs (8 waves per SIMD: four workgroups per CU).
 template <int NP> struct FuseBatch { static constexpr int U = NP <= 3 ? 4 : 2; };
-
-template <typename T, int NP>
-__device__ __forceinline__ void gather_rows(const T* __restrict__ W, const int2* list, int n,
-                                            int D, int lane, f32x4* acc) {
-  constexpr int U = FuseBatch<NP>::U;
-  constexpr int VMASK = (1 << FUSE_V_BITS) - 1;
-  for (int e0 = 0; e0 < n; e0 += 64) {
-    const int2 ent = e0 + lane < n ? list[e0 + lane] : make_int2(0, 0);
-    const int m = min(64, n - e0);
-    for (int j = 0; j < m; j += U) {
-      Raw4<T> w[U][NP];
-      float g[U];
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        // past the list end: reload the last entry's row (a cache hit) with g' = 0
-        const int jj = min(j + u, m - 1);
-        const int v = __builtin_amdgcn_readlane(ent.x, jj) & VMASK;
-        g[u] = j + u < m ? __int_as_float(__builtin_amdgcn_readlane(ent.y, jj)) : 0.0f;
-#pragma unroll
-        for (int p = 0; p < NP; ++p) {
-          const int d = p * 256 + lane * 4;
-          if (d < D) w[u][p].load(W + (int64_t)v * D + d);
-          else w[u][p].zero();
-        }
-      }
-#pragma unroll
-      for (int u = 0; u < U; ++u)
-#pragma unroll
-        for (int p = 0; p < NP; ++p) acc[p] += g[u] * w[u][p].f();
-    }
-  }
-}
+// Batches gathered per step (one per wave; half the waves for wide rows, whose partials
+// take twice the LDS).
+template <int NP> struct FuseSlots { static constexpr int value = NP <= 3 ? FUSE_WAVES : FUSE_WAVES / 2; };
+static_assert(DH_BATCH % FuseBatch<1>::U == 0 && DH_BATCH % FuseBatch<6>::U == 0, "whole batches");
 
 // PER: 64-id blocks per thread in the prefix (nvb <= PER * 64 * FUSE_WAVES).
-template <int PER>
+template <int PER, int NP>
 struct DhSmem {
   static constexpr int NT = 64 * FUSE_WAVES;
+  static constexpr int SLOTS = FuseSlots<NP>::value;
   static_assert(PER * NT <= FUSE_MAX_NVB, "prefix arrays");
   int pre[PER * NT];    // prefix of the runs' lengths
   int lo_of[PER * NT];  // each run's first rank in its block
   int2 stage[NT];
   int2 lst[FUSE_WAVES][FUSE_CAP];
+  f32x4 part[SLOTS][NP * 64];  // one step's batch partials, [slot][p * 64 + lane]
   int wsum[FUSE_WAVES];
+  int nlist[FUSE_WAVES];       // entries in each row's list
+  int nbat[FUSE_WAVES];        // batches of each row to gather now
+  int full[2][FUSE_WAVES];     // a row's list could overflow (two buffers: no WAR barrier)
 };
+static_assert(sizeof(DhSmem<1, 3>) <= 40 * 1024, "four dH workgroups per CU at config 2's widths");
+
+// One batch's partial (entries e0 .. e0 + m - 1 of `list`), pass by pass: pass p goes to
+// dst[p * 64 + lane] (ADD = false) or is added to acc[p] (ADD = true).
+template <typename T, int NP, bool ADD>
+__device__ __forceinline__ void dh_batch(const T* __restrict__ W, const int2* list, int e0, int m,
+                                         int D, int lane, f32x4* dst, f32x4* acc) {
+  constexpr int U = FuseBatch<NP>::U;
+  constexpr int VMASK = (1 << FUSE_V_BITS) - 1;
+  f32x4 Pr[NP];  // ADD with two load groups: the partial between them
+#pragma unroll
+  for (int u0 = 0; u0 < DH_BATCH; u0 += U) {
+    Raw4<T> w[U][NP];
+    float g[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      // past the batch's last entry: reload that entry's row (a cache hit), unused
+      const int2 ent = list[e0 + min(u0 + u, m - 1)];
+      const int v = __builtin_amdgcn_readfirstlane(ent.x) & VMASK;  // uniform
+      g[u] = __int_as_float(__builtin_amdgcn_readfirstlane(ent.y));
+#pragma unroll
+      for (int p = 0; p < NP; ++p) {
+        const int d = p * 256 + lane * 4;
+        if (d < D) w[u][p].load(W + (int64_t)v * D + d);
+        else w[u][p].zero();
+      }
+    }
+    // One pass at a time, so that only one pass of the partial is held in registers when
+    // the batch is one load group.
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+      f32x4 P = u0 == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : (ADD ? Pr[p] : dst[p * 64 + lane]);
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+        if (u0 + u < m) fma4(P, g[u], w[u][p].f());  // uniform condition
+      if (!ADD) dst[p * 64 + lane] = P;
+      else if (u0 + U >= DH_BATCH) acc[p] += P;
+      else Pr[p] = P;
+    }
+  }
+}
+
+// The workgroup's gather of every listed batch of its rows (only the complete ones unless
+// `last`); row `wave`'s partials are added to acc in batch order, and the gathered entries
+// leave the lists (a row keeps its incomplete last batch). When one row holds more than
+// `share` times the batches per wave, the waves share them: SLOTS per step, each wave's
+// partial through LDS to the row's wave. Otherwise each wave gathers its own row.
+template <typename T, int NP, int PER>
+__device__ __forceinline__ void dh_gather(DhSmem<PER, NP>& sm, const T* __restrict__ W, int D,
+                                          int wave, int lane, int& n, bool last, int share,
+                                          f32x4* acc) {
+  constexpr int SLOTS = DhSmem<PER, NP>::SLOTS;
+  const int mine = last ? (n + DH_BATCH - 1) / DH_BATCH : n / DH_BATCH;
+  if (lane == 0) {
+    sm.nlist[wave] = n;
+    sm.nbat[wave] = mine;
+  }
+  __syncthreads();
+  int st[FUSE_WAVES + 1];  // first batch of each row in the workgroup's order (uniform)
+  st[0] = 0;
+  int most = 0;
+#pragma unroll
+  for (int w = 0; w < FUSE_WAVES; ++w) {
+    const int c = __builtin_amdgcn_readfirstlane(sm.nbat[w]);
+    st[w + 1] = st[w] + c;
+    most = max(most, c);
+  }
+  const int nb = st[FUSE_WAVES];
+  if (most > share * ((nb + SLOTS - 1) / SLOTS)) {
+    for (int t0 = 0; t0 < nb; t0 += SLOTS) {
+      const int q = t0 + wave;  // this wave's batch
+      if (wave < SLOTS && q < nb) {
+        int r = 0;
+#pragma unroll
+        for (int w = 1; w < FUSE_WAVES; ++w) r += q >= st[w] ? 1 : 0;
+        const int e0 = (q - st[r]) * DH_BATCH;
+        const int m = min(DH_BATCH, __builtin_amdgcn_readfirstlane(sm.nlist[r]) - e0);
+        dh_batch<T, NP, false>(W, sm.lst[r], e0, m, D, lane, sm.part[wave], acc);
+      }
+      __syncthreads();
+      // This wave's row: its batches among this step's, in order.
+      const int b0 = max(st[wave], t0), b1 = min(st[wave + 1], t0 + SLOTS);
+      for (int q2 = b0; q2 < b1; ++q2)
+#pragma unroll
+        for (int p = 0; p < NP; ++p) acc[p] += sm.part[q2 - t0][p * 64 + lane];
+      __syncthreads();  // the partials are rewritten next step
+    }
+  } else {
+    for (int k = 0; k < mine; ++k)
+      dh_batch<T, NP, true>(W, sm.lst[wave], k * DH_BATCH, min(DH_BATCH, n - k * DH_BATCH), D,
+                            lane, nullptr, acc);
+  }
+  // The row keeps only its incomplete batch (at most DH_BATCH - 1 entries).
+  const int taken = mine * DH_BATCH;
+  const int keep = max(0, n - taken);
+  int2 e = make_int2(0, 0);
+  if (lane < keep) e = sm.lst[wave][taken + lane];
+  if (lane < keep) sm.lst[wave][lane] = e;
+  n = keep;
+}
 
 // The workgroup for batch row b and xb = FUSE_HALVES * range + half.
 template <typename T, typename O, int NP, int PER>
-__device__ __forceinline__ void dh_fused_body(DhSmem<PER>& sm, const T* __restrict__ W,
+__device__ __forceinline__ void dh_fused_body(DhSmem<PER, NP>& sm, const T* __restrict__ W,
                                               const int2* __restrict__ comp,
                                               const int* __restrict__ cnt,
                                               const int* __restrict__ offs, O* __restrict__ dH,
-                                              int S, int D, int nvb, int64_t b, int xb) {
-  constexpr int NT = DhSmem<PER>::NT;
+                                              int S, int D, int nvb, int64_t b, int xb,
+                                              int share) {
+  constexpr int NT = DhSmem<PER, NP>::NT;
   int* pre = sm.pre;
   int* lo_of = sm.lo_of;
   int2* stage = sm.stage;
@@ -916,7 +1031,7 @@ __device__ __forceinline__ void dh_fused_body(DhSmem<PER>& sm, const T* __restri
   auto& lst = sm.lst;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int k = xb / FUSE_HALVES, nr = (S + FUSE_ROWS - 1) / FUSE_ROWS;
-  // >= S: no row (the wave still keeps the barriers)
+  // >= S: no row (the wave still keeps the barriers and helps gather)
   const int s = k * FUSE_ROWS + (xb % FUSE_HALVES) * FUSE_WAVES + wave;
   // Run of block `blk`: ranks [offs[k], offs[k+1]) (the last range ends at the count).
   int c[PER], sum = 0;
@@ -962,6 +1077,7 @@ __device__ __forceinline__ void dh_fused_body(DhSmem<PER>& sm, const T* __restri
 #pragma unroll
   for (int p = 0; p < NP; ++p) acc[p] = f32x4{0.f, 0.f, 0.f, 0.f};
   int n = 0;  // entries in this wave's list (uniform)
+  int par = 0;
   for (int t0 = 0; t0 < total; t0 += NT) {
     const int t = t0 + tid;
     if (t < total) {
@@ -982,14 +1098,21 @@ __device__ __forceinline__ void dh_fused_body(DhSmem<PER>& sm, const T* __restri
       const uint64_t bal = __ballot(mine);
       if (mine) lst[wave][n + __popcll(bal & ((1ull << lane) - 1ull))] = e;
       n += __popcll(bal);
-      if (n > FUSE_CAP - 64) {  // the next 64 could overflow: gather what is listed
-        gather_rows<T, NP>(W, lst[wave], n, D, lane, acc);
-        n = 0;
+      // If any row's list could overflow on the next 64 entries, gather the complete
+      // batches listed (workgroup-uniform decision).
+      if (i * 64 + 64 < here || t0 + NT < total) {
+        if (lane == 0) sm.full[par][wave] = n > FUSE_CAP - 64 ? 1 : 0;
+        __syncthreads();
+        int any = 0;
+#pragma unroll
+        for (int w = 0; w < FUSE_WAVES; ++w) any |= sm.full[par][w];
+        par ^= 1;
+        if (any) dh_gather<T, NP, PER>(sm, W, D, wave, lane, n, false, share, acc);
       }
     }
     __syncthreads();  // stage is refilled next round
   }
-  gather_rows<T, NP>(W, lst[wave], n, D, lane, acc);
+  dh_gather<T, NP, PER>(sm, W, D, wave, lane, n, true, share, acc);
   if (s < S) {
     O* out = dH + (b * S + s) * D;
 #pragma unroll
@@ -1011,20 +1134,20 @@ __global__ __launch_bounds__(64 * FUSE_WAVES) void bwd_fused_kernel(
     const void* __restrict__ mask, int mdt, const T* __restrict__ H, const T* __restrict__ W,
     const int2* __restrict__ comp, const int* __restrict__ cnt, const int* __restrict__ offs,
     O* __restrict__ dH, O* __restrict__ dW, O* __restrict__ dbias, int B, int S, int D, int V,
-    int nvb, int n_dh_x) {
+    int nvb, int n_dh_x, int share) {
   struct DwSmem {
     float gl[FUSE_DW_IDS * DW_LD];
     uint16_t sl[FUSE_DW_IDS * DW_LD];
   };
   union Smem {
-    DhSmem<PER> h;
+    DhSmem<PER, NP> h;
     DwSmem w;
   };
   __shared__ Smem sm;
   const int n_dh = n_dh_x * B;
   if ((int)blockIdx.x < n_dh) {  // workgroup-uniform
     dh_fused_body<T, O, NP, PER>(sm.h, W, comp, cnt, offs, dH, S, D, nvb, blockIdx.x / n_dh_x,
-                                 blockIdx.x % n_dh_x);
+                                 blockIdx.x % n_dh_x, share);
   } else {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int v0 = ((int)blockIdx.x - n_dh) * FUSE_DW_IDS;
@@ -1049,6 +1172,12 @@ static int dh_row_waves(int64_t rows, int np) {
   int rw = 1;
   while (rw < 8 && rows * rw < 1024 && 2 * rw * np <= 64) rw *= 2;
   return rw;
+}
+// Fused dH: a workgroup's waves share the gathering when one row holds more than this
+// many times the batches per wave (SPARTON_BWD_SHARE overrides it; tests use 0, always).
+static int dh_share() {
+  const char* e = getenv("SPARTON_BWD_SHARE");
+  return e != nullptr ? atoi(e) : 2;
 }
 // SPARTON_BWD_PATH=five forces the five-kernel path (tests compare the two paths).
 static bool fused_path_enabled() {
@@ -1083,7 +1212,7 @@ static void launch_rows(const T* g, const RT* r, const int32_t* idx, const void*
 #define FUSED(PER)                                                                                  \
   hipLaunchKernelGGL((bwd_fused_kernel<T, O, FNP, RT, PER>), grid, dim3(64 * FUSE_WAVES), 0, st, g,  \
                      r, idx, mask, mdt, H, W, (const int2*)comp, (const int*)cnt, (const int*)offs, \
-                     dH, dW, dbias, (int)B, (int)S, (int)D, (int)V, nvb, n_dh_x)
+                     dH, dW, dbias, (int)B, (int)S, (int)D, (int)V, nvb, n_dh_x, dh_share())
     if (nvb <= 64 * FUSE_WAVES) FUSED(1);
     else FUSED(FUSE_MAX_NVB / (64 * FUSE_WAVES));
 #undef FUSED
@@ -1139,7 +1268,7 @@ static void launch_rows(const T* g, const RT* r, const int32_t* idx, const void*
         else if (rw >= 4) DH_SPLIT(4);
         else if (rw >= 2) DH_SPLIT(2);
         else
-          hipLaunchKernelGGL((bwd_dh_kernel<T, O, NP>), dim3((unsigned)cdiv(nb * sw, 4)), dim3(256), 0,
+          hipLaunchKernelGGL((bwd_dh_kernel<T, O, DhPasses<NP>::value>), dim3((unsigned)cdiv(nb * sw, 4)), dim3(256), 0,
                              st, W, (const int2*)list, (const int*)seg_start, (const int*)seg_cnt, dhb,
                              (int)nb, (int)sw, (int)D, (int)V, (int)S);
 #undef DH_SPLIT

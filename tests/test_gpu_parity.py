@@ -233,6 +233,42 @@ def test_backward_paths_agree_bitwise(case, device, monkeypatch):
         assert torch.equal(a, c)
 
 
+@pytest.mark.parametrize("case", [
+    ("bf16", 32, 256, 768, 30522, True, "int64"),   # the headline shape
+    ("fp16", 8, 512, 768, 9000, False, "holes"),
+    ("fp32", 16, 70, 132, 900, True, "frac"),
+    ("bf16", 20, 64, 1280, 3000, True, "int64"),    # two-group batches (bf16 rows past 768)
+], ids=lambda c: "-".join(map(str, c)))
+def test_backward_hot_rows(case, device, monkeypatch):
+    """Rows that win most vocab ids (position 0 scaled up, like a [CLS] token): the fused
+    dH workgroup then shares the hot row's batches among its waves. Shared, per-row and
+    the automatic choice are bitwise equal, equal to the five-kernel path, and match
+    the oracle."""
+    say(f"hot dH rows, case {case}")
+    H, W, b, m, G = make_case(*case)
+    H[:, 0, :] *= 3.0
+    Hd, Wd, md, Gd = H.to(device), W.to(device), m.to(device), G.to(device)
+    bd = None if b is None else b.to(device)
+    _, idx, reps32 = torch.ops.sparton.fused_sparton_fwd_train(Hd, Wd, bd, md)
+    runs = {}
+    for mode in ("0", "1000", None):
+        if mode is None:
+            monkeypatch.delenv("SPARTON_BWD_SHARE", raising=False)
+        else:
+            monkeypatch.setenv("SPARTON_BWD_SHARE", mode)
+        runs[mode] = [t.clone() for t in torch.ops.sparton.fused_sparton_bwd(Gd, reps32, idx, Hd, Wd, bd, md)]
+    monkeypatch.setenv("SPARTON_BWD_PATH", "five")
+    five = torch.ops.sparton.fused_sparton_bwd(Gd, reps32, idx, Hd, Wd, bd, md)
+    torch.cuda.synchronize()
+    hot = int(torch.bincount(idx[:1].flatten().long().cpu()).max())
+    say(f"  row 0's most-won position holds {hot} vocab ids")
+    for out in list(runs.values())[1:] + [five]:
+        for a, c in zip(runs["0"], out):
+            assert (a is None and c is None) or torch.equal(a, c)
+    dH, dW, db = runs[None]
+    check_bwd_isolated(H, W, b, m, G, reps32, idx, dH, dW, db)
+
+
 def test_graph_capture_replays(device):
     """Forward and backward captured into one HIP graph (all of their kernels and workspace
     allocations) replay to the eager results, bitwise, with eager work and synchronizations
