@@ -390,15 +390,6 @@ template <> struct Raw4<f16> {
 // and the five-kernel path agree bitwise.
 constexpr int DH_BATCH = 4;
 
-// Rows gathered per batch: all their loads are in flight together (about 24 per lane).
-template <int NP> struct Batch { static constexpr int U = NP <= 3 ? 8 : NP <= 6 ? 4 : NP <= 8 ? 3 : 2; };
-// bwd_dh_kernel takes at most DH_MAX_NP register passes (wider rows loop over D) and
-// whole DH_BATCH-entry batches per load group.
-constexpr int DH_MAX_NP = 8;
-template <int NP> struct DhPasses { static constexpr int value = NP < DH_MAX_NP ? NP : DH_MAX_NP; };
-template <int NP> struct DhBatch { static constexpr int U = NP <= 3 ? 8 : 4; };
-static_assert(DhBatch<1>::U % DH_BATCH == 0 && DhBatch<DH_MAX_NP>::U % DH_BATCH == 0, "whole batches");
-
 // P = fma(g, w, P) per element, written out so that every dH kernel rounds the same way.
 __device__ __forceinline__ void fma4(f32x4& P, float g, const f32x4& w) {
   P[0] = __builtin_fmaf(g, w[0], P[0]);
@@ -406,6 +397,64 @@ __device__ __forceinline__ void fma4(f32x4& P, float g, const f32x4& w) {
   P[2] = __builtin_fmaf(g, w[2], P[2]);
   P[3] = __builtin_fmaf(g, w[3], P[3]);
 }
+
+// Rows gathered per batch: all their loads are in flight together (about 24 per lane).
+template <int NP> struct Batch { static constexpr int U = NP <= 3 ? 8 : NP <= 6 ? 4 : NP <= 8 ? 3 : 2; };
+// bwd_dh_kernel takes at most DH_MAX_NP register passes (wider rows loop over D) and
+// whole DH_BATCH-entry batches per load group: U rows while at least U entries are left
+// in the 64-entry chunk, US rows otherwise. Its gathers are chains of round trips, so
+// for long rows more rows in flight beat occupancy; LONG is chosen for large vocabularies
+// (V > FUSE_V_FAST), where rows hold many entries. Measured (dH alone incl. its bucketing):
+// config 4 (V = 250002, 16-bit D = 768, ~49 entries per row) U = 8 vs 32: 279 vs 233 us;
+// config 5 (D = 4096, 8 passes) U = 4 vs 8: 233 vs 218 us; short rows (config 2 on this
+// path) lose 3 us with U = 32 (fewer waves in flight).
+constexpr int DH_MAX_NP = 8;
+template <int NP> struct DhPasses { static constexpr int value = NP < DH_MAX_NP ? NP : DH_MAX_NP; };
+template <typename T, int NP, bool LONG> struct DhBatch {
+  static constexpr bool B16 = sizeof(T) == 2;
+  static constexpr int U = NP <= 3 ? (LONG && B16 ? 32 : 8) : (LONG && B16 ? 8 : 4);
+  static constexpr int US = NP <= 3 ? 8 : 4;
+};
+static_assert(DhBatch<bf16, 1, true>::US % DH_BATCH == 0 && DhBatch<float, DH_MAX_NP, false>::U % DH_BATCH == 0,
+              "whole batches");
+
+// One load group of bwd_dh_kernel: entries j .. j + U - 1 of the chunk held one per lane
+// in ent (n of them valid), their W rows loaded together, then summed as DH_BATCH-entry
+// partials, one pass at a time (so that only one pass of a partial is held in registers).
+template <typename T, int NP, int U>
+__device__ __forceinline__ void dh_group(const T* __restrict__ W, int2 ent, int j, int n, int d0,
+                                         int D, int lane, f32x4* acc) {
+  Raw4<T> w[U][NP];
+  float g[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    // past the segment end: reload the last entry's row (a cache hit) with g' = 0,
+    // which keeps the batch free of branches so all its loads issue together
+    const int jj = min(j + u, n - 1);
+    const int v = __builtin_amdgcn_readlane(ent.x, jj);
+    g[u] = j + u < n ? __int_as_float(__builtin_amdgcn_readlane(ent.y, jj)) : 0.0f;
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+      const int d = d0 + p * 256 + lane * 4;
+      if (d < D) w[u][p].load(W + (int64_t)v * D + d);
+      else w[u][p].zero();
+    }
+  }
+#pragma unroll
+  for (int p = 0; p < NP; ++p) {
+#pragma unroll
+    for (int a = 0; a < U; a += DH_BATCH) {
+      if (j + a < n) {  // uniform: the batch exists
+        f32x4 P = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int u = a; u < a + DH_BATCH; ++u)
+          if (j + u < n) fma4(P, g[u], w[u][p].f());
+        acc[p] += P;
+      }
+    }
+  }
+}
+
 
 // The staged dW kernel gathers the rows of IDC of a wave's ids together, U rows at a
 // time. For 16-bit rows of up to 768 elements one id and 4 rows keep it within 64 VGPRs:
@@ -424,14 +473,14 @@ template <typename T, int NP> struct DwPasses {
 
 // ---- 4. dH ---------------------------------------------------------------------
 // One wave per (b,s) row; lane l owns elements d0 + p*256 + 4l .. +3 for p < NP. The
-// segment's entries sit one per lane; they are taken U at a time (a uniform loop, so
-// the summation order is the segment's v order), all U*NP loads are issued, then the
-// U rows are accumulated.
-template <typename T, typename O, int NP>
+// segment's entries sit one per lane; they are taken U (or US) at a time (a uniform
+// loop, so the summation order is the segment's v order), all loads of a group are
+// issued, then its rows are accumulated.
+template <typename T, typename O, int NP, bool LONG>
 __global__ __launch_bounds__(256) void bwd_dh_kernel(
     const T* __restrict__ W, const int2* __restrict__ list, const int* __restrict__ seg_start,
     const int* __restrict__ seg_cnt, O* __restrict__ dH, int B, int S, int D, int V, int S_row) {
-  constexpr int U = DhBatch<NP>::U;
+  constexpr int U = DhBatch<T, NP, LONG>::U, US = DhBatch<T, NP, LONG>::US;
   static_assert(NP <= DH_MAX_NP, "register passes");
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * 4 + wave;
@@ -447,39 +496,12 @@ __global__ __launch_bounds__(256) void bwd_dh_kernel(
     for (int e0 = 0; e0 < cnt; e0 += 64) {
       const int2 ent = e0 + lane < cnt ? seg[e0 + lane] : make_int2(0, 0);
       const int n = min(64, cnt - e0);
-      for (int j = 0; j < n; j += U) {
-        Raw4<T> w[U][NP];
-        float g[U];
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-          // past the segment end: reload the last entry's row (a cache hit) with g' = 0,
-          // which keeps the batch free of branches so all its loads issue together
-          const int jj = min(j + u, n - 1);
-          const int v = __builtin_amdgcn_readlane(ent.x, jj);
-          g[u] = j + u < n ? __int_as_float(__builtin_amdgcn_readlane(ent.y, jj)) : 0.0f;
-#pragma unroll
-          for (int p = 0; p < NP; ++p) {
-            const int d = d0 + p * 256 + lane * 4;
-            if (d < D) w[u][p].load(W + (int64_t)v * D + d);
-            else w[u][p].zero();
-          }
-        }
-        // Whole batches (chunks of 64 and j are multiples of DH_BATCH), one pass at a
-        // time, so only one pass of a partial is held in registers.
-#pragma unroll
-        for (int p = 0; p < NP; ++p) {
-#pragma unroll
-          for (int a = 0; a < U; a += DH_BATCH) {
-            if (j + a < n) {  // uniform: the batch exists
-              f32x4 P = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-              for (int u = a; u < a + DH_BATCH; ++u)
-                if (j + u < n) fma4(P, g[u], w[u][p].f());
-              acc[p] += P;
-            }
-          }
-        }
+      // j stays a multiple of DH_BATCH (chunks of 64 too): whole batches per group.
+      int j = 0;
+      if constexpr (U > US) {
+        for (; j + U <= n; j += U) dh_group<T, NP, U>(W, ent, j, n, d0, D, lane, acc);
       }
+      for (; j < n; j += US) dh_group<T, NP, US>(W, ent, j, n, d0, D, lane, acc);
     }
     O* out = dH + (b * S_row + (row - b * S)) * D;
 #pragma unroll
@@ -1179,6 +1201,12 @@ static int dh_share() {
   const char* e = getenv("SPARTON_BWD_SHARE");
   return e != nullptr ? atoi(e) : 2;
 }
+// The five-kernel dH takes its long-row load groups for large vocabularies
+// (SPARTON_BWD_DH_LONG=1 forces them; tests compare the two).
+static bool dh_long_rows(int64_t V) {
+  const char* e = getenv("SPARTON_BWD_DH_LONG");
+  return V > FUSE_V_FAST || (e != nullptr && strcmp(e, "1") == 0);
+}
 // SPARTON_BWD_PATH=five forces the five-kernel path (tests compare the two paths).
 static bool fused_path_enabled() {
   const char* e = getenv("SPARTON_BWD_PATH");
@@ -1267,10 +1295,14 @@ static void launch_rows(const T* g, const RT* r, const int32_t* idx, const void*
         if (rw >= 8) DH_SPLIT(8);
         else if (rw >= 4) DH_SPLIT(4);
         else if (rw >= 2) DH_SPLIT(2);
+        else if (dh_long_rows(V))
+          hipLaunchKernelGGL((bwd_dh_kernel<T, O, DhPasses<NP>::value, true>), dim3((unsigned)cdiv(nb * sw, 4)),
+                             dim3(256), 0, st, W, (const int2*)list, (const int*)seg_start,
+                             (const int*)seg_cnt, dhb, (int)nb, (int)sw, (int)D, (int)V, (int)S);
         else
-          hipLaunchKernelGGL((bwd_dh_kernel<T, O, DhPasses<NP>::value>), dim3((unsigned)cdiv(nb * sw, 4)), dim3(256), 0,
-                             st, W, (const int2*)list, (const int*)seg_start, (const int*)seg_cnt, dhb,
-                             (int)nb, (int)sw, (int)D, (int)V, (int)S);
+          hipLaunchKernelGGL((bwd_dh_kernel<T, O, DhPasses<NP>::value, false>), dim3((unsigned)cdiv(nb * sw, 4)),
+                             dim3(256), 0, st, W, (const int2*)list, (const int*)seg_start,
+                             (const int*)seg_cnt, dhb, (int)nb, (int)sw, (int)D, (int)V, (int)S);
 #undef DH_SPLIT
       }
     }

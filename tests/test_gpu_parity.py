@@ -217,7 +217,8 @@ def test_deterministic_repeat(device):
 ], ids=lambda c: "-".join(map(str, c)))
 def test_backward_paths_agree_bitwise(case, device, monkeypatch):
     """The fused backward (entries compacted by the dW kernel) and the five-kernel one
-    (count, scan, scatter) sum every gradient in the same order: bitwise equal. (Shapes
+    (count, scan, scatter; with either dH load-group size) sum every gradient in the same
+    order: bitwise equal. (Shapes
     where the fused path is taken: >= 64 row ranges, and >= 1024 rows, so that the
     five-kernel path also gives each dH row one wave.)"""
     say(f"backward paths, case {case}")
@@ -227,10 +228,12 @@ def test_backward_paths_agree_bitwise(case, device, monkeypatch):
     _, idx, reps32 = torch.ops.sparton.fused_sparton_fwd_train(Hd, Wd, bd, md)
     fused = [t.clone() for t in torch.ops.sparton.fused_sparton_bwd_train(Gd, reps32, idx, Hd, Wd, bd, md)]
     monkeypatch.setenv("SPARTON_BWD_PATH", "five")
-    five = torch.ops.sparton.fused_sparton_bwd_train(Gd, reps32, idx, Hd, Wd, bd, md)
+    five = [t.clone() for t in torch.ops.sparton.fused_sparton_bwd_train(Gd, reps32, idx, Hd, Wd, bd, md)]
+    monkeypatch.setenv("SPARTON_BWD_DH_LONG", "1")  # the large-vocabulary load groups
+    five_long = torch.ops.sparton.fused_sparton_bwd_train(Gd, reps32, idx, Hd, Wd, bd, md)
     torch.cuda.synchronize()
-    for a, c in zip(fused, five):
-        assert torch.equal(a, c)
+    for a, c, d in zip(fused, five, five_long):
+        assert torch.equal(a, c) and torch.equal(a, d)
 
 
 @pytest.mark.parametrize("case", [
