@@ -335,20 +335,31 @@ __global__ __launch_bounds__(256) void bwd_scatter_kernel(
   const int32_t* ib = idx + (int64_t)b * V;
   const uint64_t lt = (1ull << lane) - 1ull;
   const int sbits = S > 1 ? 32 - __builtin_clz((unsigned)(S - 1)) : 0;
-  for (int i0 = 0; i0 < n; i0 += 64) {
-    const bool act = i0 + lane < n;
-    const int2 e = cb[act ? i0 + lane : 0];
-    const int s = act ? ib[e.x] - s0 : 0;  // compacted entries lie in the window
-    const uint64_t act_mask = __ballot(act);
-    uint64_t same = act_mask;
-    for (int k = 0; k < sbits; ++k) {
-      const bool bit = ((s >> k) & 1) != 0;
-      const uint64_t ones = __ballot(bit);
-      same &= bit ? ones : ~ones;
+  // SCATTER_AHEAD rounds of 64 entries at a time: their entries, then their indices
+  // (one dependent round trip each, all rounds' loads in flight together).
+  constexpr int SCATTER_AHEAD = 4;
+  for (int i0 = 0; i0 < n; i0 += 64 * SCATTER_AHEAD) {
+    int2 e[SCATTER_AHEAD];
+    int s[SCATTER_AHEAD];
+#pragma unroll
+    for (int r = 0; r < SCATTER_AHEAD; ++r) e[r] = cb[min(i0 + r * 64 + lane, max(n - 1, 0))];
+#pragma unroll
+    for (int r = 0; r < SCATTER_AHEAD; ++r) s[r] = ib[e[r].x] - s0;  // entries lie in the window
+#pragma unroll
+    for (int r = 0; r < SCATTER_AHEAD; ++r) {
+      const bool act = i0 + r * 64 + lane < n;
+      uint64_t same = __ballot(act);
+      if (same == 0) break;  // uniform: no entries left
+      const int sr = act ? s[r] : 0;
+      for (int k = 0; k < sbits; ++k) {
+        const bool bit = ((sr >> k) & 1) != 0;
+        const uint64_t ones = __ballot(bit);
+        same &= bit ? ones : ~ones;
+      }
+      const int base = act ? cur[sr] : 0;
+      if (act) lb[base + __popcll(same & lt)] = e[r];
+      if (act && (same & lt) == 0) cur[sr] = base + __popcll(same);
     }
-    const int base = act ? cur[s] : 0;
-    if (act) lb[base + __popcll(same & lt)] = e;
-    if (act && (same & lt) == 0) cur[s] = base + __popcll(same);
   }
 }
 
@@ -512,73 +523,56 @@ __global__ __launch_bounds__(256) void bwd_dh_kernel(
   }
 }
 
-// Few rows (B*S small, e.g. 2 x 32 with every v active): one workgroup of RW waves per
-// row instead of one wave. Wave w sums entries [w c, (w + 1) c) of the row's segment
-// (c = ceil(cnt / RW)) in v order, as bwd_dh_kernel does, and wave 0 adds the RW partial
-// rows in wave order through LDS: deterministic, and RW times the gathers in flight.
-template <int NP> struct SplitLds { static constexpr int floats = NP * 256; };
-// RW clamped to the LDS budget (RW * NP KB <= 64 KB), as dh_row_waves chooses it.
-template <int NP, int RW> struct SplitRW {
-  static constexpr int value = RW * NP <= 64 ? RW : SplitRW<NP, RW / 2>::value;
-};
-template <int NP> struct SplitRW<NP, 1> { static constexpr int value = 1; };
-template <typename T, typename O, int NP, int RW>
-__global__ __launch_bounds__(64 * RW) void bwd_dh_split_kernel(
+// Few rows (B*S < SPLIT_ROWS, e.g. 2 x 32 with every v active): one workgroup of
+// SPLIT_WAVES waves per (row, 256-column slice of D) instead of one wave per row, so that
+// even a handful of rows keeps thousands of waves gathering. Wave w sums entries
+// [w c, (w + 1) c) of the row's segment (c = ceil(cnt / SPLIT_WAVES)) in v order over its
+// slice, and wave 0 adds the partial slices in wave order through LDS: deterministic
+// (each element's sum does not depend on the slicing).
+constexpr int SPLIT_WAVES = 8;
+constexpr int SPLIT_ROWS = 1024;
+constexpr int SPLIT_U = 16;  // rows gathered per batch (one 256-column slice each)
+template <typename T, typename O>
+__global__ __launch_bounds__(64 * SPLIT_WAVES) void bwd_dh_split_kernel(
     const T* __restrict__ W, const int2* __restrict__ list, const int* __restrict__ seg_start,
-    const int* __restrict__ seg_cnt, O* __restrict__ dH, int B, int S, int D, int V, int S_row) {
-  constexpr int U = Batch<NP>::U;
-  __shared__ __attribute__((aligned(16))) float red[RW][SplitLds<NP>::floats];
+    const int* __restrict__ seg_cnt, O* __restrict__ dH, int B, int S, int D, int V, int S_row,
+    int ns) {
+  __shared__ __attribute__((aligned(16))) float red[SPLIT_WAVES][256];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int64_t row = blockIdx.x;  // grid = B * S exactly
+  const int64_t row = blockIdx.x / ns;  // grid = B * S * ns exactly
+  const int d = (int)(blockIdx.x % ns) * 256 + lane * 4;
   const int64_t b = row / S;
   const int start = __builtin_amdgcn_readfirstlane(seg_start[row]);
   const int cnt = __builtin_amdgcn_readfirstlane(seg_cnt[row]);
-  const int per = (cnt + RW - 1) / RW;
+  const int per = (cnt + SPLIT_WAVES - 1) / SPLIT_WAVES;
   const int e_beg = min(cnt, wave * per), e_end = min(cnt, e_beg + per);
   const int2* seg = list + b * V + start;
-  for (int d0 = 0; d0 < D; d0 += NP * 256) {
-    f32x4 acc[NP];
+  f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int e0 = e_beg; e0 < e_end; e0 += 64) {
+    const int2 ent = e0 + lane < e_end ? seg[e0 + lane] : make_int2(0, 0);
+    const int n = min(64, e_end - e0);
+    for (int j = 0; j < n; j += SPLIT_U) {
+      Raw4<T> w[SPLIT_U];
+      float g[SPLIT_U];
 #pragma unroll
-    for (int p = 0; p < NP; ++p) acc[p] = f32x4{0.f, 0.f, 0.f, 0.f};
-    for (int e0 = e_beg; e0 < e_end; e0 += 64) {
-      const int2 ent = e0 + lane < e_end ? seg[e0 + lane] : make_int2(0, 0);
-      const int n = min(64, e_end - e0);
-      for (int j = 0; j < n; j += U) {
-        Raw4<T> w[U][NP];
-        float g[U];
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-          const int jj = min(j + u, n - 1);
-          const int v = __builtin_amdgcn_readlane(ent.x, jj);
-          g[u] = j + u < n ? __int_as_float(__builtin_amdgcn_readlane(ent.y, jj)) : 0.0f;
-#pragma unroll
-          for (int p = 0; p < NP; ++p) {
-            const int d = d0 + p * 256 + lane * 4;
-            if (d < D) w[u][p].load(W + (int64_t)v * D + d);
-            else w[u][p].zero();
-          }
-        }
-#pragma unroll
-        for (int u = 0; u < U; ++u)
-#pragma unroll
-          for (int p = 0; p < NP; ++p) acc[p] += g[u] * w[u][p].f();
+      for (int u = 0; u < SPLIT_U; ++u) {
+        const int jj = min(j + u, n - 1);
+        const int v = __builtin_amdgcn_readlane(ent.x, jj);
+        g[u] = j + u < n ? __int_as_float(__builtin_amdgcn_readlane(ent.y, jj)) : 0.0f;
+        if (d < D) w[u].load(W + (int64_t)v * D + d);
+        else w[u].zero();
       }
+#pragma unroll
+      for (int u = 0; u < SPLIT_U; ++u) acc += g[u] * w[u].f();
     }
+  }
+  *(f32x4*)&red[wave][lane * 4] = acc;
+  __syncthreads();
+  if (wave == 0) {
+    f32x4 t = *(const f32x4*)&red[0][lane * 4];
 #pragma unroll
-    for (int p = 0; p < NP; ++p) *(f32x4*)&red[wave][p * 256 + lane * 4] = acc[p];
-    __syncthreads();
-    if (wave == 0) {
-      O* out = dH + (b * S_row + (row - b * S)) * D;
-#pragma unroll
-      for (int p = 0; p < NP; ++p) {
-        f32x4 t = *(const f32x4*)&red[0][p * 256 + lane * 4];
-#pragma unroll
-        for (int w = 1; w < RW; ++w) t += *(const f32x4*)&red[w][p * 256 + lane * 4];
-        const int d = d0 + p * 256 + lane * 4;
-        if (d < D) store4(out + d, t);
-      }
-    }
-    __syncthreads();  // red is refilled by the next D chunk
+    for (int w = 1; w < SPLIT_WAVES; ++w) t += *(const f32x4*)&red[w][lane * 4];
+    if (d < D) store4(dH + (b * S_row + (row - b * S)) * D + d, t);
   }
 }
 
@@ -1187,14 +1181,6 @@ static int passes_for(int64_t D) {
   return (int)std::min<int64_t>(MAX_NP, std::max<int64_t>(1, cdiv(D, 256)));
 }
 
-// Waves per dH row of the five-kernel path: enough to keep ~1024 waves gathering when
-// there are few rows (1 from 1024 rows up), at most 8 (512-thread workgroups: fp32 rows
-// keep their gather batch in registers), within 64 KB of LDS for the partial rows.
-static int dh_row_waves(int64_t rows, int np) {
-  int rw = 1;
-  while (rw < 8 && rows * rw < 1024 && 2 * rw * np <= 64) rw *= 2;
-  return rw;
-}
 // Fused dH: a workgroup's waves share the gathering when one row holds more than this
 // many times the batches per wave (SPARTON_BWD_SHARE overrides it; tests use 0, always).
 static int dh_share() {
@@ -1286,16 +1272,13 @@ static void launch_rows(const T* g, const RT* r, const int32_t* idx, const void*
           hipLaunchKernelGGL(bwd_scatter_kernel, cgrid, dim3(64 * wpb), (size_t)sw * 4 * wpb, st, ib,
                              (int)sw, (int)V, (int)L.nch, (const int*)hist, (const int2*)comp,
                              (const int*)ccount, list, (int)s0);
-        const int rw = dh_row_waves(nb * sw, NP);
-#define DH_SPLIT(RW)                                                                             \
-  hipLaunchKernelGGL((bwd_dh_split_kernel<T, O, NP, SplitRW<NP, RW>::value>),                    \
-                     dim3((unsigned)(nb * sw)), dim3(64 * SplitRW<NP, RW>::value), 0, st, W,     \
-                     (const int2*)list, (const int*)seg_start, (const int*)seg_cnt, dhb, (int)nb, \
-                     (int)sw, (int)D, (int)V, (int)S)
-        if (rw >= 8) DH_SPLIT(8);
-        else if (rw >= 4) DH_SPLIT(4);
-        else if (rw >= 2) DH_SPLIT(2);
-        else if (dh_long_rows(V))
+        if (nb * sw < SPLIT_ROWS) {
+          const int64_t ns = cdiv(D, 256);
+          hipLaunchKernelGGL((bwd_dh_split_kernel<T, O>), dim3((unsigned)(nb * sw * ns)),
+                             dim3(64 * SPLIT_WAVES), 0, st, W, (const int2*)list,
+                             (const int*)seg_start, (const int*)seg_cnt, dhb, (int)nb, (int)sw,
+                             (int)D, (int)V, (int)S, (int)ns);
+        } else if (dh_long_rows(V))
           hipLaunchKernelGGL((bwd_dh_kernel<T, O, DhPasses<NP>::value, true>), dim3((unsigned)cdiv(nb * sw, 4)),
                              dim3(256), 0, st, W, (const int2*)list, (const int*)seg_start,
                              (const int*)seg_cnt, dhb, (int)nb, (int)sw, (int)D, (int)V, (int)S);
@@ -1303,7 +1286,6 @@ static void launch_rows(const T* g, const RT* r, const int32_t* idx, const void*
           hipLaunchKernelGGL((bwd_dh_kernel<T, O, DhPasses<NP>::value, false>), dim3((unsigned)cdiv(nb * sw, 4)),
                              dim3(256), 0, st, W, (const int2*)list, (const int*)seg_start,
                              (const int*)seg_cnt, dhb, (int)nb, (int)sw, (int)D, (int)V, (int)S);
-#undef DH_SPLIT
       }
     }
   }
