@@ -51,7 +51,7 @@ constexpr int MAX_NP = 16;         // D up to 16 * 256 per register pass
 
 struct Layout {
   int64_t nch;
-  size_t hist, seg_start, seg_cnt, list, comp, ccount, cnt64, off64, total;  // hist: [B][nch][S] int32
+  size_t hist, seg_start, seg_cnt, list, comp, ccount, cnt64, off64, hot, total;  // hist: [B][nch][S] int32
 };
 
 static Layout layout(int64_t B, int64_t S, int64_t V) {
@@ -66,6 +66,7 @@ static Layout layout(int64_t B, int64_t S, int64_t V) {
   L.list = take((size_t)(B * round_up(V, 64)) * 8);
   L.comp = take((size_t)(B * L.nch * CHW) * 8);  // [B][nch][CHW] active (v, g') per chunk
   L.ccount = take((size_t)(B * L.nch) * 4);      // [B][nch] their number
+  L.hot = take((size_t)(B * S + 1) * 4);          // [0]: hot rows; [1 ..]: their (b * S + s)
   L.cnt64 = take((size_t)(B * cdiv(V, 64)) * 4);  // fused path: [B][V/64] entries per block
   L.off64 = take((size_t)(B * cdiv(V, 64) * cdiv(std::min<int64_t>(S, 1024), 16)) * 4);  // and per row range
   L.total = off;
@@ -144,8 +145,10 @@ template <typename T, typename RT>
 __global__ __launch_bounds__(256) void bwd_count_kernel(
     const T* __restrict__ grad, const RT* __restrict__ reps, const int32_t* __restrict__ idx,
     const void* __restrict__ mask, int mdt, int S, int V, int nch, int* __restrict__ hist,
-    int2* __restrict__ comp, int* __restrict__ ccount, int s0, int64_t mrow0, int S_row) {
+    int2* __restrict__ comp, int* __restrict__ ccount, int s0, int64_t mrow0, int S_row,
+    int* __restrict__ hot) {
   float* maskf = (float*)sparton_bwd_smem;
+  if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) hot[0] = 0;  // the scan lists them
   const int wpb = blockDim.x >> 6, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   int* h = (int*)(maskf + S) + wave * S;
   const int b = blockIdx.y, c = blockIdx.x * wpb + wave;
@@ -190,10 +193,17 @@ constexpr int SCAN_BATCH = 8;  // chunk counts loaded together
 // One workgroup per batch row, threads over s: thread s sums its chunks' counts
 // hist[b][c][s] (coalesced across threads), a block scan over s gives the segment
 // starts, and a second pass rewrites each count as its chunk's first slot.
+// Both scans also list the rows with more than hot_min entries (hot[0] counts them, set
+// to 0 by the count kernel; integer atomics, so only the list's order varies).
+__device__ __forceinline__ void list_hot_row(int* hot, int hot_min, int64_t row, int cnt) {
+  if (cnt > hot_min) hot[1 + atomicAdd(&hot[0], 1)] = (int)row;
+}
+
 __global__ __launch_bounds__(SCAN_THREADS) void bwd_scan_kernel(int* __restrict__ hist,
                                                                 int* __restrict__ seg_start,
                                                                 int* __restrict__ seg_cnt, int S,
-                                                                int nch) {
+                                                                int nch, int* __restrict__ hot,
+                                                                int hot_min) {
   __shared__ int wsum[SCAN_THREADS / 64];
   __shared__ int carry;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -226,6 +236,7 @@ __global__ __launch_bounds__(SCAN_THREADS) void bwd_scan_kernel(int* __restrict_
     if (in) {
       seg_start[b * S + s] = run;
       seg_cnt[b * S + s] = tot;
+      list_hot_row(hot, hot_min, b * S + s, tot);
     }
     for (int c0 = 0; c0 < nch; c0 += SCAN_BATCH) {
       int x[SCAN_BATCH];
@@ -252,7 +263,9 @@ __global__ __launch_bounds__(SCAN_THREADS) void bwd_scan_kernel(int* __restrict_
 __global__ __launch_bounds__(SCAN_THREADS) void bwd_scan_parts_kernel(int* __restrict__ hist,
                                                                       int* __restrict__ seg_start,
                                                                       int* __restrict__ seg_cnt,
-                                                                      int S, int nch, int Sr) {
+                                                                      int S, int nch, int Sr,
+                                                                      int* __restrict__ hot,
+                                                                      int hot_min) {
   __shared__ int ptot[SCAN_THREADS];
   __shared__ int base[SCAN_THREADS];
   __shared__ int wsum[SCAN_THREADS / 64];
@@ -293,6 +306,7 @@ __global__ __launch_bounds__(SCAN_THREADS) void bwd_scan_parts_kernel(int* __res
     if (in) {
       seg_start[b * S + s] = run;
       seg_cnt[b * S + s] = t;
+      list_hot_row(hot, hot_min, b * S + s, t);
     }
     base[s] = run;
   }
@@ -490,7 +504,8 @@ template <typename T, int NP> struct DwPasses {
 template <typename T, typename O, int NP, bool LONG>
 __global__ __launch_bounds__(256) void bwd_dh_kernel(
     const T* __restrict__ W, const int2* __restrict__ list, const int* __restrict__ seg_start,
-    const int* __restrict__ seg_cnt, O* __restrict__ dH, int B, int S, int D, int V, int S_row) {
+    const int* __restrict__ seg_cnt, O* __restrict__ dH, int B, int S, int D, int V, int S_row,
+    int hot_min) {
   constexpr int U = DhBatch<T, NP, LONG>::U, US = DhBatch<T, NP, LONG>::US;
   static_assert(NP <= DH_MAX_NP, "register passes");
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -499,6 +514,7 @@ __global__ __launch_bounds__(256) void bwd_dh_kernel(
   const int64_t b = row / S;
   const int start = __builtin_amdgcn_readfirstlane(seg_start[row]);
   const int cnt = __builtin_amdgcn_readfirstlane(seg_cnt[row]);
+  if (cnt > hot_min) return;  // bwd_dh_hot_kernel writes this row
   const int2* seg = list + b * V + start;
   for (int d0 = 0; d0 < D; d0 += NP * 256) {
     f32x4 acc[NP];
@@ -520,6 +536,71 @@ __global__ __launch_bounds__(256) void bwd_dh_kernel(
       const int d = d0 + p * 256 + lane * 4;
       if (d < D) store4(out + d, acc[p]);
     }
+  }
+}
+
+// Hot rows (more than hot_min entries, e.g. a position that wins most vocab ids; at
+// config 4, V = 250002, rows hold ~49 entries and up to 776): one wave per row would
+// gather them alone. Measured at config 4, backward with HOT_MIN = 64 / 128 / 256 / 512 /
+// off: 341 / 342 / 369 / 398 / 390 us; configs 1, 2, 3 (five-kernel) and 5 unchanged. Here a workgroup of HOT_WAVES waves takes one
+// (hot row, 256-column slice) at a time from the list the scan built (a grid of fixed
+// size walks the list). Each step its waves compute HOT_PER_WAVE consecutive batch
+// partials each (the DH_BATCH-entry partials of bwd_dh_kernel, over the slice) into LDS,
+// and wave 0 adds them in batch order: the same sums as bwd_dh_kernel, bitwise.
+constexpr int HOT_MIN = 128;
+constexpr int HOT_WAVES = 16;
+constexpr int HOT_PER_WAVE = 2;
+constexpr int HOT_STEP = HOT_WAVES * HOT_PER_WAVE;  // batches per step
+constexpr int HOT_GRID = 512;
+template <typename T, typename O>
+__global__ __launch_bounds__(64 * HOT_WAVES) void bwd_dh_hot_kernel(
+    const T* __restrict__ W, const int2* __restrict__ list, const int* __restrict__ seg_start,
+    const int* __restrict__ seg_cnt, const int* __restrict__ hot, O* __restrict__ dH, int S,
+    int D, int V, int S_row, int ns) {
+  __shared__ f32x4 part[HOT_STEP][64];
+  constexpr int U = HOT_PER_WAVE * DH_BATCH;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int n_items = __builtin_amdgcn_readfirstlane(hot[0]) * ns;
+  for (int item = blockIdx.x; item < n_items; item += gridDim.x) {
+    const int64_t row = __builtin_amdgcn_readfirstlane(hot[1 + item / ns]);
+    const int d = (item % ns) * 256 + lane * 4;
+    const int64_t b = row / S;
+    const int start = __builtin_amdgcn_readfirstlane(seg_start[row]);
+    const int cnt = __builtin_amdgcn_readfirstlane(seg_cnt[row]);
+    const int2* seg = list + b * V + start;
+    const int nbat = (cnt + DH_BATCH - 1) / DH_BATCH;
+    f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int t0 = 0; t0 < nbat; t0 += HOT_STEP) {
+      const int e0 = (t0 + wave * HOT_PER_WAVE) * DH_BATCH;  // this wave's first entry
+      if (e0 < cnt) {  // uniform
+        const int2 ent = lane < U ? seg[min(e0 + lane, cnt - 1)] : make_int2(0, 0);
+        Raw4<T> w[U];
+        float g[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          // past the row's last entry: reload that entry's row (a cache hit), unused
+          const int v = __builtin_amdgcn_readlane(ent.x, u);
+          g[u] = __int_as_float(__builtin_amdgcn_readlane(ent.y, u));
+          if (d < D) w[u].load(W + (int64_t)v * D + d);
+          else w[u].zero();
+        }
+#pragma unroll
+        for (int h = 0; h < HOT_PER_WAVE; ++h) {
+          f32x4 P = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int u = h * DH_BATCH; u < (h + 1) * DH_BATCH; ++u)
+            if (e0 + u < cnt) fma4(P, g[u], w[u].f());  // uniform condition
+          part[wave * HOT_PER_WAVE + h][lane] = P;
+        }
+      }
+      __syncthreads();
+      if (wave == 0) {
+        const int m = min(HOT_STEP, nbat - t0);
+        for (int j = 0; j < m; ++j) acc += part[j][lane];
+      }
+      __syncthreads();  // the partials are rewritten next step
+    }
+    if (wave == 0 && d < D) store4(dH + (b * S_row + (row - b * S)) * D + d, acc);
   }
 }
 
@@ -1187,6 +1268,12 @@ static int dh_share() {
   const char* e = getenv("SPARTON_BWD_SHARE");
   return e != nullptr ? atoi(e) : 2;
 }
+// Rows with more entries than this go to bwd_dh_hot_kernel (SPARTON_BWD_HOT_MIN overrides
+// it; tests compare both).
+static int dh_hot_min() {
+  const char* e = getenv("SPARTON_BWD_HOT_MIN");
+  return e != nullptr ? atoi(e) : HOT_MIN;
+}
 // The five-kernel dH takes its long-row load groups for large vocabularies
 // (SPARTON_BWD_DH_LONG=1 forces them; tests compare the two).
 static bool dh_long_rows(int64_t V) {
@@ -1246,6 +1333,8 @@ static void launch_rows(const T* g, const RT* r, const int32_t* idx, const void*
     int2* list = (int2*)((char*)ws + L.list);
     int2* comp = (int2*)((char*)ws + L.comp);
     int* ccount = (int*)((char*)ws + L.ccount);
+    int* hot = (int*)((char*)ws + L.hot);
+    const int hot_min = dh_hot_min();
     for (int64_t b0 = 0; b0 < B; b0 += Bc) {
       const int64_t nb = std::min(Bc, B - b0);
       const T* gb = g + b0 * V;
@@ -1260,14 +1349,15 @@ static void launch_rows(const T* g, const RT* r, const int32_t* idx, const void*
         if (L.nch > 0)
           hipLaunchKernelGGL((bwd_count_kernel<T, RT>), cgrid, dim3(64 * wpb), cl, st, gb, rb, ib,
                              mask, mdt, (int)sw, (int)V, (int)L.nch, hist, comp, ccount, (int)s0,
-                             b0, (int)S);
+                             b0, (int)S, hot);
         if (sw <= SCAN_THREADS / 2)
           hipLaunchKernelGGL(bwd_scan_parts_kernel, dim3((unsigned)nb), dim3(SCAN_THREADS), 0, st,
-                             hist, seg_start, seg_cnt, (int)sw, (int)L.nch, (int)round_up(sw, 64));
+                             hist, seg_start, seg_cnt, (int)sw, (int)L.nch, (int)round_up(sw, 64),
+                             hot, hot_min);
         else
           hipLaunchKernelGGL(bwd_scan_kernel, dim3((unsigned)nb),
                              dim3((unsigned)std::min<int64_t>(SCAN_THREADS, round_up(sw, 64))), 0, st,
-                             hist, seg_start, seg_cnt, (int)sw, (int)L.nch);
+                             hist, seg_start, seg_cnt, (int)sw, (int)L.nch, hot, hot_min);
         if (L.nch > 0)
           hipLaunchKernelGGL(bwd_scatter_kernel, cgrid, dim3(64 * wpb), (size_t)sw * 4 * wpb, st, ib,
                              (int)sw, (int)V, (int)L.nch, (const int*)hist, (const int2*)comp,
@@ -1278,14 +1368,24 @@ static void launch_rows(const T* g, const RT* r, const int32_t* idx, const void*
                              dim3(64 * SPLIT_WAVES), 0, st, W, (const int2*)list,
                              (const int*)seg_start, (const int*)seg_cnt, dhb, (int)nb, (int)sw,
                              (int)D, (int)V, (int)S, (int)ns);
-        } else if (dh_long_rows(V))
-          hipLaunchKernelGGL((bwd_dh_kernel<T, O, DhPasses<NP>::value, true>), dim3((unsigned)cdiv(nb * sw, 4)),
-                             dim3(256), 0, st, W, (const int2*)list, (const int*)seg_start,
-                             (const int*)seg_cnt, dhb, (int)nb, (int)sw, (int)D, (int)V, (int)S);
-        else
-          hipLaunchKernelGGL((bwd_dh_kernel<T, O, DhPasses<NP>::value, false>), dim3((unsigned)cdiv(nb * sw, 4)),
-                             dim3(256), 0, st, W, (const int2*)list, (const int*)seg_start,
-                             (const int*)seg_cnt, dhb, (int)nb, (int)sw, (int)D, (int)V, (int)S);
+        } else {
+          if (dh_long_rows(V))
+            hipLaunchKernelGGL((bwd_dh_kernel<T, O, DhPasses<NP>::value, true>), dim3((unsigned)cdiv(nb * sw, 4)),
+                               dim3(256), 0, st, W, (const int2*)list, (const int*)seg_start,
+                               (const int*)seg_cnt, dhb, (int)nb, (int)sw, (int)D, (int)V, (int)S,
+                               hot_min);
+          else
+            hipLaunchKernelGGL((bwd_dh_kernel<T, O, DhPasses<NP>::value, false>), dim3((unsigned)cdiv(nb * sw, 4)),
+                               dim3(256), 0, st, W, (const int2*)list, (const int*)seg_start,
+                               (const int*)seg_cnt, dhb, (int)nb, (int)sw, (int)D, (int)V, (int)S,
+                               hot_min);
+          // The rows bwd_dh_kernel left (listed by the scan; the count kernel zeroed the list).
+          if (L.nch > 0)
+            hipLaunchKernelGGL((bwd_dh_hot_kernel<T, O>), dim3(HOT_GRID), dim3(64 * HOT_WAVES), 0, st, W,
+                               (const int2*)list, (const int*)seg_start, (const int*)seg_cnt,
+                               (const int*)hot, dhb, (int)sw, (int)D, (int)V, (int)S,
+                               (int)cdiv(D, 256));
+        }
       }
     }
   }

@@ -272,6 +272,37 @@ def test_backward_hot_rows(case, device, monkeypatch):
     check_bwd_isolated(H, W, b, m, G, reps32, idx, dH, dW, db)
 
 
+@pytest.mark.parametrize("case", [
+    ("bf16", 4, 64, 64, 70000, True, "int64"),      # V > 65536: the five-kernel path
+    ("fp32", 8, 100, 96, 8000, False, "int64"),     # five-kernel path forced
+    ("fp16", 4, 50, 1280, 12000, True, "int64"),    # five 256-column slices per row
+], ids=lambda c: "-".join(map(str, c)))
+def test_backward_hot_rows_five_kernel(case, device, monkeypatch):
+    """Rows with more than 128 entries (position 0 scaled up) on the five-kernel path go to
+    bwd_dh_hot_kernel, whose workgroup shares a row's batches: bitwise the same dH as one
+    wave per row (SPARTON_BWD_HOT_MIN set past every row), and the oracle's."""
+    say(f"hot dH rows on the five-kernel path, case {case}")
+    H, W, b, m, G = make_case(*case)
+    H[:, 0, :] *= 3.0
+    Hd, Wd, md, Gd = H.to(device), W.to(device), m.to(device), G.to(device)
+    bd = None if b is None else b.to(device)
+    monkeypatch.setenv("SPARTON_BWD_PATH", "five")
+    _, idx, reps32 = torch.ops.sparton.fused_sparton_fwd_train(Hd, Wd, bd, md)
+    hot = [t.clone() for t in torch.ops.sparton.fused_sparton_bwd(Gd, reps32, idx, Hd, Wd, bd, md)]
+    monkeypatch.setenv("SPARTON_BWD_HOT_MIN", str(2 ** 30))
+    plain = torch.ops.sparton.fused_sparton_bwd(Gd, reps32, idx, Hd, Wd, bd, md)
+    torch.cuda.synchronize()
+    act = (Gd != 0) & (reps32 > 0)
+    cnt = torch.zeros(H.shape[0], H.shape[1], dtype=torch.int64, device=device)
+    cnt.scatter_add_(1, idx.long(), act.long())
+    n_hot = int((cnt > 128).sum())
+    say(f"  {n_hot} rows with more than 128 entries (largest {int(cnt.max())})")
+    assert n_hot > 0
+    for a, c in zip(hot, plain):
+        assert (a is None and c is None) or torch.equal(a, c)
+    check_bwd_isolated(H, W, b, m, G, reps32, idx, *hot)
+
+
 def test_graph_capture_replays(device):
     """Forward and backward captured into one HIP graph (all of their kernels and workspace
     allocations) replay to the eager results, bitwise, with eager work and synchronizations
