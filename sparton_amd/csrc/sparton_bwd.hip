@@ -430,14 +430,15 @@ template <int NP> struct Batch { static constexpr int U = NP <= 3 ? 8 : NP <= 6 
 // in the 64-entry chunk, US rows otherwise. Its gathers are chains of round trips, so
 // for long rows more rows in flight beat occupancy; LONG is chosen for large vocabularies
 // (V > FUSE_V_FAST), where rows hold many entries. Measured (dH alone incl. its bucketing):
-// config 4 (V = 250002, 16-bit D = 768, ~49 entries per row) U = 8 vs 32: 279 vs 233 us;
-// config 5 (D = 4096, 8 passes) U = 4 vs 8: 233 vs 218 us; short rows (config 2 on this
-// path) lose 3 us with U = 32 (fewer waves in flight).
+// config 4 (V = 250002, 16-bit D = 768, ~49 entries per row) U = 8 vs 32: 279 vs 233 us
+// with every row here; with rows past HOT_MIN entries in bwd_dh_hot_kernel, U = 8 / 16 /
+// 32: 187 / 181 / 187 us. Config 5 (D = 4096, 8 passes) U = 4 vs 8: 233 vs 218 us; short
+// rows (config 2 on this path) lose 3 us with U = 32 (fewer waves in flight).
 constexpr int DH_MAX_NP = 8;
 template <int NP> struct DhPasses { static constexpr int value = NP < DH_MAX_NP ? NP : DH_MAX_NP; };
 template <typename T, int NP, bool LONG> struct DhBatch {
   static constexpr bool B16 = sizeof(T) == 2;
-  static constexpr int U = NP <= 3 ? (LONG && B16 ? 32 : 8) : (LONG && B16 ? 8 : 4);
+  static constexpr int U = NP <= 3 ? (LONG && B16 ? 16 : 8) : (LONG && B16 ? 8 : 4);
   static constexpr int US = NP <= 3 ? 8 : 4;
 };
 static_assert(DhBatch<bf16, 1, true>::US % DH_BATCH == 0 && DhBatch<float, DH_MAX_NP, false>::U % DH_BATCH == 0,
