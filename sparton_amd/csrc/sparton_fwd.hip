@@ -1176,6 +1176,10 @@ constexpr int SMALL_WAVES = 4;
 // 64-128 rows at V = 30522 and 32 rows at V = 128256 win by 7-36%, 128 rows at V = 250002
 // loses by 15%); fp32 ones always (1.8-2x faster at every measured shape).
 constexpr int64_t SMALL_MAX_WORK_16 = (int64_t)1 << 24;
+// W slabs in each wave's register ring (SMALL_RING - 1 in flight). Deeper rings did not
+// stream W faster: 6 and 8 slots measured 0-8% slower (1 x 16 bf16 rows at config-2
+// widths 13.7 / 14.9 / 14.8 us; config 1, fp32, 40.9 / 41.1 / 42.4 us).
+constexpr int SMALL_RING = 4;
 
 // The lane's W row, slab k: four 16-byte chunks (lane half h: bytes 64h + 16p), the
 // offsets clamped into the row (chunks past D are cleared at use).
@@ -1253,20 +1257,20 @@ __global__ __launch_bounds__(64 * SMALL_WAVES) void fwd_small_kernel(
 #pragma unroll
   for (int r = 0; r < RB; ++r) hrow[r] = (const char*)(H + (int64_t)min(r * 32 + hr, rows - 1) * D);
   if (nk > 0) {
-    // Slab j: W from ring slot j % 4 (three slabs in flight while one is multiplied), H
-    // from LDS buffer j % 2. Loads past the last slab re-read it (unused), so every step
-    // issues the same loads; the scheduling barriers keep the loads in issue order (H's
-    // first), so each wait counts only what it needs.
-    u32x4 f0[4], f1[4], f2[4], f3[4], hv[RB];
+    // Slab j: W from ring slot j % SMALL_RING (SMALL_RING - 1 slabs in flight while one is
+    // multiplied), H from LDS buffer j % 2. Loads past the last slab re-read it (unused),
+    // so every step issues the same loads; the scheduling barriers keep the loads in issue
+    // order (H's first), so each wait counts only what it needs.
+    constexpr int R = SMALL_RING;
+    u32x4 f[R][4], hv[RB];
     small_h_load<RB>(hv, hrow, 0, hc, row_bytes);
-    small_w_load(f0, wrow, 0, h, row_bytes);
-    small_w_load(f1, wrow, min(1, nk - 1), h, row_bytes);
-    small_w_load(f2, wrow, min(2, nk - 1), h, row_bytes);
+#pragma unroll
+    for (int i = 0; i + 1 < R; ++i) small_w_load(f[i], wrow, min(i, nk - 1), h, row_bytes);
     small_h_store<RB>(sm.h[0], hv, 0, hr, hc, row_bytes);
     __syncthreads();
     auto step = [&](int j, const u32x4 (&fc)[4], u32x4 (&fn)[4]) {
       small_h_load<RB>(hv, hrow, min(j + 1, nk - 1), hc, row_bytes);
-      small_w_load(fn, wrow, min(j + 3, nk - 1), h, row_bytes);
+      small_w_load(fn, wrow, min(j + R - 1, nk - 1), h, row_bytes);
       __builtin_amdgcn_sched_barrier(0);
       small_slab<T, RB>(sm.h[j & 1], fc, acc, j, l32, h, row_bytes);
       __builtin_amdgcn_sched_barrier(0);
@@ -1274,16 +1278,14 @@ __global__ __launch_bounds__(64 * SMALL_WAVES) void fwd_small_kernel(
       __syncthreads();
     };
     int k = 0;
-    for (; k + 3 < nk; k += 4) {
-      step(k, f0, f3);
-      step(k + 1, f1, f0);
-      step(k + 2, f2, f1);
-      step(k + 3, f3, f2);
+    for (; k + R - 1 < nk; k += R) {
+#pragma unroll
+      for (int i = 0; i < R; ++i) step(k + i, f[i], f[(i + R - 1) % R]);
     }
-    // f0, f1, f2 hold slabs k, k + 1, k + 2 (loads clamped to the last slab)
-    if (k < nk) step(k, f0, f3);
-    if (k + 1 < nk) step(k + 1, f1, f0);
-    if (k + 2 < nk) step(k + 2, f2, f1);
+    // slots 0 .. R - 2 hold slabs k .. k + R - 2 (loads clamped to the last slab)
+#pragma unroll
+    for (int i = 0; i + 1 < R; ++i)
+      if (k + i < nk) step(k + i, f[i], f[(i + R - 1) % R]);
   }
   // (the last step's barrier: every wave is done with the H slabs, sm.xs may be written)
   __syncthreads();  // mk is staged (also when nk == 0)
