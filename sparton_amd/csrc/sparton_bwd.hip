@@ -503,14 +503,15 @@ template <typename T, int NP> struct DwPasses {
 // loop, so the summation order is the segment's v order), all loads of a group are
 // issued, then its rows are accumulated.
 template <typename T, typename O, int NP, bool LONG>
-__global__ __launch_bounds__(256) void bwd_dh_kernel(
-    const T* __restrict__ W, const int2* __restrict__ list, const int* __restrict__ seg_start,
-    const int* __restrict__ seg_cnt, O* __restrict__ dH, int B, int S, int D, int V, int S_row,
-    int hot_min) {
+__device__ __forceinline__ void dh_rows_body(const T* __restrict__ W, const int2* __restrict__ list,
+                                             const int* __restrict__ seg_start,
+                                             const int* __restrict__ seg_cnt, O* __restrict__ dH,
+                                             int B, int S, int D, int V, int S_row, int hot_min,
+                                             int blk) {
   constexpr int U = DhBatch<T, NP, LONG>::U, US = DhBatch<T, NP, LONG>::US;
   static_assert(NP <= DH_MAX_NP, "register passes");
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int64_t row = (int64_t)blockIdx.x * 4 + wave;
+  const int64_t row = (int64_t)blk * 4 + wave;
   if (row >= (int64_t)B * S) return;
   const int64_t b = row / S;
   const int start = __builtin_amdgcn_readfirstlane(seg_start[row]);
@@ -538,6 +539,14 @@ __global__ __launch_bounds__(256) void bwd_dh_kernel(
       if (d < D) store4(out + d, acc[p]);
     }
   }
+}
+template <typename T, typename O, int NP, bool LONG>
+__global__ __launch_bounds__(256) void bwd_dh_kernel(
+    const T* __restrict__ W, const int2* __restrict__ list, const int* __restrict__ seg_start,
+    const int* __restrict__ seg_cnt, O* __restrict__ dH, int B, int S, int D, int V, int S_row,
+    int hot_min) {
+  dh_rows_body<T, O, NP, LONG>(W, list, seg_start, seg_cnt, dH, B, S, D, V, S_row, hot_min,
+                               (int)blockIdx.x);
 }
 
 // Hot rows (more than hot_min entries, e.g. a position that wins most vocab ids; at
@@ -615,14 +624,14 @@ constexpr int SPLIT_WAVES = 8;
 constexpr int SPLIT_ROWS = 1024;
 constexpr int SPLIT_U = 16;  // rows gathered per batch (one 256-column slice each)
 template <typename T, typename O>
-__global__ __launch_bounds__(64 * SPLIT_WAVES) void bwd_dh_split_kernel(
-    const T* __restrict__ W, const int2* __restrict__ list, const int* __restrict__ seg_start,
-    const int* __restrict__ seg_cnt, O* __restrict__ dH, int B, int S, int D, int V, int S_row,
-    int ns) {
-  __shared__ __attribute__((aligned(16))) float red[SPLIT_WAVES][256];
+__device__ __forceinline__ void dh_split_body(float (*red)[256], const T* __restrict__ W,
+                                              const int2* __restrict__ list,
+                                              const int* __restrict__ seg_start,
+                                              const int* __restrict__ seg_cnt, O* __restrict__ dH,
+                                              int S, int D, int V, int S_row, int ns, int blk) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int64_t row = blockIdx.x / ns;  // grid = B * S * ns exactly
-  const int d = (int)(blockIdx.x % ns) * 256 + lane * 4;
+  const int64_t row = blk / ns;  // workgroups = B * S * ns exactly
+  const int d = (int)(blk % ns) * 256 + lane * 4;
   const int64_t b = row / S;
   const int start = __builtin_amdgcn_readfirstlane(seg_start[row]);
   const int cnt = __builtin_amdgcn_readfirstlane(seg_cnt[row]);
@@ -656,6 +665,14 @@ __global__ __launch_bounds__(64 * SPLIT_WAVES) void bwd_dh_split_kernel(
     for (int w = 1; w < SPLIT_WAVES; ++w) t += *(const f32x4*)&red[w][lane * 4];
     if (d < D) store4(dH + (b * S_row + (row - b * S)) * D + d, t);
   }
+}
+template <typename T, typename O>
+__global__ __launch_bounds__(64 * SPLIT_WAVES) void bwd_dh_split_kernel(
+    const T* __restrict__ W, const int2* __restrict__ list, const int* __restrict__ seg_start,
+    const int* __restrict__ seg_cnt, O* __restrict__ dH, int B, int S, int D, int V, int S_row,
+    int ns) {
+  __shared__ __attribute__((aligned(16))) float red[SPLIT_WAVES][256];
+  dh_split_body<T, O>(red, W, list, seg_start, seg_cnt, dH, S, D, V, S_row, ns, (int)blockIdx.x);
 }
 
 // Entries (b_i, v) for N batch rows (b_i >= B or v >= V: inactive): g' (0 if inactive) and
@@ -926,6 +943,63 @@ __global__ __launch_bounds__(64 * DW_WAVES) void bwd_dw_staged_kernel(
   dw_stage<T, RT, 64, DW_WAVES>(gl, sl, grad, reps, idx, mask, mdt, B, S, V, v0, wave, lane);
   __syncthreads();
   dw_gather<T, O, NP, RT, 64, DW_WAVES>(gl, sl, H, dW, dbias, B, S, D, V, v0, wave, lane);
+}
+
+// dH and the staged dW in one launch, for the five-kernel path when it makes one pass
+// (B <= MAX_B, S <= MAX_S), dW is staged (B <= DW_STAGE_B, S <= DW_STAGE_S) and the rows
+// are wide (the launch rule is at the host dispatch): the dH workgroups first, then dW
+// workgroups of 4 ids per wave. dW reads only the inputs, so its workgroups fill the CUs
+// that the dH rows leave idle, and its own launch (about 4.5 us of dispatch and cache
+// work at each kernel boundary) is saved. The sums are those of the separate kernels.
+template <typename T, typename O, int NP, bool LONG, int DNP, typename RT>
+__global__ __launch_bounds__(256) void bwd_dh_dw_kernel(
+    const T* __restrict__ W, const int2* __restrict__ list, const int* __restrict__ seg_start,
+    const int* __restrict__ seg_cnt, O* __restrict__ dH, int B, int S, int D, int V,
+    int hot_min, int n_dh, const T* __restrict__ grad, const RT* __restrict__ reps,
+    const int32_t* __restrict__ idx, const void* __restrict__ mask, int mdt,
+    const T* __restrict__ H, O* __restrict__ dW, O* __restrict__ dbias) {
+  constexpr int NW = 4, NIDS = 4 * NW;
+  __shared__ float gl[NIDS * DW_LD];
+  __shared__ uint16_t sl[NIDS * DW_LD];
+  if ((int)blockIdx.x < n_dh) {  // workgroup-uniform
+    dh_rows_body<T, O, NP, LONG>(W, list, seg_start, seg_cnt, dH, B, S, D, V, S, hot_min,
+                                 (int)blockIdx.x);
+    return;
+  }
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int v0 = ((int)blockIdx.x - n_dh) * NIDS;
+  dw_stage<T, RT, NIDS, NW>(gl, sl, grad, reps, idx, mask, mdt, B, S, V, v0, wave, lane);
+  __syncthreads();
+  dw_gather<T, O, DNP, RT, NIDS, NW>(gl, sl, H, dW, dbias, B, S, D, V, v0, wave, lane);
+}
+
+// The same for few rows: the split dH workgroups, then dW workgroups of 4 ids per wave.
+template <typename T, typename O, int DNP, typename RT>
+__global__ __launch_bounds__(64 * SPLIT_WAVES) void bwd_dh_split_dw_kernel(
+    const T* __restrict__ W, const int2* __restrict__ list, const int* __restrict__ seg_start,
+    const int* __restrict__ seg_cnt, O* __restrict__ dH, int B, int S, int D, int V, int ns,
+    int n_dh, const T* __restrict__ grad, const RT* __restrict__ reps,
+    const int32_t* __restrict__ idx, const void* __restrict__ mask, int mdt,
+    const T* __restrict__ H, O* __restrict__ dW, O* __restrict__ dbias) {
+  constexpr int NW = SPLIT_WAVES, NIDS = 4 * NW;
+  struct DwSmem {
+    float gl[NIDS * DW_LD];
+    uint16_t sl[NIDS * DW_LD];
+  };
+  union Smem {
+    float red[SPLIT_WAVES][256];
+    DwSmem w;
+  };
+  __shared__ __attribute__((aligned(16))) Smem sm;
+  if ((int)blockIdx.x < n_dh) {  // workgroup-uniform
+    dh_split_body<T, O>(sm.red, W, list, seg_start, seg_cnt, dH, S, D, V, S, ns, (int)blockIdx.x);
+    return;
+  }
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int v0 = ((int)blockIdx.x - n_dh) * NIDS;
+  dw_stage<T, RT, NIDS, NW>(sm.w.gl, sm.w.sl, grad, reps, idx, mask, mdt, B, S, V, v0, wave, lane);
+  __syncthreads();
+  dw_gather<T, O, DNP, RT, NIDS, NW>(sm.w.gl, sm.w.sl, H, dW, dbias, B, S, D, V, v0, wave, lane);
 }
 
 // The fused path's compaction, for the dH workgroups: for batch row b and 64-id block
@@ -1281,6 +1355,14 @@ static bool dh_long_rows(int64_t V) {
   const char* e = getenv("SPARTON_BWD_DH_LONG");
   return V > FUSE_V_FAST || (e != nullptr && strcmp(e, "1") == 0);
 }
+// Register passes from which the many-rows dH launch also takes dW's workgroups.
+constexpr int DH_MERGE_NP = 6;
+// The five-kernel path runs dW in the dH launch where it can (SPARTON_BWD_DW_MERGE=0 keeps
+// it a separate launch; tests compare the two).
+static bool dw_merge_on() {
+  const char* e = getenv("SPARTON_BWD_DW_MERGE");
+  return e == nullptr || strcmp(e, "0") != 0;
+}
 // SPARTON_BWD_PATH=five forces the five-kernel path (tests compare the two paths).
 static bool fused_path_enabled() {
   const char* e = getenv("SPARTON_BWD_PATH");
@@ -1320,6 +1402,7 @@ static void launch_rows(const T* g, const RT* r, const int32_t* idx, const void*
 #undef FUSED
     return;
   }
+  bool merged_dw = false;
   if (dH != nullptr && B * S > 0 && D > 0) {
     // Batch rows in chunks of at most MAX_B and positions in windows of at most MAX_S:
     // each pass runs count -> scan -> scatter -> dH over rows [b0, b0 + nb) and
@@ -1336,6 +1419,15 @@ static void launch_rows(const T* g, const RT* r, const int32_t* idx, const void*
     int* ccount = (int*)((char*)ws + L.ccount);
     int* hot = (int*)((char*)ws + L.hot);
     const int hot_min = dh_hot_min();
+    // One pass and a staged dW: dW's workgroups join the dH launch when that launch
+    // does not take dW's occupancy away. Measured (backward, one box): few rows (config
+    // 1, split dH) 78.9 -> 73.6 us; wide rows (config 5, D = 4096: 182 VGPRs for dH
+    // against 107 for dW) 520 -> 504 us; but config 4 (D = 768, long rows: dH at 125
+    // VGPRs, dW at 58) 328 -> 346 us, so rows under DH_MERGE_NP passes keep two launches.
+    const bool few_rows = B * S < SPLIT_ROWS;
+    merged_dw = (dW != nullptr || dbias != nullptr) && V > 0 && B <= Bc && S <= Sc &&
+                B <= DW_STAGE_B && S <= DW_STAGE_S && L.nch > 0 && dw_merge_on() &&
+                (few_rows || DhPasses<NP>::value >= DH_MERGE_NP);
     for (int64_t b0 = 0; b0 < B; b0 += Bc) {
       const int64_t nb = std::min(Bc, B - b0);
       const T* gb = g + b0 * V;
@@ -1365,10 +1457,38 @@ static void launch_rows(const T* g, const RT* r, const int32_t* idx, const void*
                              (const int*)ccount, list, (int)s0);
         if (nb * sw < SPLIT_ROWS) {
           const int64_t ns = cdiv(D, 256);
-          hipLaunchKernelGGL((bwd_dh_split_kernel<T, O>), dim3((unsigned)(nb * sw * ns)),
-                             dim3(64 * SPLIT_WAVES), 0, st, W, (const int2*)list,
-                             (const int*)seg_start, (const int*)seg_cnt, dhb, (int)nb, (int)sw,
-                             (int)D, (int)V, (int)S, (int)ns);
+          if (merged_dw)
+            hipLaunchKernelGGL((bwd_dh_split_dw_kernel<T, O, DwPasses<T, NP>::value, RT>),
+                               dim3((unsigned)(nb * sw * ns + cdiv(V, 4 * SPLIT_WAVES))),
+                               dim3(64 * SPLIT_WAVES), 0, st, W, (const int2*)list,
+                               (const int*)seg_start, (const int*)seg_cnt, dhb, (int)B, (int)S,
+                               (int)D, (int)V, (int)ns, (int)(nb * sw * ns), g, r, idx, mask, mdt,
+                               H, dW, dbias);
+          else
+            hipLaunchKernelGGL((bwd_dh_split_kernel<T, O>), dim3((unsigned)(nb * sw * ns)),
+                               dim3(64 * SPLIT_WAVES), 0, st, W, (const int2*)list,
+                               (const int*)seg_start, (const int*)seg_cnt, dhb, (int)nb, (int)sw,
+                               (int)D, (int)V, (int)S, (int)ns);
+        } else if (merged_dw) {
+          if constexpr (DhPasses<NP>::value >= DH_MERGE_NP) {
+            const int n_dh = (int)cdiv(nb * sw, 4);
+            const dim3 grid((unsigned)(n_dh + cdiv(V, 16)));
+            if (dh_long_rows(V))
+              hipLaunchKernelGGL((bwd_dh_dw_kernel<T, O, DhPasses<NP>::value, true, DwPasses<T, NP>::value, RT>),
+                                 grid, dim3(256), 0, st, W, (const int2*)list, (const int*)seg_start,
+                                 (const int*)seg_cnt, dhb, (int)B, (int)S, (int)D, (int)V, hot_min,
+                                 n_dh, g, r, idx, mask, mdt, H, dW, dbias);
+            else
+              hipLaunchKernelGGL((bwd_dh_dw_kernel<T, O, DhPasses<NP>::value, false, DwPasses<T, NP>::value, RT>),
+                                 grid, dim3(256), 0, st, W, (const int2*)list, (const int*)seg_start,
+                                 (const int*)seg_cnt, dhb, (int)B, (int)S, (int)D, (int)V, hot_min,
+                                 n_dh, g, r, idx, mask, mdt, H, dW, dbias);
+          }
+          if (L.nch > 0)
+            hipLaunchKernelGGL((bwd_dh_hot_kernel<T, O>), dim3(HOT_GRID), dim3(64 * HOT_WAVES), 0, st, W,
+                               (const int2*)list, (const int*)seg_start, (const int*)seg_cnt,
+                               (const int*)hot, dhb, (int)sw, (int)D, (int)V, (int)S,
+                               (int)cdiv(D, 256));
         } else {
           if (dh_long_rows(V))
             hipLaunchKernelGGL((bwd_dh_kernel<T, O, DhPasses<NP>::value, true>), dim3((unsigned)cdiv(nb * sw, 4)),
@@ -1390,7 +1510,7 @@ static void launch_rows(const T* g, const RT* r, const int32_t* idx, const void*
       }
     }
   }
-  if ((dW != nullptr || dbias != nullptr) && V > 0) {
+  if ((dW != nullptr || dbias != nullptr) && V > 0 && !merged_dw) {
     if (B <= DW_STAGE_B && S <= DW_STAGE_S)
       hipLaunchKernelGGL((bwd_dw_staged_kernel<T, O, DwPasses<T, NP>::value, RT>),
                          dim3((unsigned)cdiv(V, 64)), dim3(64 * DW_WAVES), 0,

@@ -633,6 +633,34 @@ def test_backward_few_rows_split(case, device):
 
 
 
+@pytest.mark.parametrize("case,long_rows", [
+    (("fp32", 2, 32, 768, 3000, True, "int64"), False),    # few rows: split dH + dW, one launch
+    (("bf16", 3, 100, 256, 2000, False, "holes"), False),  # few rows, no bias
+    (("bf16", 8, 160, 1536, 1200, True, "int64"), False),  # 1280 rows, six register passes
+    (("fp16", 6, 200, 2048, 3000, True, "frac"), True),    # eight passes, long-row dH groups
+], ids=lambda c: "-".join(map(str, c)) if isinstance(c, tuple) else f"long{int(c)}")
+def test_backward_dw_in_dh_launch(case, long_rows, device, monkeypatch):
+    """On the five-kernel path, dW's workgroups run in the dH launch (few rows, or rows of
+    six or more register passes): bitwise the same dH, dW and dbias as a separate dW
+    launch (SPARTON_BWD_DW_MERGE=0), and the oracle's."""
+    say(f"dW in the dH launch, case {case}, long-row groups {long_rows}")
+    H, W, b, m, G = make_case(*case)
+    Hd, Wd, md, Gd = H.to(device), W.to(device), m.to(device), G.to(device)
+    bd = None if b is None else b.to(device)
+    monkeypatch.setenv("SPARTON_BWD_PATH", "five")
+    if long_rows:
+        monkeypatch.setenv("SPARTON_BWD_DH_LONG", "1")
+    _, idx, reps32 = torch.ops.sparton.fused_sparton_fwd_train(Hd, Wd, bd, md)
+    merged = [None if t is None else t.clone()
+              for t in torch.ops.sparton.fused_sparton_bwd(Gd, reps32, idx, Hd, Wd, bd, md)]
+    monkeypatch.setenv("SPARTON_BWD_DW_MERGE", "0")
+    apart = torch.ops.sparton.fused_sparton_bwd(Gd, reps32, idx, Hd, Wd, bd, md)
+    torch.cuda.synchronize()
+    for a, c in zip(merged, apart):
+        assert (a is None and c is None) or torch.equal(a, c)
+    check_bwd_isolated(H, W, b, m, G, reps32, idx, *merged)
+
+
 @pytest.mark.parametrize("case", [
     ("bf16", 2, 20000, 64, 320, True, "holes"),     # S > 16384: two dH windows
     ("fp32", 1, 40000, 32, 200, False, "int64"),    # three windows, the last partial
