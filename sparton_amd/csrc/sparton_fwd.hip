@@ -706,41 +706,60 @@ __device__ __forceinline__ Unit unit_of(int w, int r, int G, int n_units, int n_
 // into the previous M-tile (slot 0) or the next one (slot 1). A group's key holds its
 // maximum x (5 low mantissa bits cleared) and its row r in the 32-row block (as
 // 31 - r); the row's position is the group's first position plus r mod 16.
+// The segment boundaries are wave-uniform: lane g of every copy wave compares group g's
+// batch row with group g+1's, and one ballot gives the bitmask of segment ends (lanes
+// NGRP, NGRP + 1 hold the rows of the groups just before and after the tile). The merge
+// is unrolled with scalar branches and keeps, per column, the best value and the group
+// and row that hold it; a segment end reads that group's first position (one LDS read),
+// so no LDS read waits inside the per-group merge.
 template <typename T>
 __device__ __forceinline__ void write_unit(const Smem& sm, const UnitMeta& um, int m, int v0, int V,
                                            int n_valid, int ct, T* reps, int32_t* argmax,
                                            float* reps_f32, float2* part) {
-  if (v0 + ct >= V) return;
-  const int v = v0 + ct;
-  const int b_prev = um.grp_b[NGRP], b_next = um.grp_b[NGRP + 1];
+  const int lane = ct & 63;
+  const int gbv = um.grp_b[min(lane, NGRP + 1)];
+  const int gbn = um.grp_b[min(lane + 1, NGRP + 1)];
+  const uint64_t ends = __ballot(lane < n_valid && (lane + 1 == n_valid || gbn != gbv));
+  const int b_prev = __builtin_amdgcn_readlane(gbv, NGRP);
+  const int b_next = __builtin_amdgcn_readlane(gbv, NGRP + 1);
+  const int b_first = __builtin_amdgcn_readlane(gbv, 0);
+  const bool live = v0 + ct < V;
+  const int v = min(v0 + ct, V - 1);
   int kr[NGRP];
 #pragma unroll
   for (int g = 0; g < NGRP; ++g) kr[g] = sm.key[g][ct];  // all loads first (groups past n_valid are unused)
   float bv = 0.0f;
-  int bi = 0;
-#pragma unroll
-  for (int g = 0; g < NGRP; ++g) {
-    if (g >= n_valid) break;
-    const float x = __int_as_float(kr[g] & ~31);
-    if (x > bv) {  // earlier groups hold lower s: strict '>' keeps them on ties
-      bv = x;
-      bi = um.grp_s[g] + ((31 - (kr[g] & 31)) & (GROUP - 1));
-    }
-    const int b = um.grp_b[g];
-    if (g + 1 == n_valid || um.grp_b[g + 1] != b) {  // the segment of batch row b ends
-      const bool cont_prev = b == um.grp_b[0] && b == b_prev;
-      const bool cont_next = g + 1 == n_valid && b == b_next;
-      if (cont_prev || cont_next) {
-        part[((int64_t)m * 2 + (cont_prev ? 0 : 1)) * V + v] = make_float2(bv, __int_as_float(bi));
-      } else {
-        const int64_t o = (int64_t)b * V + v;
-        const float rv = log1pf(bv);
-        reps[o] = from_f32<T>(rv);
-        if (argmax != nullptr) argmax[o] = bi;
-        if (reps_f32 != nullptr) reps_f32[o] = rv;
+  int bk = 0;  // (group << 5) | (31 - row in the 32-row block) of the best value
+  // A rolled loop (kr indexed through M0): unrolled, the copy path's registers and SGPR
+  // spills outgrow the kernel's 168-VGPR budget.
+#pragma unroll 1
+  for (int g = 0; g < n_valid; ++g) {  // uniform
+    {
+      const int key = kr[g];
+      const float x = __int_as_float(key & ~31);
+      const bool gt = x > bv;  // earlier groups hold lower s: strict '>' keeps them on ties
+      bv = gt ? x : bv;
+      bk = gt ? ((g << 5) | (key & 31)) : bk;
+      if ((ends >> g) & 1) {  // uniform: the segment of batch row b ends
+        const int b = __builtin_amdgcn_readlane(gbv, g);
+        const bool cont_prev = b == b_first && b == b_prev;
+        const bool cont_next = g + 1 == n_valid && b == b_next;
+        // the best row's position (0 when no value is positive)
+        const int bi = bv > 0.0f ? um.grp_s[bk >> 5] + ((31 - (bk & 31)) & (GROUP - 1)) : 0;
+        if (live) {
+          if (cont_prev || cont_next) {
+            part[((int64_t)m * 2 + (cont_prev ? 0 : 1)) * V + v] = make_float2(bv, __int_as_float(bi));
+          } else {
+            const int64_t o = (int64_t)b * V + v;
+            const float rv = log1p_pos(bv);
+            reps[o] = from_f32<T>(rv);
+            if (argmax != nullptr) argmax[o] = bi;
+            if (reps_f32 != nullptr) reps_f32[o] = rv;
+          }
+        }
+        bv = 0.0f;
+        bk = 0;
       }
-      bv = 0.0f;
-      bi = 0;
     }
   }
 }
@@ -1144,7 +1163,7 @@ __global__ __launch_bounds__(256) void fwd_fixup_kernel(int V, const int* __rest
     const int v = blockIdx.x * FIX_COLS + k * 256 + threadIdx.x;
     if (v >= V) break;
     const int64_t o = (int64_t)b * V + v;
-    const float rv = log1pf(bv[k]);
+    const float rv = log1p_pos(bv[k]);
     reps[o] = from_f32<T>(rv);
     if (argmax != nullptr) argmax[o] = bi[k];
     if (reps_f32 != nullptr) reps_f32[o] = rv;
@@ -1314,7 +1333,7 @@ __global__ __launch_bounds__(64 * SMALL_WAVES) void fwd_small_kernel(
       }
     }
     const int64_t o = (int64_t)b * V + v;
-    const float rv = log1pf(bvx);
+    const float rv = log1p_pos(bvx);
     reps[o] = from_f32<T>(rv);
     if (argmax != nullptr) argmax[o] = bi;
     if (reps_f32 != nullptr) reps_f32[o] = rv;

@@ -781,9 +781,10 @@ def test_reference_op_autograd(cfg, use_bias, device):
 def test_reps_value_truncation_bound(device):
     """The kernel's max keeps each logit with its 5 low mantissa bits cleared (the row index
     takes them), so in fp32 reps = log1p(M') with M - M' <= 2^-18 M, always rounding down,
-    plus the fp32 accumulation error. Bounded here on an fp32 case, entry by entry:
+    plus the fp32 accumulation error and the kernel's log1p (a few ulp). Bounded here on an
+    fp32 case, entry by entry:
     |reps - log1p(M)| <= (2^-18 M + gamma_{D+2} * sum|h w + b| at the oracle's argmax) / (1 + M)
-    + 2^-23."""
+    + 2^-23 + 2^-21 log1p(M)."""
     say("fp32 reps value bound")
     H, W, b, m, _ = make_case("fp32", 4, 200, 384, 3000, True, "int64", seed=3)
     reps, idx, r32 = torch.ops.sparton.fused_sparton_fwd_train(H.to(device), W.to(device), b.to(device),
@@ -791,7 +792,7 @@ def test_reps_value_truncation_bound(device):
     M, I, ref = oracle.fused_fwd_ref(H, W, b, m)
     A = oracle.logit_at(H.abs(), W.abs(), b.abs(), m.abs(), I)
     D = H.shape[-1]
-    bound = (2.0 ** -18 * M + (D + 2) * 2.0 ** -24 * A) / (1 + M) + 2.0 ** -23
+    bound = (2.0 ** -18 * M + (D + 2) * 2.0 ** -24 * A) / (1 + M) + 2.0 ** -23 + 2.0 ** -21 * ref
     err = (r32.cpu().to(F64) - ref).abs()
     assert bool((err <= bound).all()), float((err - bound).max())
     say(f"  max |reps - log1p(M)| = {float(err.max()):.3e}, mean bound {float(bound.mean()):.3e}")
