@@ -54,6 +54,9 @@ def parse():
     p.add_argument("--kernel-reps", type=int, default=50, help="back-to-back launches per kernel timing")
     p.add_argument("--cpu-seconds", type=float, default=25.0, help="budget (s) of the CPU baseline leg")
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--fp32-precision", choices=["high", "highest"], default="high",
+                   help="torch float32 matmul precision for fp32 workloads; the reference sets "
+                        "'high' when it is imported (sparton_kernel.py:14)")
     p.add_argument("--copy-probe-mib", type=int, default=0,
                    help="after timing, launch one device copy of this many MiB (PMC calibration)")
     return p.parse_args()
@@ -74,13 +77,18 @@ KNAME = {"bf16": "bf16", "fp16": "f16", "fp32": "f32"}
 # Batches of at most 128 rows (B * S) run one kernel, one wave per 32 vocab columns: fp32
 # always, 16-bit up to B * S * V = 2^24.
 SMALL_MAX_ROWS = 128
-SMALL_KERNEL = "sparton::fwd::fwd_small_kernel<%s, %d>"
+SMALL_KERNEL = "sparton::fwd::fwd_small_kernel<%s, %d, %s>"
 SMALL_TNAME = {"bf16": "__bf16", "fp16": "_Float16", "fp32": "float"}
 
 
-def fwd_kernel_name(w, dname):
-    if w.B * w.S <= SMALL_MAX_ROWS and (dname == "fp32" or w.B * w.S * w.V <= 1 << 24):
-        return SMALL_KERNEL % (SMALL_TNAME[dname], min(4, -(-w.B * w.S // 32)))
+def small_path(w, dname):
+    return w.B * w.S <= SMALL_MAX_ROWS and (dname == "fp32" or w.B * w.S * w.V <= 1 << 24)
+
+
+def fwd_kernel_name(w, dname, split):
+    if small_path(w, dname):
+        return SMALL_KERNEL % (SMALL_TNAME[dname], min(4, -(-w.B * w.S // 32)),
+                               "true" if split else "false")
     return FWD_KERNEL % KNAME[dname]
 
 
@@ -167,7 +175,7 @@ def time_main_kernel(torch, H, W, b, mask, reps_n):
     L = _lib.load()
     B, S, D = H.shape
     V = W.shape[0]
-    dt = _lib.DTYPE_CODE[H.dtype]
+    dt = _lib.fwd_dtype_code(H.dtype)
     reps = torch.empty((B, V), dtype=H.dtype, device=H.device)
     idx = torch.empty((B, V), dtype=torch.int32, device=H.device)
     reps32 = torch.empty((B, V), dtype=torch.float32, device=H.device)
@@ -458,6 +466,8 @@ def main():
     import sparton
     from sparton_amd.workloads import WORKLOADS, make_inputs
 
+    torch.set_float32_matmul_precision(args.fp32_precision)
+
     assert torch.cuda.is_available(), "bench.py needs a ROCm device"
     dev = torch.device("cuda:0")
     w = WORKLOADS[args.config]
@@ -533,6 +543,14 @@ def main():
     # host cost of a step: the queue is held by a spin kernel while the steps are enqueued
     step_dev_ms, step_host_ms, step_enq_ms = time_device(torch, step, args.kernel_reps)
     main_ms = time_main_kernel(torch, Hd.contiguous(), Wd.contiguous(), bd, mask, args.kernel_reps)
+    # fp32 products as bf16 hi/lo parts (torch 'high'/'medium'): small batches only
+    split = dname == "fp32" and args.fp32_precision != "highest" and small_path(w, dname)
+    main_ms_exact = None
+    if split:
+        torch.set_float32_matmul_precision("highest")
+        main_ms_exact = time_main_kernel(torch, Hd.contiguous(), Wd.contiguous(), bd, mask,
+                                         args.kernel_reps)
+        torch.set_float32_matmul_precision(args.fp32_precision)
     xf = transform_timing(torch, w, dev, args.kernel_reps)
     lossr = loss_timing(torch, w, dev, args.kernel_reps)
     mixed = autocast_timing(torch, w, inp, dev, args.kernel_reps)
@@ -565,13 +583,23 @@ def main():
     bwd_bytes = (w.B * w.V * (e + 4 + 4) + u_w * w.D * e + u_h * w.D * e
                  + w.B * w.S * w.D * e + w.V * w.D * e + (w.V * e if has_bias else 0))
     bwd_gbs = bwd_bytes / (bwd_ms * 1e-3) / 1e9
-    kname = fwd_kernel_name(w, dname)
+    kname = fwd_kernel_name(w, dname, split)
+    # The forward kernel's bound: useful flops at the MFMA peak (three bf16 MFMAs per fp32
+    # product in split mode) against its compulsory bytes at the HBM peak: H, W, bias and the
+    # mask read once; reps, int32 argmax and fp32 reps written once.
+    mask_e = mask.element_size()
+    fwd_bytes = (w.B * w.S * w.D * e + w.V * w.D * e + (w.V * e if has_bias else 0)
+                 + w.B * w.S * mask_e + w.B * w.V * (e + 4 + 4))
+    mfma_peak = PEAK_TFLOPS["bf16"] / 3.0 if split else peak_tf
+    t_mfma = useful_flops / (mfma_peak * 1e12)
+    t_hbm = fwd_bytes / (PEAK_HBM_GBS * 1e9)
+    fwd_bound = "mfma" if t_mfma >= t_hbm else "hbm"
     traffic, traffic_src = measured_traffic(args.config, kname)
     ceiling = mfma_ceiling(torch, dname)
     # whole-step roofline: the forward at the MFMA peak plus the backward's
     # compulsory bytes at HBM peak, over the measured step; useful flops only
     t_step = elapsed / args.steps
-    t_roof = useful_flops / (peak_tf * 1e12) + bwd_bytes / (PEAK_HBM_GBS * 1e9)
+    t_roof = max(t_mfma, t_hbm) + bwd_bytes / (PEAK_HBM_GBS * 1e9)
     step_flops = useful_flops + 4.0 * nnz * w.D
 
     out = {
@@ -589,9 +617,21 @@ def main():
         "data": "synthetic (seeded; BASELINE.json distributions), random-init head weights",
         "config": {"workload": f"{w.name} SpartonHead fwd+bwd", "B": w.B, "S": w.S, "D": w.D, "V": w.V,
                    "global_batch": w.B, "seq_len": w.S, "use_bias": has_bias,
-                   "valid_tokens": valid_tokens, "parallelism": "none (1 GPU)"},
-        "roofline": {"bound": "mfma", "kernel": kname, "achieved": round(fwd_tflops, 2),
-                     "peak": peak_tf, "unit": "TFLOP/s", "frac": round(fwd_tflops / peak_tf, 4),
+                   "valid_tokens": valid_tokens, "parallelism": "none (1 GPU)",
+                   **({"fp32_matmul_precision": args.fp32_precision,
+                       "fp32_products": ("bf16 hi*hi + hi*lo + lo*hi, fp32 accumulation (within 3*2^-18 "
+                                         "relative per product)" if split else "fp32 MFMA"),
+                       "main_ms_fp32_highest": (round(main_ms_exact, 4) if main_ms_exact else None)}
+                      if dname == "fp32" else {})},
+        "roofline": {**({"bound": "mfma", "achieved": round(fwd_tflops, 2), "peak": round(mfma_peak, 1),
+                          "unit": "TFLOP/s", "frac": round(fwd_tflops / mfma_peak, 4)}
+                         if fwd_bound == "mfma" else
+                         {"bound": "hbm", "achieved": round(fwd_bytes / (main_ms * 1e-3) / 1e9, 1),
+                          "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                          "frac": round(fwd_bytes / (main_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}),
+                     "kernel": kname, "bytes_per_launch": fwd_bytes,
+                     "mfma_bound_ms": round(t_mfma * 1e3, 4), "hbm_bound_ms": round(t_hbm * 1e3, 4),
+                     "tflops": round(fwd_tflops, 2),
                      "traffic": traffic, "traffic_source": traffic_src, "flops_per_launch": useful_flops,
                      "flops_basis": "useful: 2*D*V*valid_tokens (fully masked 32-row blocks are skipped)",
                      "dense_equiv_tflops": round(dense_flops / (main_ms * 1e-3) / 1e12, 2),
@@ -602,7 +642,7 @@ def main():
                      "op_tflops": round(useful_flops / (fwd_ms * 1e-3) / 1e12, 2),
                      "op_ms_back_to_back": round(fwd_b2b, 4),
                      "frac_of_mfma_ceiling": (round(fwd_tflops / ceiling["tflops"], 4)
-                                              if ceiling else None)},
+                                              if ceiling and not split and dname != "fp32" else None)},
         "step_roofline": {"frac": round(t_roof / t_step, 4), "roofline_ms": round(t_roof * 1e3, 4),
                           "step_ms": round(t_step * 1e3, 4),
                           "basis": "(useful F_fwd / MFMA peak + compulsory bwd bytes / 8 TB/s) / measured step"},

@@ -42,6 +42,18 @@ enum sparton_dtype {
   SPARTON_F16 = 2,
 };
 
+/*
+ * Flag OR'ed into the forward's `dtype` with SPARTON_F32 only (sparton_fwd,
+ * sparton_fwd_noalloc, sparton_fwd_profile; any other use is SPARTON_EINVAL): torch's
+ * 'high' float32 matmul precision, which the reference sets when it is imported
+ * (src/sparton/sparton_kernel.py:14, torch.set_float32_matmul_precision('high')). Each
+ * fp32 operand is taken as the sum of two bf16 values (hi = bf16(x), lo = bf16(x - hi)) and
+ * each product as hi*hi + hi*lo + lo*hi on bf16 MFMAs with fp32 accumulation, within
+ * 3 * 2^-18 relative of the exact product. It applies to the small-batch kernel
+ * (B*S <= 128); larger batches are computed in fp32 exactly either way.
+ */
+#define SPARTON_F32_SPLIT 0x100
+
 /* Element type of the attention mask. Any nonzero value takes part in the
  * multiply; a tokenizer mask is int64 0/1. */
 enum sparton_mask_dtype {
@@ -261,7 +273,8 @@ const char* sparton_strerror(int code);
  * B * S and B * V must also stay below 2^31). */
 void sparton_limits(int64_t* max_bwd_seq, int64_t* max_bwd_batch);
 
-/* ABI version of this header (bumped on any signature change). */
+/* ABI version of this header (bumped on any signature change or new argument value;
+ * 10: SPARTON_F32_SPLIT). */
 int sparton_abi_version(void);
 
 #ifdef __cplusplus

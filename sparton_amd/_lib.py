@@ -15,10 +15,21 @@ import torch  # noqa: F401  (must be imported first: see module docstring)
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 DEFAULT_LIB = os.path.join(_HERE, "libsparton_hip.so")
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 # enum sparton_dtype / sparton_mask_dtype (include/sparton.h)
 DTYPE_CODE = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
+F32_SPLIT = 0x100  # SPARTON_F32_SPLIT
+
+
+def fwd_dtype_code(dtype):
+    """The forward's dtype argument: fp32 follows torch's float32 matmul precision, as the
+    reference's GEMM does (it sets 'high' at import, sparton_kernel.py:14): 'high' and
+    'medium' take the bf16 hi/lo split (SPARTON_F32_SPLIT), 'highest' exact fp32."""
+    code = DTYPE_CODE[dtype]
+    if dtype == torch.float32 and torch.get_float32_matmul_precision() != "highest":
+        code |= F32_SPLIT
+    return code
 MASK_CODE = {
     torch.int64: 0,
     torch.int32: 1,

@@ -4,7 +4,7 @@
 #define SPARTON_EXPORT extern "C" __attribute__((visibility("default")))
 
 namespace {
-constexpr int kAbiVersion = 9;
+constexpr int kAbiVersion = 10;
 // The backward takes any S and B with B * S and B * V below 2^31 (it runs its dH passes
 // over windows of positions and chunks of batch rows).
 constexpr int64_t kMaxBwdSeq = INT32_MAX;

@@ -484,6 +484,40 @@ template <> struct Mfma<float> {
   }
 };
 
+// fp32 as two bf16 ("split" mode, torch's 'high' float32 matmul precision): x = hi + lo + r
+// with hi = bf16(x) and lo = bf16(x - hi) (both round to nearest even; x - hi is exact), so
+// |r| <= 2^-18 |x|. A product is taken as hi_a hi_b + hi_a lo_b + lo_a hi_b: the dropped
+// lo_a lo_b and the residuals keep it within 3 * 2^-18 relative of the exact one. (An
+// infinite x gives a NaN lo, so infinities in H or W come out as NaN in this mode.)
+typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2;
+typedef __attribute__((ext_vector_type(2))) float f32x2;
+__device__ __forceinline__ void split_pair(float x0, float x1, uint32_t& hi, uint32_t& lo) {
+  const f32x2 v = {x0, x1};
+  hi = __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
+  const f32x2 hf = {__uint_as_float(hi << 16), __uint_as_float(hi & 0xffff0000u)};
+  lo = __builtin_bit_cast(uint32_t, __builtin_convertvector(v - hf, bf16x2));
+}
+// Eight floats (x0: k = 0..3, x1: k = 4..7) as bf16x8 hi and lo parts in k order.
+__device__ __forceinline__ void split8(const u32x4& x0, const u32x4& x1, u32x4& hi, u32x4& lo) {
+  uint32_t h0, h1, h2, h3, l0, l1, l2, l3;
+  split_pair(__uint_as_float(x0[0]), __uint_as_float(x0[1]), h0, l0);
+  split_pair(__uint_as_float(x0[2]), __uint_as_float(x0[3]), h1, l1);
+  split_pair(__uint_as_float(x1[0]), __uint_as_float(x1[1]), h2, l2);
+  split_pair(__uint_as_float(x1[2]), __uint_as_float(x1[3]), h3, l3);
+  hi = u32x4{h0, h1, h2, h3};
+  lo = u32x4{l0, l1, l2, l3};
+}
+// acc += a b over 16 k (8 per lane half), both as hi + lo: the two small terms first.
+__device__ __forceinline__ void mfma_split(const u32x4& ahi, const u32x4& alo, const u32x4& bhi,
+                                           const u32x4& blo, f32x16& c) {
+  c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, alo),
+                                               __builtin_bit_cast(bf16x8, bhi), c, 0, 0, 0);
+  c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, ahi),
+                                               __builtin_bit_cast(bf16x8, blo), c, 0, 0, 0);
+  c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, ahi),
+                                               __builtin_bit_cast(bf16x8, bhi), c, 0, 0, 0);
+}
+
 // ---- unit schedule ----
 //
 // The grid is persistent (about one workgroup per CU); the units (M-tile, vocab tile)
@@ -1199,6 +1233,9 @@ constexpr int64_t SMALL_MAX_WORK_16 = (int64_t)1 << 24;
 // stream W faster: 6 and 8 slots measured 0-8% slower (1 x 16 bf16 rows at config-2
 // widths 13.7 / 14.9 / 14.8 us; config 1, fp32, 40.9 / 41.1 / 42.4 us).
 constexpr int SMALL_RING = 4;
+// The same depth for the split mode (fp32 as bf16 hi/lo): 6, 8 and 10 slots measured 2-10%
+// slower at config 1 (25.1 / 25.5 / 26.2 / 27.2 us).
+constexpr int SMALL_RING_SPLIT = 4;
 
 // The lane's W row, slab k: four 16-byte chunks (lane half h: bytes 64h + 16p), the
 // offsets clamped into the row (chunks past D are cleared at use).
@@ -1229,6 +1266,49 @@ __device__ __forceinline__ void small_h_store(u32x4* buf, const u32x4 (&hv)[RB],
     buf[(r * 32 + hr) * CHUNKS + (hc ^ swz_key(hr))] = ok ? hv[r] : u32x4{0u, 0u, 0u, 0u};
 }
 
+// Split mode (fp32): the slab's row holds its 32 floats as bf16 hi parts in logical chunks
+// 0..3 and lo parts in chunks 4..7 (chunk c: k = 8c..8c+7 of the slab), under the same
+// XOR swizzle. Thread chunk hc (k = 4hc..4hc+3) fills half hc & 1 of chunks hc / 2 and
+// 4 + hc / 2; chunks past D hold zeros.
+template <int RB>
+__device__ __forceinline__ void small_h_store_split(u32x4* buf, const u32x4 (&hv)[RB], int k, int hr,
+                                                    int hc, int row_bytes) {
+  const bool ok = k * 128 + hc * 16 < row_bytes;
+  u32x2* b2 = (u32x2*)buf;
+  const int kx = swz_key(hr);
+#pragma unroll
+  for (int r = 0; r < RB; ++r) {
+    uint32_t h0, l0, h1, l1;
+    split_pair(__uint_as_float(hv[r][0]), __uint_as_float(hv[r][1]), h0, l0);
+    split_pair(__uint_as_float(hv[r][2]), __uint_as_float(hv[r][3]), h1, l1);
+    const int row = (r * 32 + hr) * CHUNKS;
+    b2[(row + ((hc >> 1) ^ kx)) * 2 + (hc & 1)] = ok ? u32x2{h0, h1} : u32x2{0u, 0u};
+    b2[(row + ((4 + (hc >> 1)) ^ kx)) * 2 + (hc & 1)] = ok ? u32x2{l0, l1} : u32x2{0u, 0u};
+  }
+}
+
+// Split-mode MFMAs of slab k: lane half h takes k = 16h..16h+15 of the slab, in two
+// MFMA steps q of 8 (W chunks 2q, 2q + 1 of the lane; H chunks 2h + q and 4 + 2h + q).
+template <int RB>
+__device__ __forceinline__ void small_slab_split(const u32x4* buf, const u32x4 (&f)[4],
+                                                 f32x16 (&acc)[RB], int k, int l32, int h,
+                                                 int row_bytes) {
+  const int kx = swz_key(l32);
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    const int b0 = k * 128 + h * 64 + q * 32;
+    const u32x4 w0 = b0 < row_bytes ? f[2 * q] : u32x4{0u, 0u, 0u, 0u};
+    const u32x4 w1 = b0 + 16 < row_bytes ? f[2 * q + 1] : u32x4{0u, 0u, 0u, 0u};
+    u32x4 bhi, blo;
+    split8(w0, w1, bhi, blo);
+#pragma unroll
+    for (int r = 0; r < RB; ++r) {
+      const u32x4* row = buf + (r * 32 + l32) * CHUNKS;
+      mfma_split(row[(2 * h + q) ^ kx], row[(4 + 2 * h + q) ^ kx], bhi, blo, acc[r]);
+    }
+  }
+}
+
 // The MFMAs of slab k: A from the LDS slab, B from the W registers.
 template <typename T, int RB>
 __device__ __forceinline__ void small_slab(const u32x4* buf, const u32x4 (&f)[4], f32x16 (&acc)[RB],
@@ -1244,7 +1324,7 @@ __device__ __forceinline__ void small_slab(const u32x4* buf, const u32x4 (&f)[4]
   }
 }
 
-template <typename T, int RB>
+template <typename T, int RB, bool SPLIT>
 __global__ __launch_bounds__(64 * SMALL_WAVES) void fwd_small_kernel(
     const T* __restrict__ H, const T* __restrict__ W, const T* __restrict__ bias,
     const void* __restrict__ mask, int mask_dtype, T* __restrict__ reps,
@@ -1276,24 +1356,29 @@ __global__ __launch_bounds__(64 * SMALL_WAVES) void fwd_small_kernel(
 #pragma unroll
   for (int r = 0; r < RB; ++r) hrow[r] = (const char*)(H + (int64_t)min(r * 32 + hr, rows - 1) * D);
   if (nk > 0) {
-    // Slab j: W from ring slot j % SMALL_RING (SMALL_RING - 1 slabs in flight while one is
-    // multiplied), H from LDS buffer j % 2. Loads past the last slab re-read it (unused),
-    // so every step issues the same loads; the scheduling barriers keep the loads in issue
-    // order (H's first), so each wait counts only what it needs.
-    constexpr int R = SMALL_RING;
+    // Slab j: W from ring slot j % R (R - 1 slabs in flight while one is multiplied), H
+    // from LDS buffer j % 2. Loads past the last slab re-read it (unused), so every step
+    // issues the same loads; the scheduling barriers keep the loads in issue order (H's
+    // first), so each wait counts only what it needs.
+    constexpr int R = SPLIT ? SMALL_RING_SPLIT : SMALL_RING;
     u32x4 f[R][4], hv[RB];
     small_h_load<RB>(hv, hrow, 0, hc, row_bytes);
 #pragma unroll
     for (int i = 0; i + 1 < R; ++i) small_w_load(f[i], wrow, min(i, nk - 1), h, row_bytes);
-    small_h_store<RB>(sm.h[0], hv, 0, hr, hc, row_bytes);
+    if constexpr (SPLIT) small_h_store_split<RB>(sm.h[0], hv, 0, hr, hc, row_bytes);
+    else small_h_store<RB>(sm.h[0], hv, 0, hr, hc, row_bytes);
     __syncthreads();
     auto step = [&](int j, const u32x4 (&fc)[4], u32x4 (&fn)[4]) {
       small_h_load<RB>(hv, hrow, min(j + 1, nk - 1), hc, row_bytes);
       small_w_load(fn, wrow, min(j + R - 1, nk - 1), h, row_bytes);
       __builtin_amdgcn_sched_barrier(0);
-      small_slab<T, RB>(sm.h[j & 1], fc, acc, j, l32, h, row_bytes);
+      if constexpr (SPLIT) small_slab_split<RB>(sm.h[j & 1], fc, acc, j, l32, h, row_bytes);
+      else small_slab<T, RB>(sm.h[j & 1], fc, acc, j, l32, h, row_bytes);
       __builtin_amdgcn_sched_barrier(0);
-      small_h_store<RB>(sm.h[(j + 1) & 1], hv, min(j + 1, nk - 1), hr, hc, row_bytes);
+      if constexpr (SPLIT)
+        small_h_store_split<RB>(sm.h[(j + 1) & 1], hv, min(j + 1, nk - 1), hr, hc, row_bytes);
+      else
+        small_h_store<RB>(sm.h[(j + 1) & 1], hv, min(j + 1, nk - 1), hr, hc, row_bytes);
       __syncthreads();
     };
     int k = 0;
@@ -1351,15 +1436,15 @@ static int fwd_path_override() {
   return 0;
 }
 
-template <typename T>
+template <typename T, bool SPLIT>
 static void launch_small(const void* H, const void* W, const void* bias, const void* mask,
                          int mask_dtype, void* reps, int32_t* argmax, float* reps_f32, int64_t B,
                          int64_t S, int64_t D, int64_t V, hipStream_t stream) {
   const dim3 grid((unsigned)cdiv(cdiv(V, 32), SMALL_WAVES)), block(64 * SMALL_WAVES);
 #define SMALL(RB)                                                                                   \
-  hipLaunchKernelGGL((fwd_small_kernel<T, RB>), grid, block, 0, stream, (const T*)H, (const T*)W,  \
-                     (const T*)bias, mask, mask_dtype, (T*)reps, argmax, reps_f32, (int)B, (int)S, \
-                     (int)D, (int)V)
+  hipLaunchKernelGGL((fwd_small_kernel<T, RB, SPLIT>), grid, block, 0, stream, (const T*)H,        \
+                     (const T*)W, (const T*)bias, mask, mask_dtype, (T*)reps, argmax, reps_f32,    \
+                     (int)B, (int)S, (int)D, (int)V)
   switch (cdiv(B * S, 32)) {
     case 1: SMALL(1); break;
     case 2: SMALL(2); break;
@@ -1391,11 +1476,13 @@ static int64_t persistent_grid(int64_t n_units_max) {
 
 // ev_main: if non-null, two events recorded on `stream` just before and after the main
 // kernel (profiling).
+// split: fp32 products as bf16 hi/lo parts (SPARTON_F32_SPLIT) in the small-batch kernel;
+// the main kernel computes fp32 exactly either way.
 template <typename T>
 static int launch(const void* H, const void* W, const void* bias, const void* mask,
                   int mask_dtype, void* reps, int32_t* argmax, float* reps_f32, int64_t B,
                   int64_t S, int64_t D, int64_t V, const Work& w, hipStream_t stream,
-                  hipEvent_t* ev_main) {
+                  hipEvent_t* ev_main, bool split) {
   const int64_t ngrp = cdiv(S, GROUP);
   const int64_t n_vt = cdiv(V, BN);
   const int64_t n_mt_max = cdiv(B * ngrp, NGRP);
@@ -1405,7 +1492,15 @@ static int launch(const void* H, const void* W, const void* bias, const void* ma
   if (B * S > 0 && B * S <= SMALL_MAX_ROWS && ovr != 1 &&
       (sizeof(T) == 4 || B * S * V <= SMALL_MAX_WORK_16 || ovr == 2)) {
     if (ev_main != nullptr) (void)hipEventRecord(ev_main[0], stream);
-    launch_small<T>(H, W, bias, mask, mask_dtype, reps, argmax, reps_f32, B, S, D, V, stream);
+    bool done = false;
+    if constexpr (sizeof(T) == 4) {
+      if (split) {
+        launch_small<T, true>(H, W, bias, mask, mask_dtype, reps, argmax, reps_f32, B, S, D, V, stream);
+        done = true;
+      }
+    }
+    if (!done)
+      launch_small<T, false>(H, W, bias, mask, mask_dtype, reps, argmax, reps_f32, B, S, D, V, stream);
     if (ev_main != nullptr) (void)hipEventRecord(ev_main[1], stream);
     const hipError_t e = hipGetLastError();
     return e == hipSuccess ? SPARTON_OK : (int)e;
@@ -1471,8 +1566,15 @@ using namespace sparton;
 extern "C" __attribute__((visibility("default"))) size_t sparton_fwd_workspace_bytes(
     int64_t B, int64_t S, int64_t D, int64_t V, int dtype) {
   if (B <= 0 || S < 0 || D < 0 || V <= 0) return 0;
-  const int64_t esz = dtype == SPARTON_F32 ? 4 : 2;
+  const int64_t esz = (dtype & ~SPARTON_F32_SPLIT) == SPARTON_F32 ? 4 : 2;
   return fwd::carve(nullptr, fwd::rows_per_launch(B, S, D, esz), S, V).total;
+}
+
+// dtype: an enum sparton_dtype, or SPARTON_F32 | SPARTON_F32_SPLIT.
+static bool fwd_dtype_ok(int dtype) {
+  const int base = dtype & ~SPARTON_F32_SPLIT;
+  if (base < SPARTON_F32 || base > SPARTON_F16) return false;
+  return (dtype & SPARTON_F32_SPLIT) == 0 || base == SPARTON_F32;
 }
 
 // The forward over row chunks; with main_ms, each chunk's main kernel is bracketed by
@@ -1482,7 +1584,9 @@ static int fwd_run(const void* hidden, const void* weight, const void* bias, con
                    int64_t S, int64_t D, int64_t V, int dtype, void* workspace,
                    size_t workspace_bytes, void* stream, float* main_ms) {
   if (B < 0 || S < 0 || D < 0 || V < 0) return SPARTON_EINVAL;
-  if (dtype < SPARTON_F32 || dtype > SPARTON_F16) return SPARTON_EINVAL;
+  if (!fwd_dtype_ok(dtype)) return SPARTON_EINVAL;
+  const bool split = (dtype & SPARTON_F32_SPLIT) != 0;
+  dtype &= ~SPARTON_F32_SPLIT;
   if (mask_dtype < SPARTON_MASK_I64 || mask_dtype > SPARTON_MASK_F16) return SPARTON_EINVAL;
   if (B == 0 || V == 0) return SPARTON_OK;
   // Only pointers that will be dereferenced must be non-null (empty tensors may
@@ -1520,13 +1624,13 @@ static int fwd_run(const void* hidden, const void* weight, const void* bias, con
     int rc;
     switch (dtype) {
       case SPARTON_BF16:
-        rc = fwd::launch<bf16>(h, weight, bias, mk, mask_dtype, r, am, r32, nb, S, D, V, w, st, evp);
+        rc = fwd::launch<bf16>(h, weight, bias, mk, mask_dtype, r, am, r32, nb, S, D, V, w, st, evp, false);
         break;
       case SPARTON_F16:
-        rc = fwd::launch<f16>(h, weight, bias, mk, mask_dtype, r, am, r32, nb, S, D, V, w, st, evp);
+        rc = fwd::launch<f16>(h, weight, bias, mk, mask_dtype, r, am, r32, nb, S, D, V, w, st, evp, false);
         break;
       default:
-        rc = fwd::launch<float>(h, weight, bias, mk, mask_dtype, r, am, r32, nb, S, D, V, w, st, evp);
+        rc = fwd::launch<float>(h, weight, bias, mk, mask_dtype, r, am, r32, nb, S, D, V, w, st, evp, split);
         break;
     }
     if (main_ms != nullptr) {
@@ -1598,7 +1702,7 @@ extern "C" __attribute__((visibility("default"))) int sparton_fwd_noalloc(
     int mask_dtype, void* reps, int32_t* argmax, float* reps_f32, int64_t B, int64_t S,
     int64_t D, int64_t V, int dtype, void* stream) {
   if (B < 0 || S < 0 || D < 0 || V < 0) return SPARTON_EINVAL;
-  if (dtype < SPARTON_F32 || dtype > SPARTON_F16) return SPARTON_EINVAL;
+  if (!fwd_dtype_ok(dtype)) return SPARTON_EINVAL;
   if (mask_dtype < SPARTON_MASK_I64 || mask_dtype > SPARTON_MASK_F16) return SPARTON_EINVAL;
   const size_t need = sparton_fwd_workspace_bytes(B, S, D, V, dtype);
   if (need > kNoAllocScratchBytes) return SPARTON_ESCRATCH;

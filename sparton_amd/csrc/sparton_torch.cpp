@@ -51,6 +51,17 @@ int dtype_code(at::ScalarType t) {
   }
 }
 
+// The forward's dtype: fp32 follows torch's float32 matmul precision ('high' and 'medium':
+// the bf16 hi/lo split, SPARTON_F32_SPLIT; 'highest': exact fp32), as the reference's GEMM
+// does under the 'high' it sets at import (sparton_kernel.py:14).
+int fwd_dtype_code(at::ScalarType t) {
+  const int code = dtype_code(t);
+  if (t == at::kFloat &&
+      at::globalContext().float32MatmulPrecision() != at::Float32MatmulPrecision::HIGHEST)
+    return code | SPARTON_F32_SPLIT;
+  return code;
+}
+
 int mask_code(at::ScalarType t) {
   switch (t) {
     case at::kLong: return SPARTON_MASK_I64;
@@ -95,7 +106,7 @@ struct FwdOut {
 FwdOut head_fwd(const Tensor& h, const Tensor& w, const Tensor& b, const Tensor& m, bool with_idx,
                 bool with_f32) {
   const int64_t B = h.size(0), S = h.size(1), D = h.size(2), V = w.size(0);
-  const int dt = dtype_code(h.scalar_type());
+  const int dt = fwd_dtype_code(h.scalar_type());
   FwdOut o;
   o.reps = at::empty({B, V}, h.options());
   if (with_idx) o.idx = at::empty({B, V}, h.options().dtype(at::kInt));

@@ -85,7 +85,7 @@ def _fwd_impl(hidden: Tensor, embed: Tensor, bias: Optional[Tensor], mask: Tenso
     idx = torch.empty((B, V), dtype=torch.int32, device=dev) if with_idx else None
     reps32 = torch.empty((B, V), dtype=torch.float32, device=dev) if with_f32 else None
     L = _lib.load()
-    dt = _lib.DTYPE_CODE[hidden.dtype]
+    dt = _lib.fwd_dtype_code(hidden.dtype)
     ws_bytes = int(L.sparton_fwd_workspace_bytes(B, S, D, V, dt))
     ws = torch.empty((max(ws_bytes, 1),), dtype=torch.uint8, device=dev)
     with torch.cuda.device(dev):

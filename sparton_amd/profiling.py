@@ -44,8 +44,13 @@ def short_name(name):
         kname = rest[len(klen.group(1)):len(klen.group(1)) + int(klen.group(1))] if klen else rest
         t = {"DF16b": "bf16", "DF16_": "f16", "f": "f32"}[m.group(5)]
         return f"sparton::{ns}::{kname}<{t}>"
+    # rocprof's demangled names of kernels with int/bool template arguments: keep short
+    # argument lists ('sparton::fwd::fwd_small_kernel<float, 2, true>'), elide long ones
+    m = re.match(r"(?:void )?(sparton::\w+::\w+)<([^()]*)>\(", name)
+    if m and len(m.group(2)) <= 40:
+        return f"{m.group(1)}<{m.group(2)}>"
     m = re.match(r"(?:void )?(sparton::\w+::\w+)<", name)
-    if m and ("_Accum" in name or len(name) >= 90):  # rocprof's demangling of bool/int template args
+    if m and ("_Accum" in name or len(name) >= 90):
         return m.group(1) + "<...>"
     return name if len(name) < 90 else name[:87] + "..."
 

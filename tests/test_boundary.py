@@ -77,14 +77,35 @@ def bwd(**kw):
     (dict(ws=P + 16), -2),
     (dict(S=1 << 24), -3),                # a batch row of H reaches 2^31 bytes
     (dict(S=20000, ws_bytes=16), -4),     # S > 16384 is accepted (stops at the workspace)
+    (dict(dtype=1 | 0x100), -1),          # SPARTON_F32_SPLIT only with SPARTON_F32
+    (dict(dtype=0x200), -1),              # no other flag bits
+    (dict(dtype=0x100, D=62), -1),        # fp32 rows of 248 bytes: not a multiple of 16
+    (dict(dtype=0x100, ws=None), -4),     # fp32 split is accepted (stops at the workspace)
+    (dict(dtype=0x100, B=0), 0),
 ])
 def test_fwd_argument_validation(kw, code):
     assert fwd(**kw) == code
 
 
+def test_fwd_dtype_code_follows_torch_fp32_precision():
+    """fp32 takes the bf16 hi/lo split (SPARTON_F32_SPLIT) under torch's 'high' or 'medium'
+    float32 matmul precision (the reference sets 'high' at import, sparton_kernel.py:14),
+    exact fp32 under 'highest'; 16-bit dtypes never carry the flag."""
+    prev = torch.get_float32_matmul_precision()
+    try:
+        for prec, want in (("highest", 0), ("high", 0x100), ("medium", 0x100)):
+            torch.set_float32_matmul_precision(prec)
+            assert _lib.fwd_dtype_code(torch.float32) == want
+            assert _lib.fwd_dtype_code(torch.bfloat16) == 1
+            assert _lib.fwd_dtype_code(torch.float16) == 2
+    finally:
+        torch.set_float32_matmul_precision(prev)
+
+
 @pytest.mark.parametrize("kw,code", [
     (dict(S=-2), -1), (dict(dtype=-1), -1), (dict(reps_dtype=3), -1), (dict(grad_dtype=2), -1),
     (dict(reps_dtype=2), -1),  # reps must be fp32 or the parameters' dtype (bf16 here)
+    (dict(dtype=0x100), -1),   # the split flag is the forward's only
     (dict(grad=None), -1), (dict(dH=P + 4, grad_dtype=1, ws=P, ws_bytes=1 << 30), -2),
     (dict(dW=P + 8, grad_dtype=0, ws=P, ws_bytes=1 << 30), -2),
     (dict(weight=None), -1),

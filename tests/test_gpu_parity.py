@@ -713,6 +713,70 @@ def test_small_batch_path_equals_main_path(case, device, monkeypatch):
     say(f"  checked {n} entries, {bad} near-tie argmax differences")
 
 
+SPLIT_CASES = [
+    ("fp32", 2, 32, 768, 3000, True, "int64"),     # config 1's rows and width
+    ("fp32", 1, 100, 1024, 2000, False, "frac"),   # four 32-row blocks, fractional mask
+    ("fp32", 4, 32, 72, 500, True, "holes"),       # 288-byte rows: a 32-byte tail slab
+    ("fp32", 3, 40, 4, 300, True, "bool"),         # D = 4: one 16-byte chunk per row
+    ("fp32", 2, 48, 2048, 1200, False, "int64"),   # 64 full slabs
+]
+
+
+@pytest.mark.parametrize("case", SPLIT_CASES, ids=lambda c: "-".join(map(str, c)))
+def test_fp32_split_precision(case, device):
+    """Under torch's 'high' float32 matmul precision, which the reference sets at import
+    (sparton_kernel.py:14), small fp32 batches take each product as bf16 hi*hi + hi*lo +
+    lo*hi, within 3 * 2^-18 relative of the exact product. Checked against the oracle with
+    the tie band widened by that bound, and entry by entry: the fp32 reps against log1p of
+    the exact logit at the chosen index,
+    |reps - log1p(x)| <= (2^-18 x + (gamma_{D+2} + 3 * 2^-18) * sum|h w + b|) / (1 + x)
+    + 2^-23 + 2^-21 log1p(x). 'highest' gives the exact path back (bitwise the main path)."""
+    say(f"fp32 split precision, case {case}")
+    H, W, b, m, _ = make_case(*case)
+    Hd, Wd, md = H.to(device), W.to(device), m.to(device)
+    bd = None if b is None else b.to(device)
+    prev = torch.get_float32_matmul_precision()
+    try:
+        torch.set_float32_matmul_precision("high")
+        reps, idx, r32 = [t.clone() for t in torch.ops.sparton.fused_sparton_fwd_train(Hd, Wd, bd, md)]
+        # the C++ eager op (SpartonHead's path) reads the same setting
+        from sparton_amd import _eager
+        assert torch.equal(_eager.load().head_encode(Hd, Wd, bd, md), reps)
+        torch.set_float32_matmul_precision("highest")
+        exact = [t.clone() for t in torch.ops.sparton.fused_sparton_fwd_train(Hd, Wd, bd, md)]
+    finally:
+        torch.set_float32_matmul_precision(prev)
+    torch.cuda.synchronize()
+    n, bad = check_fwd(H, W, b, m, reps, idx, split=True)
+    say(f"  checked {n} entries, {bad} near-tie argmax differences")
+    # the value at the chosen index
+    idx_c = idx.cpu().long()
+    x = oracle.logit_at(H, W, b, m, idx_c)
+    A = oracle.logit_at(H.abs(), W.abs(), None if b is None else b.abs(),
+                        m if m.dtype == torch.bool else m.abs(), idx_c)
+    D = H.shape[-1]
+    r = r32.cpu().to(F64)
+    pos = r > 0
+    lx = torch.log1p(x.clamp_min(0))
+    bound = ((2.0 ** -18 * x.abs() + ((D + 2) * 2.0 ** -24 + 3 * 2.0 ** -18) * A) / (1 + x.clamp_min(0))
+             + 2.0 ** -23 + 2.0 ** -21 * lx)
+    err = (r - lx).abs()
+    assert bool((err[pos] <= bound[pos]).all()), float((err - bound)[pos].max())
+    say(f"  max |reps - log1p(x)| = {float(err[pos].max()):.3e}")
+    # the exact path is unchanged: bitwise the main kernel's fp32
+    main = None
+    os.environ["SPARTON_FWD_PATH"] = "main"
+    try:
+        main = torch.ops.sparton.fused_sparton_fwd_train(Hd, Wd, bd, md)
+    finally:
+        del os.environ["SPARTON_FWD_PATH"]
+    torch.cuda.synchronize()
+    for a, c in zip(exact, main):
+        assert torch.equal(a, c)
+    if D >= 64:  # the split path is a different computation (its values move at 2^-18)
+        assert not torch.equal(r32, exact[2])
+
+
 @pytest.mark.parametrize("dt", [1, 2])
 def test_mfma_probe_reports_cycles(dt, device):
     """sparton_mfma_probe (the measurement kernel bench.py reports as mfma_ceiling) runs on
