@@ -700,6 +700,13 @@ __device__ __forceinline__ void wait_all() {
   asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
 }
 
+// Step 0 of a prefetched unit: wait for every memory operation but the three metadata loads
+// issued last (vector memory operations complete in issue order). Slab 1's copies, issued
+// before them, have landed; the metadata is waited for at step 1.
+__device__ __forceinline__ void wait_all_but_meta() {
+  asm volatile("s_waitcnt vmcnt(3) lgkmcnt(0)" ::: "memory");
+}
+
 // ---- the workgroup's unit sequence ----
 //
 // Both roles walk the same sequence and pass the same barriers:
@@ -878,9 +885,13 @@ __device__ void copy_path(Smem& sm, const Args<T>& a, const Outputs<T>& o, int w
           if (ct == 0) um_next.mask_binary = 1;
           __builtin_amdgcn_global_load_lds((const void*)(a.rowmask + (int64_t)nx.m * BM + ct),
                                            (lds_void*)&um_next.maskf[c * 64], 4, 0, 0);
-          if (ct < NGRP + 2)
-            code_bits = a.list[min(max(group_entry(nx.m, ct), 0), a.n_grp - 1)];
-          if (a.bias != nullptr) bias_bits = load_bits(a.bias, min(nx.v0 + ct, a.V - 1));
+          // Exactly three memory loads per wave, issued whatever the lane: the mask copy
+          // above, the list entry (used by lanes < NGRP + 2) and the bias bits (a dummy
+          // read of the list without bias), so that step 0 can wait for slab 1 alone.
+          code_bits = a.list[min(max(group_entry(nx.m, min(ct, NGRP + 1)), 0), a.n_grp - 1)];
+          const T* bsrc = a.bias != nullptr ? a.bias + min(nx.v0 + ct, a.V - 1)
+                                            : reinterpret_cast<const T*>(a.list);
+          bias_bits = load_bits(bsrc, 0);
         } else if (k == 2) {
           const int e = group_entry(nx.m, ct);
           const bool ok = e >= 0 && e < a.n_grp && (ct >= NGRP || ct < nx.n_valid);
@@ -898,7 +909,10 @@ __device__ void copy_path(Smem& sm, const Args<T>& a, const Outputs<T>& o, int w
                       o.reps_f32, o.part);
         prev.u = -1;
       }
-      wait_all();
+      if (k == 0 && pre)
+        wait_all_but_meta();  // slab 1 (issued before E) landed; the metadata loads may not have
+      else
+        wait_all();
       if (k + 1 < nk) {
         if (k + 1 >= a.nk_full) zero_tail(sm, a.row_bytes, k + 1, buf ^ ((k + 1) & 1), c, lane);
       } else if (pre && 0 >= a.nk_full) {
