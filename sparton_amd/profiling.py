@@ -47,7 +47,7 @@ def short_name(name):
     # rocprof's demangled names of kernels with int/bool template arguments: keep short
     # argument lists ('sparton::fwd::fwd_small_kernel<float, 2, true>'), elide long ones
     m = re.match(r"(?:void )?(sparton::\w+::\w+)<([^()]*)>\(", name)
-    if m and len(m.group(2)) <= 40:
+    if m and len(m.group(2)) <= 40 and "_Accum" not in name:
         return f"{m.group(1)}<{m.group(2)}>"
     m = re.match(r"(?:void )?(sparton::\w+::\w+)<", name)
     if m and ("_Accum" in name or len(name) >= 90):
