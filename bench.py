@@ -161,6 +161,7 @@ def cpu_baseline(torch, w, inp, budget_s):
         "affinity_cpus": threads,
         "omp_num_threads_env": os.environ.get("OMP_NUM_THREADS"),
         "kind": "port",
+        "fp32_matmul_precision": torch.get_float32_matmul_precision(),
         "sample": (f"torch head (training/model.py:56-62, restated in oracle/) fwd+bwd autograd, "
                    f"{DTYPE_NAME[str(w.dtype)]}, {rows} of {w.B} batch rows ({rows * w.S} tokens), "
                    f"V-chunked by 8192, median of {n} after 1 warm-up; host CPU: {cpu_model()}"),
