@@ -620,7 +620,7 @@ def main():
                    "global_batch": w.B, "seq_len": w.S, "use_bias": has_bias,
                    "valid_tokens": valid_tokens, "parallelism": "none (1 GPU)",
                    **({"fp32_matmul_precision": args.fp32_precision,
-                       "fp32_products": ("bf16 hi*hi + hi*lo + lo*hi, fp32 accumulation (within 3*2^-18 "
+                       "fp32_products": ("bf16 hi*hi + hi*lo + lo*hi, fp32 accumulation (within 3*2^-16 "
                                          "relative per product)" if split else "fp32 MFMA"),
                        "main_ms_fp32_highest": (round(main_ms_exact, 4) if main_ms_exact else None)}
                       if dname == "fp32" else {})},

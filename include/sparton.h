@@ -49,7 +49,7 @@ enum sparton_dtype {
  * (src/sparton/sparton_kernel.py:14, torch.set_float32_matmul_precision('high')). Each
  * fp32 operand is taken as the sum of two bf16 values (hi = bf16(x), lo = bf16(x - hi)) and
  * each product as hi*hi + hi*lo + lo*hi on bf16 MFMAs with fp32 accumulation, within
- * 3 * 2^-18 relative of the exact product. It applies to the small-batch kernel
+ * 3 * 2^-16 relative of the exact product. It applies to the small-batch kernel
  * (B*S <= 128); larger batches are computed in fp32 exactly either way.
  */
 #define SPARTON_F32_SPLIT 0x100

@@ -486,8 +486,8 @@ template <> struct Mfma<float> {
 
 // fp32 as two bf16 ("split" mode, torch's 'high' float32 matmul precision): x = hi + lo + r
 // with hi = bf16(x) and lo = bf16(x - hi) (both round to nearest even; x - hi is exact), so
-// |r| <= 2^-18 |x|. A product is taken as hi_a hi_b + hi_a lo_b + lo_a hi_b: the dropped
-// lo_a lo_b and the residuals keep it within 3 * 2^-18 relative of the exact one. (An
+// |r| <= 2^-16 |x|. A product is taken as hi_a hi_b + hi_a lo_b + lo_a hi_b: the dropped
+// lo_a lo_b and the residuals keep it within 3 * 2^-16 relative of the exact one. (An
 // infinite x gives a NaN lo, so infinities in H or W come out as NaN in this mode.)
 typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2;
 typedef __attribute__((ext_vector_type(2))) float f32x2;
