@@ -950,3 +950,38 @@ def test_eager_cpp_head_equals_custom_ops(use_bias, device):
         if use_bias:
             head.bias.copy_(bd)
     assert torch.equal(head(Hd, md), e)  # no grad needed: the module takes head_encode
+
+
+def _sweep_cases(seed, n):
+    import random
+    rng = random.Random(seed)
+    out = []
+    for i in range(n):
+        dt = rng.choice(["bf16", "fp16", "fp32"])
+        B = rng.choice([1, 2, 3, 5, 8, 17])
+        S = rng.choice([1, 7, 16, 31, 64, 100])
+        D = rng.choice([8, 16, 64, 72, 200, 256]) if dt != "fp32" else rng.choice([4, 8, 64, 132, 256])
+        V = rng.choice([1, 31, 256, 300, 1000])
+        masks = ["int64", "bool", "holes", "frac", "int32"] + (["gaps"] if B >= 2 else [])
+        prec = rng.choice(["highest", "high"]) if dt == "fp32" else "highest"
+        out.append(((dt, B, S, D, V, rng.random() < 0.5, rng.choice(masks)), prec, i))
+    return out
+
+
+@pytest.mark.parametrize("case,prec,seed", _sweep_cases(7, 12),
+                         ids=lambda x: "-".join(map(str, x)) if isinstance(x, tuple) else str(x))
+def test_random_sweep(case, prec, seed, device):
+    """Seeded random shapes, dtypes, masks and (fp32) matmul precisions through the training
+    forward and the reference backward, against the oracle: edge sizes (V = 1, S = 1, D = 4,
+    K tails, ragged batch rows) mixed as a user's calls would mix them."""
+    say(f"sweep case {case} precision {prec}")
+    prev = torch.get_float32_matmul_precision()
+    try:
+        torch.set_float32_matmul_precision(prec)
+        H, W, b, m, G = make_case(*case, seed=seed)
+        reps, idx, reps32, dH, dW, db = run_fwd_bwd(H, W, b, m, G, device)
+    finally:
+        torch.set_float32_matmul_precision(prev)
+    n, bad = check_fwd(H, W, b, m, reps, idx, split=(prec == "high"))
+    check_bwd_isolated(H, W, b, m, G, reps32, idx, dH, dW, db)
+    say(f"  checked {n} entries, {bad} near-tie argmax differences")
