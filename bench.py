@@ -25,8 +25,10 @@ kernels drains the queue, so the per-op events live in their own pass.
                 epilogue kernel's compulsory bytes / mean duration vs 8 TB/s.
   loss          the SPLADE loss on reps of this shape (B queries, B documents): fused
                 vs eager torch fwd+bwd, and the HIP passes' compulsory bytes vs 8 TB/s.
+  library_gemm  torch.matmul (hipBLASLt) at the main kernel's executed GEMM shape.
   cpu_baseline  the reference's torch head (training/model.py:56-62, restated in
-                oracle/) fwd+bwd on the host cores, on a bounded sample of batch rows.
+                oracle/) fwd+bwd on the host cores, on a bounded sample of batch rows;
+                also its forward alone and the peak resident memory a step adds.
 """
 import argparse
 import json
@@ -118,8 +120,34 @@ def time_events(torch, fn, reps):
     return start.elapsed_time(end) / reps
 
 
+def _rss_kib(field):
+    """VmRSS / VmHWM of this process in KiB (Linux /proc), or None."""
+    try:
+        for ln in open("/proc/self/status"):
+            if ln.startswith(field + ":"):
+                return int(ln.split()[1])
+    except OSError:
+        pass
+    return None
+
+
+def _reset_peak_rss():
+    """Reset this process's peak resident set size (VmHWM) to its current size; True if the
+    kernel took the request (Linux >= 4.0, /proc/self/clear_refs)."""
+    try:
+        with open("/proc/self/clear_refs", "w") as f:
+            f.write("5")
+        return True
+    except OSError:
+        return False
+
+
 def cpu_baseline(torch, w, inp, budget_s):
-    """The reference torch head fwd+bwd on the host, on the first rows of the batch."""
+    """The reference torch head on the host, on the first rows of the batch: fwd+bwd through
+    autograd (the value), the forward alone (autograd on, as in training), and the peak
+    resident memory one fwd+bwd step adds to the process."""
+    import resource
+
     import oracle
     # every core this process may run on (its CPU affinity), recorded beside the host's count
     threads = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
@@ -133,13 +161,15 @@ def cpu_baseline(torch, w, inp, budget_s):
         state["b"] = inp.bias.clone().requires_grad_() if inp.bias is not None else None
         state["m"], state["G"] = inp.mask[:rows], inp.grad[:rows]
 
-    def step():
-        out = oracle.torch_head_chunked(state["H"], state["W"], state["b"], state["m"], v_chunk=8192)
-        out.backward(state["G"])
+    def fwd():
+        return oracle.torch_head_chunked(state["H"], state["W"], state["b"], state["m"], v_chunk=8192)
 
-    def timed():
+    def step():
+        fwd().backward(state["G"])
+
+    def timed(fn=step):
         t0 = time.perf_counter()
-        step()
+        fn()
         return time.perf_counter() - t0
 
     # Size the sample so that about 5 timed steps fill the budget.
@@ -151,20 +181,38 @@ def cpu_baseline(torch, w, inp, budget_s):
     timed()  # warm-up at the final size
     times = [timed() for _ in range(5)]
     t = statistics.median(times)
+    fwd_times = [timed(fwd) for _ in range(5)]
+    t_fwd = statistics.median(fwd_times)
+    # peak memory of one fwd+bwd step above what the process held before it
+    hwm_reset = _reset_peak_rss()
+    rss0, maxrss0 = _rss_kib("VmRSS"), resource.getrusage(resource.RUSAGE_SELF).ru_maxrss
+    step()
+    hwm1, maxrss1 = _rss_kib("VmHWM"), resource.getrusage(resource.RUSAGE_SELF).ru_maxrss
+    peak_delta_kib = (hwm1 - rss0) if (hwm_reset and hwm1 is not None and rss0 is not None) \
+        else maxrss1 - maxrss0
     n = len(times)
     return {
         "value": rows * w.S / t,
-        "seconds": round(sum(times), 2),
+        "seconds": round(sum(times) + sum(fwd_times), 2),
         "unit": "tokens/s",
         "cores": torch.get_num_threads(),
+        "fwd_tokens_per_s": rows * w.S / t_fwd,
+        "fwd_bwd_ms": round(t * 1e3, 2),
+        "fwd_ms": round(t_fwd * 1e3, 2),
+        "peak_rss_delta_gb": round(peak_delta_kib * 1024 / 1e9, 3),
+        "peak_rss_basis": ("VmHWM after one fwd+bwd step minus VmRSS before it, the peak reset "
+                           "through /proc/self/clear_refs" if hwm_reset else
+                           "getrusage ru_maxrss delta over one fwd+bwd step (a lower bound: the "
+                           "process's earlier peak could not be reset)"),
         "host_cpu_count": os.cpu_count(),
         "affinity_cpus": threads,
         "omp_num_threads_env": os.environ.get("OMP_NUM_THREADS"),
         "kind": "port",
         "fp32_matmul_precision": torch.get_float32_matmul_precision(),
-        "sample": (f"torch head (training/model.py:56-62, restated in oracle/) fwd+bwd autograd, "
-                   f"{DTYPE_NAME[str(w.dtype)]}, {rows} of {w.B} batch rows ({rows * w.S} tokens), "
-                   f"V-chunked by 8192, median of {n} after 1 warm-up; host CPU: {cpu_model()}"),
+        "sample": (f"torch head (training/model.py:56-62, restated in oracle/) fwd+bwd autograd "
+                   f"(value) and fwd alone, {DTYPE_NAME[str(w.dtype)]}, {rows} of {w.B} batch rows "
+                   f"({rows * w.S} tokens), V-chunked by 8192, median of {n} after 1 warm-up; "
+                   f"host CPU: {cpu_model()}"),
     }
 
 
@@ -230,6 +278,36 @@ def mfma_ceiling(torch, dtype_name, target_ms=1.0):
             "ms": round(ms, 3), "workgroups": grid,
             "what": "sparton_mfma_probe: 4 waves per CU, independent v_mfma_f32_32x32x16 on random "
                     "register operands, all CUs at once (power-limited rate); HIP events"}
+
+
+def library_gemm(torch, w, mask, reps_n):
+    """torch.matmul (hipBLASLt) at the forward main kernel's executed GEMM shape: M = the
+    packed rows it multiplies (active 16-position groups, rounded up to whole 256-row
+    tiles), K = D, N = V, in the workload's 16-bit dtype, output in that dtype; timed back to
+    back with HIP events. A dense library GEMM on random operands, for comparison with the
+    fused kernel's rate (the kernel also reduces over S and never writes the [M, V] logits)."""
+    if w.dtype not in (torch.bfloat16, torch.float16):
+        return None
+    dev = mask.device
+    valid = torch.nn.functional.pad(mask.ne(0), (0, (-w.S) % 16))
+    groups = int(valid.view(w.B, -1, 16).any(-1).sum())
+    M = -(-groups // 16) * 256
+    gen = torch.Generator(device=dev).manual_seed(3)
+    A = torch.randn(M, w.D, device=dev, generator=gen).to(w.dtype)
+    Wm = (torch.randn(w.V, w.D, device=dev, generator=gen) * 0.02).to(w.dtype)
+    out = torch.empty(M, w.V, device=dev, dtype=w.dtype)
+    fn = lambda: torch.matmul(A, Wm.t(), out=out)
+    fn()
+    ms = time_events(torch, fn, reps_n)
+    flops = 2.0 * M * w.D * w.V
+    tf = flops / (ms * 1e-3) / 1e12
+    peak = PEAK_TFLOPS[DTYPE_NAME[str(w.dtype)]]
+    del A, Wm, out
+    return {"M": M, "K": w.D, "N": w.V, "ms": round(ms, 4), "tflops": round(tf, 1),
+            "frac_of_peak": round(tf / peak, 4),
+            "out_bytes": M * w.V * torch.tensor([], dtype=w.dtype).element_size(),
+            "what": "torch.matmul(A[M,K], W[N,K].t()) -> [M,N] (hipBLASLt), the main kernel's "
+                    "executed rows; HIP events over back-to-back calls"}
 
 
 def time_device(torch, fn, reps):
@@ -597,6 +675,7 @@ def main():
     fwd_bound = "mfma" if t_mfma >= t_hbm else "hbm"
     traffic, traffic_src = measured_traffic(args.config, kname)
     ceiling = mfma_ceiling(torch, dname)
+    libgemm = library_gemm(torch, w, mask, args.kernel_reps)
     # whole-step roofline: the forward at the MFMA peak plus the backward's
     # compulsory bytes at HBM peak, over the measured step; useful flops only
     t_step = elapsed / args.steps
@@ -650,6 +729,7 @@ def main():
         "step_tflops": round(step_flops / t_step / 1e12, 2),
         "step_tflops_basis": "(2*D*V*valid_tokens + 4*nnz*D) / measured step",
         "mfma_ceiling": ceiling,
+        "library_gemm": libgemm,
         "bwd_roofline": {"bound": "hbm", "achieved": round(bwd_gbs, 1), "peak": PEAK_HBM_GBS,
                          "unit": "GB/s", "frac": round(bwd_gbs / PEAK_HBM_GBS, 4),
                          "bytes_per_call": bwd_bytes, "nnz": nnz, "U_W": u_w, "U_H": u_h,

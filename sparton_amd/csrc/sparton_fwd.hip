@@ -487,15 +487,27 @@ template <> struct Mfma<float> {
 // fp32 as two bf16 ("split" mode, torch's 'high' float32 matmul precision): x = hi + lo + r
 // with hi = bf16(x) and lo = bf16(x - hi) (both round to nearest even; x - hi is exact), so
 // |r| <= 2^-16 |x|. A product is taken as hi_a hi_b + hi_a lo_b + lo_a hi_b: the dropped
-// lo_a lo_b and the residuals keep it within 3 * 2^-16 relative of the exact one. (An
-// infinite x gives a NaN lo, so infinities in H or W come out as NaN in this mode.)
+// lo_a lo_b and the residuals keep it within 3 * 2^-16 relative of the exact one.
+// Non-finite values: x - hi is finite whenever hi is, and NaN or infinite when x is infinite
+// or NaN (or a finite x rounds to an infinite bf16). Such a pair moves its values into the lo
+// slot (hi = 0, lo = bf16(x)), so that of the three products only lo_a hi_b or hi_a lo_b sees
+// the infinity: an infinite operand times a finite partner gives the exact product's
+// infinity (or NaN where the partner's bf16 part is 0, as inf * 0 is), instead of adding
+// inf - inf across the terms. Both operands infinite at the same k give 0 * inf = NaN where
+// the exact product is infinite. A pair's two k belong to one dot product, which is infinite
+// or NaN either way, so the finite neighbour of an infinite value may lose its lo part.
 typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2;
 typedef __attribute__((ext_vector_type(2))) float f32x2;
 __device__ __forceinline__ void split_pair(float x0, float x1, uint32_t& hi, uint32_t& lo) {
   const f32x2 v = {x0, x1};
   hi = __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
   const f32x2 hf = {__uint_as_float(hi << 16), __uint_as_float(hi & 0xffff0000u)};
-  lo = __builtin_bit_cast(uint32_t, __builtin_convertvector(v - hf, bf16x2));
+  const f32x2 d = v - hf;
+  lo = __builtin_bit_cast(uint32_t, __builtin_convertvector(d, bf16x2));
+  if (!__builtin_isfinite(d.x + d.y)) {
+    lo = hi;
+    hi = 0u;
+  }
 }
 // Eight floats (x0: k = 0..3, x1: k = 4..7) as bf16x8 hi and lo parts in k order.
 __device__ __forceinline__ void split8(const u32x4& x0, const u32x4& x1, u32x4& hi, u32x4& lo) {
@@ -885,12 +897,14 @@ __device__ void copy_path(Smem& sm, const Args<T>& a, const Outputs<T>& o, int w
           if (ct == 0) um_next.mask_binary = 1;
           __builtin_amdgcn_global_load_lds((const void*)(a.rowmask + (int64_t)nx.m * BM + ct),
                                            (lds_void*)&um_next.maskf[c * 64], 4, 0, 0);
-          // Exactly three memory loads per wave, issued whatever the lane: the mask copy
-          // above, the list entry (used by lanes < NGRP + 2) and the bias bits (a dummy
-          // read of the list without bias), so that step 0 can wait for slab 1 alone.
+          // Exactly three vector memory loads per wave, issued whatever the lane: the mask
+          // copy above, the list entry (used by lanes < NGRP + 2) and the bias bits (a dummy
+          // read of the list without bias), so that step 0 can wait for slab 1 alone. Both
+          // addresses depend on the lane, so neither can become a scalar load (which the
+          // vector memory count would not track).
           code_bits = a.list[min(max(group_entry(nx.m, min(ct, NGRP + 1)), 0), a.n_grp - 1)];
           const T* bsrc = a.bias != nullptr ? a.bias + min(nx.v0 + ct, a.V - 1)
-                                            : reinterpret_cast<const T*>(a.list);
+                                            : reinterpret_cast<const T*>(a.list + min(ct, a.n_grp - 1));
           bias_bits = load_bits(bsrc, 0);
         } else if (k == 2) {
           const int e = group_entry(nx.m, ct);

@@ -8,6 +8,7 @@ training/model.py:72-85 (ProjectionSparton) uses it unchanged.
 from __future__ import annotations
 
 import math
+import weakref
 
 import torch
 import torch.nn.functional as F
@@ -21,11 +22,15 @@ class _CastCache:
     parameter is unchanged, so the head's calls between two optimizer steps (train.py calls
     it for queries and for documents, training/train.py:165-172) share one cast of W.
 
-    A copy is keyed on the parameter's storage address, its version counter, dtype and
-    padding: an in-place update (an optimizer step, load(), copy_) bumps the version counter,
-    re-binding (tie_weights) changes the address, and either makes the next call cast again.
-    Writes through `param.data` are not versioned by torch and are not seen: update
-    parameters in place under torch.no_grad() instead."""
+    A copy is tied to the parameter object itself (a weak reference, so a new tensor that
+    reuses a freed address is a different key), its storage address, its version counter,
+    dtype and padding: an in-place update (an optimizer step, load(), copy_) bumps the version
+    counter, re-binding (tie_weights) changes the object, and either makes the next call cast
+    again. Training also drops every copy when a backward runs through the head (a hook on
+    the output's gradient): whatever updates the parameters after that backward -- including
+    optimizers that write through `param.data`, which torch does not version -- is seen by
+    the next forward. Inference calls with no backward in between keep their copy: update
+    parameters in place under torch.no_grad() (versioned) rather than through `.data`."""
 
     def __init__(self):
         self._entries = {}
@@ -33,17 +38,28 @@ class _CastCache:
     def __call__(self, t, dt, pad, slot):
         key = (t.data_ptr(), t._version, tuple(t.shape), dt, pad)
         hit = self._entries.get(slot)
-        if hit is not None and hit[0] == key:
+        if hit is not None and hit[0] == key and hit[2]() is t:
             return hit[1]
         with torch.no_grad():
             v = t.detach().to(dt)
             if pad:
                 v = F.pad(v, (0, pad))
-        self._entries[slot] = (key, v)
+        self._entries[slot] = (key, v, weakref.ref(t))
         return v
 
     def clear(self):
         self._entries.clear()
+
+    def clear_on_backward(self, out):
+        """Drop the copies when the gradient of `out` is computed (the backward that precedes
+        the optimizer step); returns `out`."""
+        entries = self._entries
+
+        def hook(grad):
+            entries.clear()
+
+        out.register_hook(hook)
+        return out
 
 
 class SpartonHead(nn.Module):
@@ -98,8 +114,9 @@ class SpartonHead(nn.Module):
                 wc = self._cast_cache(weight, dt, pad, "weight")
                 bc = self._cast_cache(bias, dt, 0, "bias") if bias is not None else None
                 _check_autocast(hidden, weight, bias, attention_mask, wc)
-                return _eager.load().head_train_autocast(hidden, weight, bias, attention_mask,
-                                                         wc, bc, pad)
+                out = _eager.load().head_train_autocast(hidden, weight, bias, attention_mask,
+                                                        wc, bc, pad)
+                return self._cast_cache.clear_on_backward(out)
             if (weight.dtype == torch.float32 and not torch.compiler.is_compiling()
                     and not (torch.is_grad_enabled() and weight.requires_grad)):
                 weight = self._cast_cache(weight, dt, 0, "weight")  # inference: reuse the cast copy

@@ -96,3 +96,95 @@ def check_bwd_isolated(H, W, b, m, G, reps, idx, dH, dW, db):
     if b is not None:
         torch.testing.assert_close(db.cpu().to(F64), rb, **BWD_TOL)
     return rH, rW, rb
+
+
+U64 = 2.0 ** -53          # fp64 unit roundoff
+
+
+def check_fwd_full_gpu(Hd, Wd, bd, md, reps, idx, split=False, chunk=None):
+    """Every (b, v) of a full-size forward against logits recomputed on the GPU by a library
+    routine: V-chunked float64 GEMMs (torch.matmul), x = (H W^T + b) * m, M = max(0, max_s x)
+    and its index. reps within FWD_TOL of log1p(M); a zero rep carries index 0; an index that
+    differs from the recomputed one must be a near-tie: the recomputed logit at it lies within
+    tau of M, tau as in check_fwd, widened by the float64 GEMM's own bound
+    (D+2) * 2^-53 * (A(idx) + A(I)). Returns (n_checked, n_index_mismatch)."""
+    B, S, D = Hd.shape
+    V = Wd.shape[0]
+    if chunk is None:
+        chunk = max(256, min(8192, (1 << 27) // max(1, B * S * 8)))
+    gam = (D + 2) * U32 + (D + 2) * U64 + (SPLIT_REL if split else 0.0)
+    H64 = Hd.reshape(B * S, D).double()
+    Ha = H64.abs()
+    m64 = md.double()
+    ma = m64.abs()
+    reps, idx = reps.double(), idx.long()
+    n_bad = 0
+    for v0 in range(0, V, chunk):
+        v1 = min(V, v0 + chunk)
+        C = v1 - v0
+        Wc = Wd[v0:v1].double()
+        X = (H64 @ Wc.t()).view(B, S, C)
+        A = (Ha @ Wc.abs().t()).view(B, S, C)
+        if bd is not None:
+            bc = bd[v0:v1].double()
+            X += bc
+            A += bc.abs()
+        X *= m64[:, :, None]
+        A *= ma[:, :, None]
+        M, I = X.max(dim=1)
+        M = M.clamp_min(0.0)
+        I = torch.where(M > 0, I, torch.zeros_like(I))
+        r, ix = reps[:, v0:v1], idx[:, v0:v1]
+        torch.testing.assert_close(r, torch.log1p(M), **FWD_TOL)
+        assert int(ix.min()) >= 0 and int(ix.max()) < max(S, 1), "argmax out of range"
+        zero = r == 0
+        assert bool((ix[zero] == 0).all()), (
+            f"cols {v0}..{v1}: {int((ix[zero] != 0).sum())} zero reps carry a nonzero argmax")
+        bad = ix != I
+        nb = int(bad.sum())
+        if nb:
+            x_at = X.gather(1, ix.view(B, 1, C)).view(B, C)
+            A_at = A.gather(1, ix.view(B, 1, C)).view(B, C)
+            A_I = A.gather(1, I.view(B, 1, C)).view(B, C)
+            tau = KEY_REL * M.abs() + gam * (A_at + A_I) + 4 * U32 * M.abs()
+            pos = bad & (r != 0)
+            near = x_at >= M - tau
+            assert bool(near[pos].all()), (
+                f"cols {v0}..{v1}: {int((~near & pos).sum())} argmax entries are not near-ties")
+            zb = bad & (r == 0)
+            small = M <= KEY_REL * M.abs() + gam * 2 * A_I + 4 * U32 * M.abs()
+            assert bool(small[zb].all()), (
+                f"cols {v0}..{v1}: {int((~small & zb).sum())} zero reps where the max is clearly positive")
+        n_bad += nb
+    return B * V, n_bad
+
+
+def check_dw_identity_gpu(Gd, reps32, idx, Hd, md, dW, chunk=None):
+    """Every row of dW against the identity dW[v,:] = sum_b g'[b,v] H[b, I[b,v], :], with
+    g' = G exp(-reps) m[b,I] where reps > 0, evaluated in float64 on the GPU at the GPU's own
+    reps and argmax. The kernel sums B products in fp32 from a g' with one expf, so
+    |dW - ref| <= (B + 8) * 2^-24 * sum_b |g' H| elementwise."""
+    B, S, D = Hd.shape
+    V = dW.shape[0]
+    if chunk is None:
+        chunk = max(64, (1 << 27) // max(1, B * D * 8))
+    r = reps32.double()
+    ix = idx.long()
+    mI = md.double().gather(1, ix)
+    gp = torch.where(r > 0, Gd.double() * torch.exp(-r), torch.zeros_like(r)) * mI
+    H64 = Hd.double()
+    rows = torch.arange(B, device=Hd.device).view(B, 1)
+    worst = 0.0
+    for v0 in range(0, V, chunk):
+        v1 = min(V, v0 + chunk)
+        Hg = H64[rows, ix[:, v0:v1]]                      # [B, C, D]
+        g = gp[:, v0:v1, None]
+        ref = (g * Hg).sum(0)
+        bound = (B + 8) * U32 * (g.abs() * Hg.abs()).sum(0)
+        err = (dW[v0:v1].double() - ref).abs()
+        ok = err <= bound + 1e-30
+        assert bool(ok.all()), (
+            f"dW rows {v0}..{v1}: {int((~ok).sum())} elements off the identity; worst "
+            f"{float((err - bound).max()):.3e} above the bound")
+        worst = max(worst, float((err / (bound + 1e-30)).max()))
+    return worst

@@ -13,7 +13,8 @@ import oracle
 import sparton
 from sparton_amd import _lib
 from sparton_amd.workloads import WORKLOADS, make_inputs
-from _parity import BWD_TOL, F64, FWD_TOL, check_bwd_isolated, check_fwd, say
+from _parity import (BWD_TOL, F64, FWD_TOL, check_bwd_isolated, check_dw_identity_gpu,
+                     check_fwd, check_fwd_full_gpu, say)
 
 pytestmark = pytest.mark.gpu
 
@@ -163,16 +164,40 @@ def sample_cols(V, n=1024, tail=64, seed=0):
     return torch.unique(torch.cat([cols, torch.arange(max(0, V - tail), V)]))
 
 
-@pytest.mark.parametrize("cfg", [1, 2, 3, 4, 5])
-def test_baseline_config_full_size(cfg, device):
+@pytest.mark.parametrize("cfg,prec", [(1, "highest"), (1, "high"), (2, None), (3, None), (4, None),
+                                      (5, None)])
+def test_baseline_config_full_size(cfg, prec, device):
+    """Each BASELINE config at full size. Config 1 (fp32) runs under torch's 'highest' (exact
+    fp32 MFMAs) and 'high' (the bf16 hi/lo split kernel, the bench default) matmul precision,
+    every column against the CPU oracle. Configs 2-5: every (b, v) of reps and argmax against
+    float64 library GEMMs on the GPU, every dW row against the identity dW = G'^T H[b, I] on
+    the GPU, dH in full against the CPU oracle, and the fp64 oracle on sampled columns."""
     w = WORKLOADS[cfg]
-    say(f"config {cfg} {w.name} B={w.B} S={w.S} D={w.D} V={w.V} {w.dtype}")
+    say(f"config {cfg} {w.name} B={w.B} S={w.S} D={w.D} V={w.V} {w.dtype} precision={prec}")
     inp = make_inputs(w)
     H, W, b, m, G = inp.hidden, inp.weight, inp.bias, inp.mask, inp.grad
-    reps, idx, reps32, dH, dW, db = run_fwd_bwd(H, W, b, m, G, device)
+    old_prec = torch.get_float32_matmul_precision()
+    if prec is not None:
+        torch.set_float32_matmul_precision(prec)
+    try:
+        reps, idx, reps32, dH, dW, db = run_fwd_bwd(H, W, b, m, G, device)
+    finally:
+        torch.set_float32_matmul_precision(old_prec)
+    split = prec == "high"
     cols = None if cfg == 1 else sample_cols(w.V)
-    n, bad = check_fwd(H, W, b, m, reps, idx, cols)
-    say(f"  fwd: checked {n} entries, {bad} near-tie argmax differences")
+    n, bad = check_fwd(H, W, b, m, reps, idx, cols, split=split)
+    say(f"  fwd (oracle): checked {n} entries, {bad} near-tie argmax differences")
+    if cfg != 1:
+        torch.set_float32_matmul_precision("highest")
+        try:
+            n, bad = check_fwd_full_gpu(H.to(device), W.to(device), None if b is None else b.to(device),
+                                        m.to(device), reps, idx)
+        finally:
+            torch.set_float32_matmul_precision(old_prec)
+        say(f"  fwd (every column, fp64 GEMM on the GPU): checked {n} entries, {bad} near-tie "
+            f"argmax differences")
+        worst = check_dw_identity_gpu(G.to(device), reps32, idx, H.to(device), m.to(device), dW)
+        say(f"  dW (every row, identity on the GPU): worst error {worst:.3f} of its bound")
     # Backward: dH in full, dW/dbias on the sampled rows (all rows for config 1).
     reps_c, idx_c = reps32.cpu(), idx.cpu()
     rH, _, rb = oracle.fused_bwd_ref(G, reps_c, idx_c, H, W, b is not None, m, with_dW=False)
@@ -777,6 +802,46 @@ def test_fp32_split_precision(case, device):
         assert not torch.equal(r32, exact[2])
 
 
+def test_fp32_split_infinite_entries(device):
+    """Infinite entries in H and in W under 'high' (the bf16 hi/lo split kernel): reps and
+    argmax equal the exact fp32 path's ('highest'), infinities and NaNs included, as long as
+    no product has both operands infinite. A pair holding a non-finite value keeps it in its
+    lo part (hi = 0), so only one of the three bf16 products sees the infinity."""
+    say("fp32 split mode with infinite entries in H and W")
+    g = torch.Generator().manual_seed(21)
+    B, S, D, V = 2, 32, 768, 3000
+    H = torch.randn(B, S, D, generator=g)
+    W = torch.randn(V, D, generator=g) * 0.02
+    b = torch.randn(V, generator=g) * 0.02
+    m = torch.ones(B, S, dtype=torch.long)
+    m[1, 20:] = 0
+    H[0, 5, 17] = float("inf")
+    H[1, 3, 400] = float("-inf")
+    W[7, 100] = float("-inf")
+    W[2999, 767] = float("inf")
+    Hd, Wd, bd, md = H.to(device), W.to(device), b.to(device), m.to(device)
+    prev = torch.get_float32_matmul_precision()
+    try:
+        torch.set_float32_matmul_precision("high")
+        split = [t.clone() for t in torch.ops.sparton.fused_sparton_fwd_train(Hd, Wd, bd, md)]
+        torch.set_float32_matmul_precision("highest")
+        exact = [t.clone() for t in torch.ops.sparton.fused_sparton_fwd_train(Hd, Wd, bd, md)]
+    finally:
+        torch.set_float32_matmul_precision(prev)
+    torch.cuda.synchronize()
+    r_s, r_e = split[2].cpu(), exact[2].cpu()
+    nonfinite = ~torch.isfinite(r_e)
+    say(f"  {int(nonfinite.sum())} non-finite reps in the exact path, "
+        f"{int(torch.isinf(r_e).sum())} infinite")
+    assert int(torch.isinf(r_e).sum()) > 100
+    assert torch.equal(nonfinite, ~torch.isfinite(r_s))
+    assert torch.equal(r_s[nonfinite].isnan(), r_e[nonfinite].isnan())
+    assert torch.equal(r_s[torch.isinf(r_e)], r_e[torch.isinf(r_e)])
+    assert torch.equal(split[1].cpu()[nonfinite], exact[1].cpu()[nonfinite])
+    fin = ~nonfinite
+    torch.testing.assert_close(r_s[fin].double(), r_e[fin].double(), **FWD_TOL)
+
+
 @pytest.mark.parametrize("dt", [1, 2])
 def test_mfma_probe_reports_cycles(dt, device):
     """sparton_mfma_probe (the measurement kernel bench.py reports as mfma_ceiling) runs on
@@ -916,6 +981,34 @@ def test_autocast_weight_cast_is_cached_until_updated(device):
         with torch.autocast("cuda", dtype=torch.bfloat16):
             r4 = head(H, m)
     assert torch.equal(r4, r3.detach())
+
+    def ref_now():
+        return oracle.torch_head(H.detach().cpu().bfloat16().double(),
+                                 head.weight.detach().cpu().bfloat16().double(),
+                                 head.bias.detach().cpu().bfloat16().double(), m.cpu())
+
+    # A write through .data is not versioned by torch; the backward dropped the copies, so
+    # the next forward sees it (optimizers that update p.data after backward).
+    r3.float().sum().backward()
+    head.weight.data.mul_(-1.0)
+    head.bias.data.add_(0.05)
+    r5 = run()
+    torch.testing.assert_close(r5.detach().cpu().double(), ref_now(), **FWD_TOL)
+    assert not torch.equal(r5, r3)
+    # A new parameter object (here likely at the freed address of the old one, version 0)
+    # is a new key.
+    r5.float().sum().backward()
+    with torch.no_grad():
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            head(H, m)   # caches a copy of the current weight for inference
+    new_w = head.weight.detach().clone() * 2.0
+    head.weight = None
+    head.weight = torch.nn.Parameter(new_w)
+    del new_w
+    with torch.no_grad():
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            r6 = head(H, m)
+    torch.testing.assert_close(r6.cpu().double(), ref_now(), **FWD_TOL)
 
 
 @pytest.mark.parametrize("use_bias", [True, False])
