@@ -468,8 +468,6 @@ def loss_timing(torch, w, dev, reps_n):
     from sparton_amd import _lib
     from sparton_amd import loss as sl
     B, V, dt = w.B, w.V, w.dtype
-    if B > sl.MAX_ROWS:
-        return None
     gen = torch.Generator(device=dev).manual_seed(11)
 
     def reps():

@@ -220,8 +220,11 @@ int sparton_transform_chunk_sum(const float* part, void* out, int64_t C, int64_t
  *   L1(x) = mean_b sum_v |x[b,v]|               l1_regularization (:80-82)
  *   FL(x) = mean_v (sum_b x[b,v])^2             flops_regularization (:85-87)
  *   total = w_ce CE + w_l1 (L1(q) + L1(d)) + w_flops (FL(q) + FL(d))   (:196-197)
- * Limits: 1 <= Bq <= 128, 0 <= Bd <= 128, Bq <= Bd when Bd > 0 (the labels index d's
- * rows), temperature > 0 and finite when Bd > 0. Computed in fp32 whatever the reps dtype.
+ * Limits: Bq >= 1, Bd >= 0, Bq <= Bd when Bd > 0 (the labels index d's rows), temperature
+ * > 0 and finite when Bd > 0; sizes whose scores or offsets pass the kernels' int range return
+ * SPARTON_EUNSUPPORTED. Up to 128 rows per side run slice-staged kernels, larger batches
+ * GEMM kernels on the fp32 matrix cores (the workspace size follows). Computed in fp32
+ * whatever the reps dtype.
  */
 size_t sparton_loss_workspace_bytes(int64_t Bq, int64_t Bd, int64_t V);
 

@@ -369,6 +369,414 @@ static void bwd_all(const void* q, const void* d, const float* P, const Grads6& 
   else launch_bwd<T, 128>(q, d, P, g, Bq, Bd, V, w_ce, w_l1, w_fl, gq, gd, st);
 }
 
+// ---- batches past MAX_B rows ---------------------------------------------------------------
+//
+// The kernels above stage every row of a 64-column slice and keep per-slice partials of all
+// Bq x Bd scores, so they stop at MAX_B rows. Larger batches take GEMM-shaped kernels on the
+// fp32 matrix cores (v_mfma_f32_32x32x2f32: the products of any reps dtype are exact in fp32,
+// and the sums accumulate in fp32, as above):
+//   forward   loss_stats_kernel   per 64-column slice: each row's sum of |x| over the slice,
+//                                 and sum_v (sum_b x)^2 of Q and of R;
+//             loss_score_kernel   S = Q R^T in 128 x 128 tiles, the vocabulary split into
+//                                 chunks (one partial S per chunk);
+//             loss_slice_sum_kernel (above) sums both sets of partials in a fixed order;
+//             loss_rows_kernel    one wave per query row: softmax, the row's CE term, P;
+//             loss_final_large_kernel the six scalars.
+//   backward  loss_bwd_large_kernel, one workgroup per 64 vocabulary columns: the columns'
+//             sums over Q and R, then dQ = c P R + ... tile by tile over 128 query rows and
+//             dR = c P^T Q + ... over 128 document rows, K (the other side's rows) streamed
+//             through LDS in stages of 32. No workspace.
+// Operand tiles sit in LDS as fp32 [k][m]; an MFMA takes A[m][k] from lane m + 32 k and B[k][n]
+// from lane n + 32 k, so both reads are consecutive floats. The row strides 161 and 97 are
+// 33 mod 64 banks, so the transposing stores and the two lane halves' reads barely conflict.
+namespace big {
+constexpr int TM = 128;   // score tile rows and columns; gradient rows per tile
+constexpr int KS = 32;    // K per LDS stage
+constexpr int LDA = 161;  // floats per k row of a [KS][128] tile
+constexpr int NC = 64;    // backward: vocabulary columns per workgroup
+constexpr int LDB = 97;   // floats per k row of a [KS][64] tile
+constexpr int ST_ROWS = 4;  // stats: rows whose loads are in flight together per wave
+
+__device__ __forceinline__ f32x16 zero16() {
+  f32x16 z;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) z[i] = 0.0f;
+  return z;
+}
+
+// K-contiguous source X[m][k] (row stride ld): rows [m0, m0 + 128), k in [k0, k0 + KS); zero past
+// M rows or past kend. Thread t holds k = t % 32 of rows t / 32 + 8 u.
+template <typename T>
+__device__ __forceinline__ void load_kc(const T* __restrict__ X, int64_t ld, int m0, int M, int k0,
+                                        int kend, T (&v)[16]) {
+  const int t = threadIdx.x, k = k0 + (t & 31), rb = t >> 5;
+#pragma unroll
+  for (int u = 0; u < 16; ++u) {
+    const int m = m0 + rb + 8 * u;
+    v[u] = (m < M && k < kend) ? X[(int64_t)m * ld + k] : T(0.0f);
+  }
+}
+template <typename T>
+__device__ __forceinline__ void store_kc(float* s, const T (&v)[16]) {
+  const int t = threadIdx.x, kk = t & 31, rb = t >> 5;
+#pragma unroll
+  for (int u = 0; u < 16; ++u) s[kk * LDA + rb + 8 * u] = to_f32(v[u]);
+}
+
+// N-contiguous source X[k][n] (row stride ld): k in [k0, k0 + KS) below kend, n in [n0, n0 + NN)
+// below nend, into s[k][n] (row stride LD). Thread t holds n = t % NN of k rows t / NN + (NT/NN) u.
+template <typename T, int NN>
+__device__ __forceinline__ void load_nc(const T* __restrict__ X, int64_t ld, int k0, int kend, int n0,
+                                        int nend, T (&v)[KS * NN / NT]) {
+  constexpr int KSTEP = NT / NN;
+  const int t = threadIdx.x, n = n0 + t % NN, kb = t / NN;
+#pragma unroll
+  for (int u = 0; u < KS / KSTEP; ++u) {
+    const int k = k0 + kb + KSTEP * u;
+    v[u] = (k < kend && n < nend) ? X[(int64_t)k * ld + n] : T(0.0f);
+  }
+}
+template <typename T, int NN, int LD>
+__device__ __forceinline__ void store_nc(float* s, const T (&v)[KS * NN / NT]) {
+  constexpr int KSTEP = NT / NN;
+  const int t = threadIdx.x, n = t % NN, kb = t / NN;
+#pragma unroll
+  for (int u = 0; u < KS / KSTEP; ++u) s[(kb + KSTEP * u) * LD + n] = to_f32(v[u]);
+}
+
+// acc[bi][bj] += A[am0 + 32 bi .., :] B[:, bn0 + 32 bj ..] over one stage (KS values of k).
+template <int BI, int BJ, int LDa, int LDb>
+__device__ __forceinline__ void mma_stage(const float* sA, int am0, const float* sB, int bn0,
+                                          f32x16 (&acc)[BI][BJ]) {
+  const int lane = threadIdx.x & 63, l32 = lane & 31, h = lane >> 5;
+#pragma unroll 4
+  for (int ks = 0; ks < KS / 2; ++ks) {
+    const int k = 2 * ks + h;
+    float a[BI], b[BJ];
+#pragma unroll
+    for (int i = 0; i < BI; ++i) a[i] = sA[k * LDa + am0 + 32 * i + l32];
+#pragma unroll
+    for (int j = 0; j < BJ; ++j) b[j] = sB[k * LDb + bn0 + 32 * j + l32];
+#pragma unroll
+    for (int i = 0; i < BI; ++i)
+#pragma unroll
+      for (int j = 0; j < BJ; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i], b[j], acc[i][j], 0, 0, 0);
+  }
+}
+
+// Row of accumulator register r of a 32 x 32 block held by lane half h (the lane holds column
+// lane % 32).
+__device__ __forceinline__ int acc_row(int r, int h) { return 8 * (r >> 2) + 4 * h + (r & 3); }
+
+// Partial S = Q R^T over the vocabulary chunk blockIdx.y (columns [chunk y, chunk (y+1))) for
+// the 128 x 128 tile blockIdx.x, at part + y Bq Bd. Four waves of 64 x 64 (2 x 2 blocks).
+template <typename T>
+__global__ __launch_bounds__(NT) void loss_score_kernel(const T* __restrict__ Q, const T* __restrict__ R,
+                                                        int Bq, int Bd, int V, int chunk,
+                                                        float* __restrict__ part) {
+  __shared__ float sA[KS * LDA];
+  __shared__ float sB[KS * LDA];
+  const int tj = (Bd + TM - 1) / TM;
+  const int i0 = (blockIdx.x / tj) * TM, j0 = (blockIdx.x % tj) * TM;
+  const int kc0 = blockIdx.y * chunk, kc1 = min(V, kc0 + chunk);
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, wm = wave >> 1, wn = wave & 1;
+  f32x16 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = zero16();
+  T ra[16], rb[16];
+  load_kc(Q, V, i0, Bq, kc0, kc1, ra);
+  load_kc(R, V, j0, Bd, kc0, kc1, rb);
+  for (int k0 = kc0; k0 < kc1; k0 += KS) {
+    __syncthreads();  // the previous stage is read
+    store_kc(sA, ra);
+    store_kc(sB, rb);
+    __syncthreads();
+    if (k0 + KS < kc1) {  // the next stage's loads run under this stage's MFMAs
+      load_kc(Q, V, i0, Bq, k0 + KS, kc1, ra);
+      load_kc(R, V, j0, Bd, k0 + KS, kc1, rb);
+    }
+    mma_stage<2, 2, LDA, LDA>(sA, wm * 64, sB, wn * 64, acc);
+  }
+  float* out = part + (size_t)blockIdx.y * Bq * Bd;
+  const int l32 = lane & 31, h = lane >> 5;
+#pragma unroll
+  for (int bi = 0; bi < 2; ++bi)
+#pragma unroll
+    for (int bj = 0; bj < 2; ++bj) {
+      const int j = j0 + wn * 64 + 32 * bj + l32;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int i = i0 + wm * 64 + 32 * bi + acc_row(r, h);
+        if (i < Bq && j < Bd) out[(size_t)i * Bd + j] = acc[bi][bj][r];
+      }
+    }
+}
+
+// Per 64-column slice (blockIdx.x), at part + slice K: entries [0, Bq) and [Bq, Bq + Bd) the
+// rows' sums of |x| over the slice, Bq + Bd and Bq + Bd + 1 the slice's sum_v (sum_b x)^2 of Q
+// and of R. Wave w takes rows w, w + 4, ...; column sums are added over the waves in order.
+template <typename T>
+__global__ __launch_bounds__(NT) void loss_stats_kernel(const T* __restrict__ Q, const T* __restrict__ R,
+                                                        int Bq, int Bd, int V, float* __restrict__ part,
+                                                        int K) {
+  __shared__ float cpart[4][64];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int c = blockIdx.x * 64 + lane;
+  const bool cv = c < V;
+  float* out = part + (size_t)blockIdx.x * K;
+  for (int side = 0; side < 2; ++side) {
+    const T* X = side ? R : Q;
+    const int rows = side ? Bd : Bq, o = side ? Bq : 0;
+    float cs = 0.0f;
+    for (int b0 = wave; b0 < rows; b0 += 4 * ST_ROWS) {  // uniform per wave
+      T v[ST_ROWS];
+#pragma unroll
+      for (int u = 0; u < ST_ROWS; ++u) {
+        const int b = b0 + 4 * u;
+        v[u] = (b < rows && cv) ? X[(int64_t)b * V + c] : T(0.0f);
+      }
+#pragma unroll
+      for (int u = 0; u < ST_ROWS; ++u) {
+        const int b = b0 + 4 * u;
+        if (b < rows) {
+          const float x = to_f32(v[u]);
+          cs += x;
+          const float a = wave_sum(fabsf(x));
+          if (lane == 0) out[o + b] = a;
+        }
+      }
+    }
+    cpart[wave][lane] = cs;
+    __syncthreads();
+    if (wave == 0) {
+      const float tot = ((cpart[0][lane] + cpart[1][lane]) + cpart[2][lane]) + cpart[3][lane];
+      const float sq = wave_sum(tot * tot);
+      if (lane == 0) out[Bq + Bd + side] = sq;
+    }
+    __syncthreads();
+  }
+}
+
+// One wave per query row i: x = S[i, :] / T, the row's CE term logsumexp(x) - x[i] and
+// P[i, j] = (softmax(x)_j - [i == j]) / (Bq T).
+__global__ __launch_bounds__(NT) void loss_rows_kernel(const float* __restrict__ S, int Bq, int Bd,
+                                                       float inv_t, float* __restrict__ row_loss,
+                                                       float* __restrict__ probs) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int i = blockIdx.x * 4 + wave;
+  if (i >= Bq) return;
+  const float* srow = S + (size_t)i * Bd;
+  float m = -INFINITY;
+  for (int j = lane; j < Bd; j += 64) m = fmaxf(m, srow[j] * inv_t);
+  m = wave_max(m);
+  float s = 0.0f;
+  for (int j = lane; j < Bd; j += 64) s += expf(srow[j] * inv_t - m);
+  s = wave_sum(s);
+  if (lane == 0) row_loss[i] = m + logf(s) - srow[i] * inv_t;
+  const float rs = 1.0f / s, pscale = inv_t / (float)Bq;
+  for (int j = lane; j < Bd; j += 64)
+    probs[(size_t)i * Bd + j] = (expf(srow[j] * inv_t - m) * rs - (j == i ? 1.0f : 0.0f)) * pscale;
+}
+
+// One wave: the six scalars from the row CE terms and the summed statistics.
+__global__ __launch_bounds__(64) void loss_final_large_kernel(const float* __restrict__ row_loss,
+                                                              const float* __restrict__ stats, int Bq,
+                                                              int Bd, int V, float w_ce, float w_l1,
+                                                              float w_fl, float* __restrict__ out) {
+  const int lane = threadIdx.x;
+  float ce = 0.0f, l1q = 0.0f, l1d = 0.0f;
+  if (Bd > 0)
+    for (int i = lane; i < Bq; i += 64) ce += row_loss[i];
+  for (int i = lane; i < Bq; i += 64) l1q += stats[i];
+  for (int j = lane; j < Bd; j += 64) l1d += stats[Bq + j];
+  ce = wave_sum(ce);
+  l1q = wave_sum(l1q);
+  l1d = wave_sum(l1d);
+  if (lane == 0) {
+    ce = Bd > 0 ? ce / (float)Bq : 0.0f;
+    l1q /= (float)Bq;
+    l1d = Bd > 0 ? l1d / (float)Bd : 0.0f;
+    const float flq = stats[Bq + Bd] / (float)V, fld = stats[Bq + Bd + 1] / (float)V;
+    out[0] = w_ce * ce + w_l1 * (l1q + l1d) + w_fl * (flq + fld);
+    out[1] = ce;
+    out[2] = l1q;
+    out[3] = l1d;
+    out[4] = flq;
+    out[5] = fld;
+  }
+}
+
+// 128 rows of one gradient over the workgroup's 64 columns: acc = sum_k A[m][k] B[k][n] with A
+// from a K-contiguous (P rows, dQ) or N-contiguous (P columns, dR) source; wave w owns rows
+// 32 w .. 32 w + 31 (two 32 x 32 blocks). Then G = c_ce acc + c_s sign(X) + c_f colsum, in T.
+template <typename T, bool A_KC>
+__device__ __forceinline__ void grad_tile(float* sA, float* sB, const float* __restrict__ P,
+                                          int Bq, int Bd, const T* __restrict__ Bsrc, int K,
+                                          const T* __restrict__ X, int rows, int m0, int c0, int V,
+                                          float c_ce, float c_s, float c_f, const float* colsum,
+                                          T* __restrict__ G) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, l32 = lane & 31, h = lane >> 5;
+  f32x16 acc[1][2] = {{zero16(), zero16()}};
+  if (K > 0) {
+    float pa[16];
+    T rbv[KS * NC / NT];
+    auto load_a = [&](int k0) {
+      if (A_KC) {  // A[m][k] = P[m0 + m][k]: rows of P (dQ)
+        load_kc(P, Bd, m0, Bq, k0, K, pa);
+      } else {     // A[m][k] = P[k][m0 + m]: columns of P (dR)
+        load_nc<float, TM>(P, Bd, k0, K, m0, Bd, pa);
+      }
+    };
+    load_a(0);
+    load_nc<T, NC>(Bsrc, V, 0, K, c0, V, rbv);
+    for (int k0 = 0; k0 < K; k0 += KS) {
+      __syncthreads();
+      if (A_KC) store_kc(sA, pa);
+      else store_nc<float, TM, LDA>(sA, pa);
+      store_nc<T, NC, LDB>(sB, rbv);
+      __syncthreads();
+      if (k0 + KS < K) {
+        load_a(k0 + KS);
+        load_nc<T, NC>(Bsrc, V, k0 + KS, K, c0, V, rbv);
+      }
+      mma_stage<1, 2, LDA, LDB>(sA, wave * 32, sB, 0, acc);
+    }
+  }
+#pragma unroll
+  for (int bj = 0; bj < 2; ++bj) {
+    const int cl = 32 * bj + l32, c = c0 + cl;
+    T xv[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int i = m0 + wave * 32 + acc_row(r, h);
+      xv[r] = (i < rows && c < V) ? X[(int64_t)i * V + c] : T(0.0f);
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int i = m0 + wave * 32 + acc_row(r, h);
+      if (i < rows && c < V) {
+        const float x = to_f32(xv[r]);
+        const float sg = x > 0.0f ? 1.0f : (x < 0.0f ? -1.0f : 0.0f);
+        G[(int64_t)i * V + c] = from_f32<T>(c_ce * acc[0][bj][r] + c_s * sg + c_f * colsum[cl]);
+      }
+    }
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(NT) void loss_bwd_large_kernel(const T* __restrict__ Q, const T* __restrict__ R,
+                                                            const float* __restrict__ P, const Grads6 g,
+                                                            int Bq, int Bd, int V, float w_ce, float w_l1,
+                                                            float w_fl, T* __restrict__ GQ,
+                                                            T* __restrict__ GR) {
+  __shared__ float sA[KS * LDA];
+  __shared__ float sB[KS * LDB];
+  __shared__ float cpart[2][4][NC];
+  __shared__ float colsum[2][NC];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int c0 = blockIdx.x * NC;
+  // the columns' sums over Q's and R's rows: wave w sums rows w, w + 4, ... in order
+  {
+    const int c = c0 + lane;
+    const bool cv = c < V;
+    for (int side = 0; side < 2; ++side) {
+      const T* X = side ? R : Q;
+      const int rows = side ? Bd : Bq;
+      float cs = 0.0f;
+      for (int b0 = wave; b0 < rows; b0 += 4 * ST_ROWS) {
+        T v[ST_ROWS];
+#pragma unroll
+        for (int u = 0; u < ST_ROWS; ++u) {
+          const int b = b0 + 4 * u;
+          v[u] = (b < rows && cv) ? X[(int64_t)b * V + c] : T(0.0f);
+        }
+#pragma unroll
+        for (int u = 0; u < ST_ROWS; ++u) cs += to_f32(v[u]);
+      }
+      cpart[side][wave][lane] = cs;
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x < 2 * NC) {
+    const int side = threadIdx.x / NC, l = threadIdx.x % NC;
+    colsum[side][l] = ((cpart[side][0][l] + cpart[side][1][l]) + cpart[side][2][l]) + cpart[side][3][l];
+  }
+  __syncthreads();
+  const float g0 = grad_of(g, 0);
+  const float c_ce = g0 * w_ce + grad_of(g, 1);
+  const float c_sq = (g0 * w_l1 + grad_of(g, 2)) / (float)Bq;
+  const float c_sd = Bd > 0 ? (g0 * w_l1 + grad_of(g, 3)) / (float)Bd : 0.0f;
+  const float c_fq = 2.0f * (g0 * w_fl + grad_of(g, 4)) / (float)V;
+  const float c_fd = 2.0f * (g0 * w_fl + grad_of(g, 5)) / (float)V;
+  for (int i0 = 0; i0 < Bq; i0 += TM)  // dQ = c_ce P R + ...
+    grad_tile<T, true>(sA, sB, P, Bq, Bd, R, Bd, Q, Bq, i0, c0, V, c_ce, c_sq, c_fq, colsum[0], GQ);
+  for (int j0 = 0; j0 < Bd; j0 += TM)  // dR = c_ce P^T Q + ...
+    grad_tile<T, false>(sA, sB, P, Bq, Bd, Q, Bq, R, Bd, j0, c0, V, c_ce, c_sd, c_fd, colsum[1], GR);
+}
+
+// Score chunking: about 512 workgroups, chunks of whole LDS stages.
+struct ScorePlan {
+  int tiles, chunk, nchunk;
+};
+static ScorePlan score_plan(int64_t Bq, int64_t Bd, int64_t V) {
+  ScorePlan p;
+  p.tiles = (int)(cdiv(Bq, TM) * cdiv(Bd, TM));
+  const int64_t want = cdiv(512, p.tiles);
+  const int64_t nc = want < 1 ? 1 : (want > cdiv(V, 256) ? cdiv(V, 256) : want);
+  p.chunk = (int)round_up(cdiv(V, nc), KS);
+  p.nchunk = (int)cdiv(V, p.chunk);
+  return p;
+}
+static int64_t stats_entries(int64_t Bq, int64_t Bd) { return Bq + Bd + 2; }
+// Workspace (floats): partial S per chunk, S, partial stats per slice, stats, row CE terms.
+static int64_t workspace_floats(int64_t Bq, int64_t Bd, int64_t V) {
+  const int64_t s = Bd > 0 ? (int64_t)score_plan(Bq, Bd, V).nchunk * Bq * Bd + Bq * Bd : 0;
+  return s + (slices(V) + 1) * stats_entries(Bq, Bd) + Bq;
+}
+
+template <typename T>
+static void fwd(const void* q, const void* d, int Bq, int Bd, int V, float inv_t, float w_ce,
+                float w_l1, float w_fl, float* out, float* probs, float* ws, hipStream_t st) {
+  float* spart = ws;
+  float* S = nullptr;
+  if (Bd > 0) {
+    const ScorePlan p = score_plan(Bq, Bd, V);
+    S = spart + (size_t)p.nchunk * Bq * Bd;
+    hipLaunchKernelGGL((loss_score_kernel<T>), dim3((unsigned)p.tiles, (unsigned)p.nchunk), dim3(NT), 0,
+                       st, (const T*)q, (const T*)d, Bq, Bd, V, p.chunk, spart);
+    const int K = Bq * Bd;
+    hipLaunchKernelGGL(loss_slice_sum_kernel, dim3((unsigned)cdiv(K, 64)), dim3(64 * SUM_WAVES), 0, st,
+                       (const float*)spart, p.nchunk, K, S);
+  }
+  float* tpart = Bd > 0 ? S + (size_t)Bq * Bd : ws;
+  const int KS2 = (int)stats_entries(Bq, Bd), ns = (int)slices(V);
+  float* stats = tpart + (size_t)ns * KS2;
+  float* row_loss = stats + KS2;
+  hipLaunchKernelGGL((loss_stats_kernel<T>), dim3((unsigned)ns), dim3(NT), 0, st, (const T*)q,
+                     (const T*)d, Bq, Bd, V, tpart, KS2);
+  hipLaunchKernelGGL(loss_slice_sum_kernel, dim3((unsigned)cdiv(KS2, 64)), dim3(64 * SUM_WAVES), 0, st,
+                     (const float*)tpart, ns, KS2, stats);
+  if (Bd > 0)
+    hipLaunchKernelGGL(loss_rows_kernel, dim3((unsigned)cdiv(Bq, 4)), dim3(NT), 0, st, (const float*)S,
+                       Bq, Bd, inv_t, row_loss, probs);
+  hipLaunchKernelGGL(loss_final_large_kernel, dim3(1), dim3(64), 0, st, (const float*)row_loss,
+                     (const float*)stats, Bq, Bd, V, w_ce, w_l1, w_fl, out);
+}
+
+template <typename T>
+static void bwd(const void* q, const void* d, const float* P, const Grads6& g, int Bq, int Bd, int V,
+                float w_ce, float w_l1, float w_fl, void* gq, void* gd, hipStream_t st) {
+  hipLaunchKernelGGL((loss_bwd_large_kernel<T>), dim3((unsigned)cdiv(V, NC)), dim3(NT), 0, st,
+                     (const T*)q, (const T*)d, P, g, Bq, Bd, V, w_ce, w_l1, w_fl, (T*)gq, (T*)gd);
+}
+}  // namespace big
+
+// Batches with more than MAX_B rows on either side take the kernels in `big`.
+static bool is_big(int64_t Bq, int64_t Bd) { return Bq > MAX_B || Bd > MAX_B; }
+
 }  // namespace loss
 }  // namespace sparton
 
@@ -377,7 +785,11 @@ using namespace sparton;
 static int loss_check(int64_t Bq, int64_t Bd, int64_t V, int dtype) {
   if (dtype < SPARTON_F32 || dtype > SPARTON_F16) return SPARTON_EINVAL;
   if (Bq < 1 || Bd < 0 || V < 1) return SPARTON_EINVAL;
-  if (Bq > loss::MAX_B || Bd > loss::MAX_B || V > INT32_MAX) return SPARTON_EUNSUPPORTED;
+  // int offsets: the scores and their per-chunk partials, and row * V + column
+  if (V > INT32_MAX || Bq > INT32_MAX / 8 || Bd > INT32_MAX / 8 ||
+      (Bd > 0 && Bq * Bd * (int64_t)loss::big::score_plan(Bq, Bd, V).nchunk > INT32_MAX) ||
+      (Bq + Bd) * V > ((int64_t)1 << 62))
+    return SPARTON_EUNSUPPORTED;
   if (Bd > 0 && Bq > Bd) return SPARTON_EINVAL;  // labels arange(Bq) index R's rows
   return SPARTON_OK;
 }
@@ -386,6 +798,7 @@ extern "C" __attribute__((visibility("default"))) size_t sparton_loss_workspace_
                                                                                       int64_t Bd,
                                                                                       int64_t V) {
   if (Bq < 1 || Bd < 0 || V < 1) return 0;
+  if (loss::is_big(Bq, Bd)) return (size_t)loss::big::workspace_floats(Bq, Bd, V) * sizeof(float);
   return (size_t)((loss::slices(V) + 1) * loss::entries(Bq, Bd)) * sizeof(float);
 }
 
@@ -402,6 +815,23 @@ extern "C" __attribute__((visibility("default"))) int sparton_loss_fwd(
     return SPARTON_EWORKSPACE;
   if ((uintptr_t)workspace % 16 != 0) return SPARTON_EALIGN;
   hipStream_t st = (hipStream_t)stream;
+  if (loss::is_big(Bq, Bd)) {
+    const float inv_t = Bd > 0 ? 1.0f / temperature : 0.0f;
+    float* ws = (float*)workspace;
+    switch (dtype) {
+      case SPARTON_BF16:
+        loss::big::fwd<bf16>(q, d, (int)Bq, (int)Bd, (int)V, inv_t, w_ce, w_l1, w_flops, out, probs, ws, st);
+        break;
+      case SPARTON_F16:
+        loss::big::fwd<f16>(q, d, (int)Bq, (int)Bd, (int)V, inv_t, w_ce, w_l1, w_flops, out, probs, ws, st);
+        break;
+      default:
+        loss::big::fwd<float>(q, d, (int)Bq, (int)Bd, (int)V, inv_t, w_ce, w_l1, w_flops, out, probs, ws, st);
+        break;
+    }
+    const hipError_t e = hipGetLastError();
+    return e == hipSuccess ? SPARTON_OK : (int)e;
+  }
   const int K = (int)loss::entries(Bq, Bd), ns = (int)loss::slices(V);
   float* part = (float*)workspace;
   float* sums = part + (size_t)ns * K;
@@ -428,6 +858,24 @@ static int loss_bwd_run(const void* q, const void* d, const float* probs, const 
       (Bd > 0 && (d == nullptr || probs == nullptr || grad_d == nullptr)))
     return SPARTON_EINVAL;
   hipStream_t st = (hipStream_t)stream;
+  if (loss::is_big(Bq, Bd)) {
+    switch (dtype) {
+      case SPARTON_BF16:
+        loss::big::bwd<bf16>(q, d, probs, grad_out, (int)Bq, (int)Bd, (int)V, w_ce, w_l1, w_flops, grad_q,
+                             grad_d, st);
+        break;
+      case SPARTON_F16:
+        loss::big::bwd<f16>(q, d, probs, grad_out, (int)Bq, (int)Bd, (int)V, w_ce, w_l1, w_flops, grad_q,
+                            grad_d, st);
+        break;
+      default:
+        loss::big::bwd<float>(q, d, probs, grad_out, (int)Bq, (int)Bd, (int)V, w_ce, w_l1, w_flops, grad_q,
+                              grad_d, st);
+        break;
+    }
+    const hipError_t e = hipGetLastError();
+    return e == hipSuccess ? SPARTON_OK : (int)e;
+  }
   switch (dtype) {
     case SPARTON_BF16:
       loss::bwd_all<bf16>(q, d, probs, grad_out, (int)Bq, (int)Bd, (int)V, w_ce, w_l1, w_flops, grad_q,

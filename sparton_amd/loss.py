@@ -17,7 +17,12 @@ runs in the reps dtype), deterministically. Device tensors only, like the head.
         -> (out[6] fp32 = (total, CE, L1 q, L1 d, FLOPS q, FLOPS d), probs [Bq, Bd] fp32)
     sparton::splade_loss_bwd(grad_out[6], q, d?, probs, w_ce, w_l1, w_flops) -> (dq, dd)
 
-Limits: 1 <= Bq <= 128, Bd <= 128, Bq <= Bd (the labels arange(Bq) index d's rows).
+Batches of up to 128 rows on each side take the slice-staged kernels above. Larger batches
+take GEMM-shaped HIP kernels on the fp32 matrix cores: a split-vocabulary score GEMM with a
+fixed-order sum of its partials, per-slice row and column statistics, a row softmax, and a
+backward that recomputes each vocabulary slice's column sums and forms both gradients tile by
+tile (sparton_loss.hip). Limits: 1 <= Bq <= Bd when documents are given (the labels
+arange(Bq) index d's rows); the C ABI reports sizes past its int offsets as unsupported.
 """
 from __future__ import annotations
 
@@ -28,7 +33,7 @@ from torch import Tensor
 
 from . import _eager, _lib
 
-MAX_ROWS = 128
+SMALL_MAX_ROWS = 128   # rows per side taken by the slice-staged kernels; larger batches take the GEMM kernels
 _FLOAT_DTYPES = tuple(_lib.DTYPE_CODE)
 
 
@@ -43,7 +48,7 @@ class SpladeLossOutput(NamedTuple):
     flops_d: Tensor
 
 
-def _check(q: Tensor, d: Optional[Tensor], op: str, max_rows: Optional[int] = MAX_ROWS) -> Tuple[int, int, int]:
+def _check(q: Tensor, d: Optional[Tensor], op: str) -> Tuple[int, int, int]:
     if not q.is_cuda:
         raise RuntimeError(f"{op} only supports ROCm/HIP device tensors (got device {q.device})")
     if q.dim() != 2 or q.dtype not in _FLOAT_DTYPES:
@@ -60,9 +65,6 @@ def _check(q: Tensor, d: Optional[Tensor], op: str, max_rows: Optional[int] = MA
                              "index the documents, so Bq <= Bd")
     if Bq < 1 or V < 1:
         raise ValueError(f"{op}: needs at least one query row and V >= 1, got Bq={Bq} V={V}")
-    if max_rows is not None and (Bq > max_rows or Bd > max_rows):
-        raise ValueError(f"{op}: the fused kernels take 1..{max_rows} rows of each reps tensor, got "
-                         f"Bq={Bq} Bd={Bd} (splade_loss and the term functions take larger batches)")
     return Bq, Bd, V
 
 
@@ -155,37 +157,9 @@ def _backward(ctx, g_out, _g_probs):
 splade_loss_fwd.register_autograd(_backward, setup_context=_setup_context)
 
 
-def _large_batch_terms(q: Tensor, d: Optional[Tensor], temperature: float, w_ce: float,
-                       w_l1: float, w_flops: float) -> Tuple[Tensor, ...]:
-    """Batches past the fused kernels' MAX_ROWS rows: the same six terms from torch's GPU
-    operations in fp32, following train.py's formulas (:73-87) term by term. S = q d^T is
-    then a GEMM (its [Bq, Bd] partials no longer fit the kernels' per-slice staging), and
-    autograd gives the gradients, in the reps dtype."""
-    qf = q.float()
-    l1q = qf.abs().sum(-1).mean()
-    flq = (qf.sum(0) ** 2).mean()
-    zero = qf.new_zeros(())
-    if d is not None:
-        df = d.float()
-        s = qf @ df.t() / temperature
-        ce = torch.nn.functional.cross_entropy(s, torch.arange(q.shape[0], device=q.device))
-        l1d = df.abs().sum(-1).mean()
-        fld = (df.sum(0) ** 2).mean()
-    else:
-        ce, l1d, fld = zero, zero, zero
-    total = w_ce * ce + w_l1 * (l1q + l1d) + w_flops * (flq + fld)
-    return total, ce, l1q, l1d, flq, fld
-
-
 def _run(q: Tensor, d: Optional[Tensor], temperature: float, w_ce: float, w_l1: float,
          w_flops: float) -> Tuple[Tensor, ...]:
     """The six terms (total, CE, L1(q), L1(d), FL(q), FL(d)) as separate scalars."""
-    if q.is_cuda and (q.dim() == 2 and q.shape[0] > MAX_ROWS or
-                      d is not None and d.dim() == 2 and d.shape[0] > MAX_ROWS):
-        _check(q, d, "splade_loss", max_rows=None)
-        if d is not None and not temperature > 0.0:
-            raise ValueError(f"splade_loss: temperature must be > 0, got {temperature}")
-        return _large_batch_terms(q, d, temperature, w_ce, w_l1, w_flops)
     if torch.compiler.is_compiling() or not q.is_cuda:
         out, _ = torch.ops.sparton.splade_loss_fwd(q, d, temperature, w_ce, w_l1, w_flops)
         return out.unbind(0)

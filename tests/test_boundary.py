@@ -323,7 +323,7 @@ def loss_bwd(**kw):
     (dict(Bq=0), -1), (dict(V=0), -1), (dict(dtype=3), -1), (dict(Bq=9), -1),   # Bq > Bd
     (dict(q=None), -1), (dict(d=None), -1), (dict(probs=None), -1), (dict(out=None), -1),
     (dict(T=0.0), -1), (dict(T=float("inf")), -1), (dict(T=float("nan")), -1),
-    (dict(Bq=129, Bd=129), -3), (dict(Bd=200), -3),
+    (dict(Bq=1 << 28, Bd=1 << 28), -3), (dict(V=1 << 31), -3),
     (dict(ws=None), -4), (dict(ws_bytes=64), -4), (dict(ws=P + 4), -2),
 ])
 def test_loss_fwd_argument_validation(kw, code):
@@ -332,7 +332,8 @@ def test_loss_fwd_argument_validation(kw, code):
 
 @pytest.mark.parametrize("kw,code", [
     (dict(Bq=0), -1), (dict(g=None), -1), (dict(gq=None), -1), (dict(gd=None), -1),
-    (dict(probs=None), -1), (dict(Bq=9), -1), (dict(Bd=129), -3), (dict(dtype=-1), -1),
+    (dict(probs=None), -1), (dict(Bq=9), -1), (dict(Bd=1 << 28), -3), (dict(V=1 << 31), -3),
+    (dict(dtype=-1), -1),
 ])
 def test_loss_bwd_argument_validation(kw, code):
     assert loss_bwd(**kw) == code
@@ -349,7 +350,8 @@ def loss_bwd_terms(**kw):
 
 @pytest.mark.parametrize("kw,code", [
     (dict(terms=None), -1), (dict(Bq=0), -1), (dict(gq=None), -1), (dict(gd=None), -1),
-    (dict(probs=None), -1), (dict(Bq=9), -1), (dict(Bd=129), -3), (dict(dtype=-1), -1),
+    (dict(probs=None), -1), (dict(Bq=9), -1), (dict(Bd=1 << 28), -3), (dict(V=1 << 31), -3),
+    (dict(dtype=-1), -1),
 ])
 def test_loss_bwd_terms_argument_validation(kw, code):
     assert loss_bwd_terms(**kw) == code
@@ -362,6 +364,12 @@ def test_loss_workspace_size():
     assert L.sparton_loss_workspace_bytes(32, 32, 30522) == (477 + 1) * (1024 + 64 + 2) * 4
     assert L.sparton_loss_workspace_bytes(4, 0, 64) == 2 * (4 + 2) * 4
     assert L.sparton_loss_workspace_bytes(0, 4, 64) == 0
+    # past 128 rows: 16 score tiles of 128 x 128 -> 32 vocabulary chunks of 960 columns, one
+    # partial S each, S itself, per-slice row/column statistics plus their sums, and Bq row
+    # CE terms
+    assert L.sparton_loss_workspace_bytes(512, 512, 30522) == (
+        32 * 512 * 512 + 512 * 512 + (477 + 1) * (512 + 512 + 2) + 512) * 4
+    assert L.sparton_loss_workspace_bytes(300, 0, 1000) == ((16 + 1) * (300 + 2) + 300) * 4
 
 
 def test_loss_module_surface():

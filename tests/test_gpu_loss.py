@@ -81,12 +81,23 @@ def test_loss_matches_oracle(dt, Bq, Bd, V, T, w_l1, w_fl, device):
     say(f"  total {out[0].item():.6f} (oracle {want[0]:.6f})")
 
 
-@pytest.mark.parametrize("dt,Bq,Bd,V", [("fp32", 200, 200, 700), ("bf16", 150, 300, 2000),
-                                         ("fp16", 129, 0, 500)])
+LARGE_CASES = [  # dtype, Bq, Bd, V
+    ("fp32", 200, 200, 700),
+    ("bf16", 150, 300, 2000),
+    ("fp16", 129, 0, 500),        # query reps only
+    ("bf16", 512, 512, 30522),    # config 2's vocabulary, 16x its batch
+    ("fp32", 129, 1000, 4099),    # ragged tiles and chunks
+    ("fp16", 300, 300, 31),       # fewer columns than one slice
+    ("bf16", 1, 700, 3000),       # one query, many documents
+]
+
+
+@pytest.mark.parametrize("dt,Bq,Bd,V", LARGE_CASES, ids=[f"{c[0]}-{c[1]}x{c[2]}-V{c[3]}" for c in LARGE_CASES])
 def test_loss_large_batches_match_oracle(dt, Bq, Bd, V, device):
-    """More than 128 rows: splade_loss and the single-term functions take the batch through
-    torch's GPU operations in fp32 (train.py's formulas). Values and gradients against the
-    float64 oracle, weighting the six terms as the kernel test does."""
+    """More than 128 rows on a side: the GEMM kernels on the fp32 matrix cores (split-vocabulary
+    score GEMM, per-slice statistics, row softmax; a backward that forms both gradients tile
+    by tile). Values and gradients against the float64 oracle, weighting the six terms as the
+    kernel test does, through splade_loss (the eager C++ op) and the single-term functions."""
     say(f"loss large batch {dt} Bq={Bq} Bd={Bd} V={V}")
     T, w_l1, w_fl = 0.5, 1e-2, 1e-3
     q = reps_like(Bq, V, dt, seed=Bq + V)
@@ -108,6 +119,27 @@ def test_loss_large_batches_match_oracle(dt, Bq, Bd, V, device):
         close_rel(dd.grad, gd, GRAD_TOL[dt], "dd")
     np.testing.assert_allclose(sl.l1_regularization(qd).item(), want[2], rtol=1e-4)
     np.testing.assert_allclose(sl.flops_regularization(qd).item(), want[4], rtol=1e-4)
+    say(f"  total {res.total.item():.6f} (oracle {want[0]:.6f})")
+
+
+def test_loss_large_batch_deterministic_and_paths_agree(device):
+    """The large-batch kernels are bitwise reproducible, and the custom op (what torch.compile
+    traces) and the eager C++ op run the same kernels."""
+    q = reps_like(300, 5000, "bf16", seed=31).to(device)
+    d = reps_like(400, 5000, "bf16", seed=32).to(device)
+    runs = []
+    for _ in range(2):
+        qs, ds = q.clone().requires_grad_(), d.clone().requires_grad_()
+        res = sl.splade_loss(qs, ds, 0.7, 1e-3, 1e-3)
+        res.total.backward()
+        runs.append((torch.stack(list(res)).detach(), qs.grad, ds.grad))
+    for a, b in zip(*runs):
+        assert torch.equal(a, b)
+    qs, ds = q.clone().requires_grad_(), d.clone().requires_grad_()
+    out, _ = torch.ops.sparton.splade_loss_fwd(qs, ds, 0.7, 1.0, 1e-3, 1e-3)
+    out[0].backward()
+    assert torch.equal(out.detach(), runs[0][0])
+    assert torch.equal(qs.grad, runs[0][1]) and torch.equal(ds.grad, runs[0][2])
 
 
 def test_loss_matches_torch_formulas_fp32(device):
