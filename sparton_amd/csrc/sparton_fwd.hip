@@ -873,8 +873,8 @@ __device__ void copy_path(Smem& sm, const Args<T>& a, const Outputs<T>& o, int w
   cu.n_valid = cur.n_valid;
   copy_start(sm, a, o, sm.um[0], cu, buf, prev, sm.um[1], ct, c, lane);
 
+  Unit next = unit_of(w, 1, G, n_units, n_mt, n_vt, a.n_grp);
   for (int r = 1;; ++r) {
-    const Unit next = unit_of(w, r, G, n_units, n_mt, n_vt, a.n_grp);
     const bool pre = next.u >= 0 && nk >= PREFETCH_MIN_NK;
     UnitMeta& um_next = sm.um[par ^ 1];
     const int buf_next = buf ^ (nk & 1);
@@ -935,7 +935,9 @@ __device__ void copy_path(Smem& sm, const Args<T>& a, const Outputs<T>& o, int w
       lds_barrier();  // B_k
     }
     if (pre) issue_slab(sm, a, nx, 1, buf_next ^ 1, c, lane);
-    lds_barrier();  // E: the compute waves' pv/pi are written
+    // the unit after next, worked out while the compute waves run their epilogue
+    const Unit next2 = next.u >= 0 ? unit_of(w, r + 1, G, n_units, n_mt, n_vt, a.n_grp) : next;
+    lds_barrier();  // E: the compute waves' keys are written
     if (next.u < 0) {
       write_unit<T>(sm, sm.um[par], cur.m, cur.v0, a.V, cur.n_valid, ct, o.reps, o.argmax,
                     o.reps_f32, o.part);
@@ -948,6 +950,7 @@ __device__ void copy_path(Smem& sm, const Args<T>& a, const Outputs<T>& o, int w
     }
     cur = next;
     cu = nx;
+    next = next2;
     par ^= 1;
     buf = buf_next;
   }
