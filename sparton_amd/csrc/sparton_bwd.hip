@@ -1357,6 +1357,319 @@ static bool dh_long_rows(int64_t V) {
 }
 // Register passes from which the many-rows dH launch also takes dW's workgroups.
 constexpr int DH_MERGE_NP = 6;
+// ---- few dH rows (B * S <= FEW_ROWS) ------------------------------------------------------
+//
+// With few dH rows every W row serves several of them (config 1: each of the 30522 ids is
+// active in both batch rows), so gathering W rows per dH row reads W once per batch row.
+// Here one launch does all of the backward: a workgroup owns a range of vocabulary ids and
+// a 256-column slice of D, and walks the range tile by tile (FEW_TILE ids), reading each W
+// row of its slice once.
+//   dH: wave w holds dH rows FEW_RPW w .. FEW_RPW w + FEW_RPW - 1 of the slice in registers
+//   (lane l: columns 4 l .. 4 l + 3), indexed statically. A row b S + s takes the tile's
+//   ids whose entry (b, id) is active with index s (one ballot), in ascending v, so its
+//   partial sum runs over the range in ascending v; bwd_few_sum_kernel adds the ranges'
+//   partials in range order. These sums are this path's own order (they agree with every
+//   other path to fp32 rounding, not bitwise).
+//   dW, dbias: wave w also owns the tile's ids 8 w .. 8 w + 7 and sums their active entries'
+//   H rows (the slice of all B S rows sits in LDS) in ascending b, exactly as the staged dW
+//   kernel does (same operations in the same order: the results are bitwise the same).
+//
+// The tile's W rows travel HBM -> registers -> LDS: they are loaded during the previous
+// tile and written to LDS at the start of this one, so the loads overlap a whole tile's
+// work. (Direct-to-LDS copies would not: the compiler cannot tell the copy's target from
+// the buffer being read and waits for every copy before each LDS read.)
+constexpr int FEW_ROWS = 64;                          // dH rows held per workgroup
+constexpr int FEW_TILE = 64;                          // vocabulary ids per tile (one per lane)
+constexpr int FEW_WAVES = 8;
+constexpr int FEW_THREADS = 64 * FEW_WAVES;
+constexpr int FEW_COLS = 256;                         // columns of D per slice (4 per lane)
+constexpr int FEW_RPW = FEW_ROWS / FEW_WAVES;         // dH rows per wave
+constexpr int FEW_IPW = FEW_TILE / FEW_WAVES;         // dW ids per wave
+constexpr int FEW_IDC = 4;                            // dW ids summed together
+constexpr int FEW_NJ = FEW_ROWS * FEW_TILE / FEW_THREADS;  // entry rounds: batch rows per wave
+constexpr int FEW_ES_LD = 68;   // bytes per id of the index table: 17 words, odd, so a wave's
+                                // 64 ids fall in 64 different banks
+constexpr uint8_t FEW_NONE = 0xff;  // index table: inactive entry (S <= FEW_ROWS < 255)
+
+// SPARTON_BWD_FEW=0 sends few-row batches down the count/scan/scatter path instead (tests
+// compare the two).
+static bool few_enabled() {
+  const char* e = getenv("SPARTON_BWD_FEW");
+  return e == nullptr || strcmp(e, "0") != 0;
+}
+
+struct FewPlan {
+  bool fits;       // the shape qualifies (the workspace is sized for it whatever the switch)
+  int slices, ranges, range_len;
+  size_t part_bytes;
+};
+static FewPlan few_plan(int64_t B, int64_t S, int64_t D, int64_t V) {
+  FewPlan p{};
+  p.fits = B * S > 0 && B * S <= FEW_ROWS && D > 0 && V > 0;
+  if (!p.fits) return p;
+  p.slices = (int)cdiv(D, FEW_COLS);
+  // about one workgroup per CU: each reads range_len W rows of its slice once
+  const int64_t want = std::max<int64_t>(1, 256 / p.slices);
+  p.range_len = (int)(cdiv(cdiv(V, FEW_TILE), want) * FEW_TILE);
+  p.ranges = (int)cdiv(V, p.range_len);
+  p.part_bytes = (size_t)p.ranges * (size_t)(B * S) * (size_t)D * 4;
+  return p;
+}
+
+// Workgroup barrier once this wave's LDS operations are complete. Global loads in flight
+// (the next tile's, into registers) are not waited for; the memory clobber keeps the
+// compiler from moving memory accesses across it.
+__device__ __forceinline__ void few_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+// Rows of a matrix with row stride D, slice columns c0 .. c0 + FEW_COLS - 1, in 16-byte
+// chunks: chunk q = i * FEW_THREADS + thread is row q / CPR, chunk q % CPR of the row, so
+// consecutive threads read consecutive bytes. Chunks past D re-read the slice's first chunk
+// (those columns are never stored); D * sizeof(T) is a multiple of 16.
+template <typename T>
+struct FewChunks {
+  static constexpr int CPR = FEW_COLS * (int)sizeof(T) / 16;  // chunks per row
+  static constexpr int PER = 16 / (int)sizeof(T);             // elements per chunk
+  static __device__ __forceinline__ u32x4 load(const T* __restrict__ M, int row, int q, int D,
+                                               int c0) {
+    const int col = c0 + (q % CPR) * PER;
+    return *(const u32x4*)(M + (int64_t)row * D + (col < D ? col : c0));
+  }
+};
+
+// One tile's W rows (ids past V re-read id V-1: their entries are inactive), held in
+// registers between their load and their store to LDS.
+template <typename T>
+struct FewStage {
+  static constexpr int NL = FEW_TILE * FewChunks<T>::CPR / FEW_THREADS;  // chunks per thread
+  u32x4 c[NL];
+  __device__ __forceinline__ void load(const T* __restrict__ W, int v0, int V, int D, int c0,
+                                       int t) {
+#pragma unroll
+    for (int i = 0; i < NL; ++i) {
+      const int q = i * FEW_THREADS + t;
+      c[i] = FewChunks<T>::load(W, min(v0 + q / FewChunks<T>::CPR, V - 1), q, D, c0);
+    }
+  }
+  __device__ __forceinline__ void store(T* wt, int t) const {
+#pragma unroll
+    for (int i = 0; i < NL; ++i) ((u32x4*)wt)[i * FEW_THREADS + t] = c[i];
+  }
+};
+
+template <typename T, typename O, typename RT>
+__global__ __launch_bounds__(FEW_THREADS) void bwd_few_kernel(
+    const T* __restrict__ grad, const RT* __restrict__ reps, const int32_t* __restrict__ idx,
+    const void* __restrict__ mask, int mdt, const T* __restrict__ H, const T* __restrict__ W,
+    float* __restrict__ part, O* __restrict__ dW, O* __restrict__ dbias, int B, int S, int D,
+    int V, int slices, int range_len) {
+  // Each table has one more row, of zeros (row FEW_TILE, FEW_ROWS): a pass points a row or
+  // id with no entry left at it, and adding g' * w = +0 * +0 changes no sum.
+  __shared__ __attribute__((aligned(16))) T wt[FEW_TILE + 1][FEW_COLS];  // the tile's W rows
+  __shared__ __attribute__((aligned(16))) T hs[FEW_ROWS + 1][FEW_COLS];  // H's B*S rows, this slice
+  __shared__ float eg[FEW_ROWS][FEW_TILE + 1];  // g' of entry (b, v0 + id) at [b][id], 0 = inactive
+  __shared__ uint8_t es[FEW_TILE][FEW_ES_LD];       // its index s, FEW_NONE = inactive
+  __shared__ float maskf[FEW_ROWS];
+  const int t = threadIdx.x, lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);  // uniform: scalar registers, branches
+  const int range = (int)blockIdx.x / slices, slice = (int)blockIdx.x - range * slices;
+  const int c0 = slice * FEW_COLS;
+  const int BS = B * S;
+  const int v_beg = range * range_len, v_end = min(V, v_beg + range_len);
+  const bool dw_on = dW != nullptr || dbias != nullptr;
+  for (int i = t; i < BS; i += FEW_THREADS) maskf[i] = load_mask(mask, mdt, i);
+  for (int i = t; i < FEW_COLS; i += FEW_THREADS) {
+    wt[FEW_TILE][i] = T(0.0f);
+    hs[FEW_ROWS][i] = T(0.0f);
+  }
+  for (int i = t; i < FEW_ROWS; i += FEW_THREADS) eg[i][FEW_TILE] = 0.0f;
+  if (dW != nullptr) {  // (H may be absent when only dbias is asked for)
+    for (int q = t; q < BS * FewChunks<T>::CPR; q += FEW_THREADS)
+      ((u32x4*)&hs[0][0])[q] = FewChunks<T>::load(H, q / FewChunks<T>::CPR, q, D, c0);
+  }
+  // This wave's dH rows: batch row and index of each (rows past B*S take none).
+  int rb[FEW_RPW], rs[FEW_RPW];
+#pragma unroll
+  for (int r = 0; r < FEW_RPW; ++r) {
+    const int row = wave * FEW_RPW + r;
+    rb[r] = row < BS ? row / S : 0;
+    rs[r] = row < BS ? row - rb[r] * S : -1;
+  }
+  f32x4 acc[FEW_RPW];
+#pragma unroll
+  for (int r = 0; r < FEW_RPW; ++r) acc[r] = f32x4{0.f, 0.f, 0.f, 0.f};
+  // The tile's W rows and entries (b, v0 + lane), loaded one tile ahead; round j of wave w
+  // holds batch row b = FEW_WAVES j + w (B <= FEW_ROWS).
+  FewStage<T> stage;
+  T gr[FEW_NJ];
+  RT rr[FEW_NJ];
+  int sr[FEW_NJ];
+  auto load_entries = [&](int v0) {
+    const int v = min(v0 + lane, V - 1);
+#pragma unroll
+    for (int j = 0; j < FEW_NJ; ++j) {
+      const int b = FEW_WAVES * j + wave;
+      if (b < B) {  // uniform per wave
+        const int64_t o = (int64_t)b * V + v;
+        gr[j] = grad[o];
+        rr[j] = reps[o];
+        sr[j] = idx[o];
+      }
+    }
+  };
+  stage.load(W, v_beg, V, D, c0, t);
+  load_entries(v_beg);
+  const T* wcol = &wt[0][lane * 4];
+  const int c = c0 + lane * 4;
+  for (int v0 = v_beg; v0 < v_end; v0 += FEW_TILE) {
+    // the previous tile's rows and ids are done: wt, eg and es are free
+    few_barrier();
+    stage.store(&wt[0][0], t);
+    const bool more = v0 + FEW_TILE < v_end;
+    // The next tile's W rows load under all of this tile's work; its entries load once
+    // this tile's are used, below. (The next tile's first wait is for all of them, and for
+    // this tile's dW stores: stores and loads share one counter.)
+    if (more) stage.load(W, v0 + FEW_TILE, V, D, c0, t);
+    const int v = v0 + lane;
+#pragma unroll
+    for (int j = 0; j < FEW_NJ; ++j) {
+      const int b = FEW_WAVES * j + wave;
+      if (b < B) {  // uniform per wave
+        float gp;
+        const int si = sr[j];
+        const bool act = v < v_end && entry(gr[j], rr[j], si, maskf + b * S, S, &gp) &&
+                         gp != 0.0f;
+        eg[b][lane] = act ? gp : 0.0f;
+        es[lane][b] = act ? (uint8_t)si : FEW_NONE;
+      }
+    }
+    if (more) load_entries(v0 + FEW_TILE);
+    few_barrier();
+    // dW, dbias: this wave's ids, FEW_IDC at a time, pass k taking each id's k-th active
+    // batch row (ascending); an id with none left takes the zero rows.
+    if (dw_on) {
+#pragma unroll 1
+      for (int i0 = 0; i0 < FEW_IPW; i0 += FEW_IDC) {
+        uint64_t p[FEW_IDC];
+        int npass = 0;
+#pragma unroll
+        for (int i = 0; i < FEW_IDC; ++i) {
+          const int il = wave * FEW_IPW + i0 + i;
+          // eg holds +0.0 for every inactive entry
+          p[i] = __ballot(lane < B && __float_as_int(eg[min(lane, FEW_ROWS - 1)][il]) != 0);
+          npass = max(npass, __popcll(p[i]));
+        }
+        f32x4 ad[FEW_IDC];
+        float bsum[FEW_IDC];
+#pragma unroll
+        for (int i = 0; i < FEW_IDC; ++i) {
+          ad[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+          bsum[i] = 0.0f;
+        }
+        for (int k = 0; k < npass; ++k) {
+          float g[FEW_IDC];
+          f32x4 h[FEW_IDC];
+#pragma unroll
+          for (int i = 0; i < FEW_IDC; ++i) {
+            const bool on = p[i] != 0;  // uniform
+            const int b = on ? (int)__builtin_ctzll(p[i]) : 0;
+            p[i] &= ~(1ull << b);
+            const int iv = wave * FEW_IPW + i0 + i;
+            g[i] = eg[b][on ? iv : FEW_TILE];
+            const int hr = on ? b * S + (int)es[iv][b] : FEW_ROWS;
+            h[i] = load4(&hs[hr][lane * 4]);
+          }
+#pragma unroll
+          for (int i = 0; i < FEW_IDC; ++i) {
+            ad[i] = f32x4{fmaf(g[i], h[i][0], ad[i][0]), fmaf(g[i], h[i][1], ad[i][1]),
+                          fmaf(g[i], h[i][2], ad[i][2]), fmaf(g[i], h[i][3], ad[i][3])};
+            bsum[i] += g[i];
+          }
+        }
+#pragma unroll
+        for (int i = 0; i < FEW_IDC; ++i) {
+          const int vi = v0 + wave * FEW_IPW + i0 + i;
+          if (vi < v_end) {
+            if (dW != nullptr && c < D) store4(dW + (int64_t)vi * D + c, ad[i]);
+            if (dbias != nullptr && slice == 0 && lane == 0) dbias[vi] = from_f32<O>(bsum[i]);
+          }
+        }
+      }
+    }
+    // dH: this wave's rows, pass k taking each row's k-th id (ascending); a row with none
+    // left takes the zero rows. Straight-line passes: the ids are scalar, the coefficients
+    // come by broadcast LDS reads, and a pass's reads are independent of each other.
+    {
+      uint64_t m[FEW_RPW];
+      int npass = 0;
+#pragma unroll
+      for (int r = 0; r < FEW_RPW; ++r) {
+        m[r] = __ballot((int)es[lane][rb[r]] == rs[r]);
+        npass = max(npass, __popcll(m[r]));
+      }
+      for (int k = 0; k < npass; ++k) {
+        float g[FEW_RPW];
+        f32x4 w[FEW_RPW];
+#pragma unroll
+        for (int r = 0; r < FEW_RPW; ++r) {
+          const int id = m[r] != 0 ? (int)__builtin_ctzll(m[r]) : FEW_TILE;  // uniform
+          m[r] &= ~(1ull << (id & 63));
+          g[r] = eg[rb[r]][id];
+          w[r] = load4(wcol + id * FEW_COLS);
+        }
+#pragma unroll
+        for (int r = 0; r < FEW_RPW; ++r)
+          acc[r] = f32x4{fmaf(g[r], w[r][0], acc[r][0]), fmaf(g[r], w[r][1], acc[r][1]),
+                         fmaf(g[r], w[r][2], acc[r][2]), fmaf(g[r], w[r][3], acc[r][3])};
+      }
+    }
+  }
+  if (c < D) {
+    float* out = part + (int64_t)range * BS * D + c;
+#pragma unroll
+    for (int r = 0; r < FEW_RPW; ++r) {
+      const int row = wave * FEW_RPW + r;
+      if (row < BS) *(f32x4*)(out + (int64_t)row * D) = acc[r];
+    }
+  }
+}
+
+// dH = the ranges' partial rows added in range order, in the output dtype. A workgroup
+// takes 256 elements (4 per lane of a wave); its FEW_SUM_WAVES waves sum consecutive
+// groups of the ranges, and the groups are added in order.
+constexpr int FEW_SUM_WAVES = 8;
+template <typename O>
+__global__ __launch_bounds__(64 * FEW_SUM_WAVES) void bwd_few_sum_kernel(
+    const float* __restrict__ part, O* __restrict__ dH, int64_t n, int ranges) {
+  __shared__ f32x4 red[FEW_SUM_WAVES - 1][64];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int64_t i = ((int64_t)blockIdx.x * 64 + lane) * 4;
+  const int q = (ranges + FEW_SUM_WAVES - 1) / FEW_SUM_WAVES;
+  const int k0 = min(ranges, wave * q), k1 = min(ranges, k0 + q);
+  f32x4 s = f32x4{0.f, 0.f, 0.f, 0.f};
+  if (i < n) {  // n is a multiple of 4
+    int k = k0;
+    for (; k + 4 <= k1; k += 4) {
+      f32x4 x[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) x[j] = *(const f32x4*)(part + (int64_t)(k + j) * n + i);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) s += x[j];
+    }
+    for (; k < k1; ++k) s += *(const f32x4*)(part + (int64_t)k * n + i);
+  }
+  if (wave > 0) red[wave - 1][lane] = s;
+  __syncthreads();
+  if (wave == 0 && i < n) {
+#pragma unroll
+    for (int w = 0; w < FEW_SUM_WAVES - 1; ++w) s += red[w][lane];
+    store4(dH + i, s);
+  }
+}
+
 // The five-kernel path runs dW in the dH launch where it can (SPARTON_BWD_DW_MERGE=0 keeps
 // it a separate launch; tests compare the two).
 static bool dw_merge_on() {
@@ -1378,6 +1691,18 @@ static void launch_rows(const T* g, const RT* r, const int32_t* idx, const void*
   // gives each dH row one wave: it needs many ranges and few blocks. Measured on MI355X:
   // B = 32, S = 256, V = 30522: fused 61 us vs 65 us; B = 2, S = 32 (dense grads):
   // 1133 us vs 331 us; V = 250002: 753 us vs 460 us.
+  const FewPlan few = few_plan(B, S, D, V);
+  if (few.fits && few_enabled() && dH != nullptr) {
+    float* part = (float*)ws;
+    hipLaunchKernelGGL((bwd_few_kernel<T, O, RT>), dim3((unsigned)(few.ranges * few.slices)),
+                       dim3(FEW_THREADS), 0, st, g, r, idx, mask, mdt, H, W, part, dW, dbias,
+                       (int)B, (int)S, (int)D, (int)V, few.slices, few.range_len);
+    const int64_t n = B * S * D;
+    hipLaunchKernelGGL((bwd_few_sum_kernel<O>), dim3((unsigned)cdiv(n, 256)), dim3(64 * FEW_SUM_WAVES),
+                       0, st,
+                       (const float*)part, dH, n, few.ranges);
+    return;
+  }
   const bool fused = fused_path_enabled() && dH != nullptr && dW != nullptr && B * S > 0 &&
                      D > 0 && V > 0 &&
                      B <= DW_STAGE_B && S <= FUSE_MAX_S && V <= FUSE_V_FAST &&
@@ -1557,7 +1882,8 @@ using namespace sparton;
 extern "C" __attribute__((visibility("default"))) size_t sparton_bwd_workspace_bytes(
     int64_t B, int64_t S, int64_t D, int64_t V) {
   if (B <= 0 || S <= 0 || D <= 0 || V < 0) return 0;
-  return bwd::pass_layout(B, S, V).total;
+  const bwd::FewPlan few = bwd::few_plan(B, S, D, V);
+  return std::max(bwd::pass_layout(B, S, V).total, few.fits ? few.part_bytes : (size_t)0);
 }
 
 extern "C" __attribute__((visibility("default"))) int sparton_bwd(
@@ -1586,7 +1912,7 @@ extern "C" __attribute__((visibility("default"))) int sparton_bwd(
     return SPARTON_EUNSUPPORTED;
   if (need_dh) {
     if (workspace == nullptr) return SPARTON_EWORKSPACE;
-    if (workspace_bytes < bwd::pass_layout(B, S, V).total) return SPARTON_EWORKSPACE;
+    if (workspace_bytes < sparton_bwd_workspace_bytes(B, S, D, V)) return SPARTON_EWORKSPACE;
     if ((uintptr_t)workspace % 256 != 0) return SPARTON_EALIGN;
   }
   if (!need_dh && !need_dw) return SPARTON_OK;

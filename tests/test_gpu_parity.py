@@ -641,10 +641,12 @@ def test_opcheck_and_compile(device):
     ("bf16", 3, 100, 256, 2000, True, "holes"),    # 300 rows: 4 waves per row
     ("fp16", 1, 700, 64, 500, False, "frac"),      # 700 rows: 2 waves per row
 ], ids=lambda c: "-".join(map(str, c)))
-def test_backward_few_rows_split(case, device):
+def test_backward_few_rows_split(case, device, monkeypatch):
     """Few dH rows: the five-kernel path splits each row's entries over several waves and
-    adds their partial rows in wave order. Against the oracle, and bitwise repeatable."""
+    adds their partial rows in wave order (SPARTON_BWD_FEW=0 keeps batches of at most 64 rows
+    on it too). Against the oracle, and bitwise repeatable."""
     say(f"backward few rows, case {case}")
+    monkeypatch.setenv("SPARTON_BWD_FEW", "0")
     H, W, b, m, G = make_case(*case)
     Hd, Wd, md, Gd = H.to(device), W.to(device), m.to(device), G.to(device)
     bd = None if b is None else b.to(device)
@@ -656,6 +658,91 @@ def test_backward_few_rows_split(case, device):
         assert torch.equal(a, c)
     check_bwd_isolated(H, W, b, m, G, reps32, idx, *outs[0])
 
+
+
+FEW_ROW_CASES = [
+    ("fp32", 2, 32, 768, 30522, True, "int64"),    # config 1's shape: W read once for both rows
+    ("bf16", 1, 64, 1024, 5000, False, "frac"),    # one batch row of 64 positions, no bias
+    ("fp16", 64, 1, 128, 3000, True, "bool"),      # 64 batch rows of one position
+    ("fp32", 3, 20, 72, 2000, True, "holes"),      # a partial 256-column slice, masked holes
+    ("bf16", 2, 16, 4096, 3000, True, "int64"),    # 16 column slices
+    ("fp16", 5, 7, 264, 777, True, "gaps"),        # ragged everything
+]
+
+
+@pytest.mark.parametrize("case", FEW_ROW_CASES, ids=lambda c: "-".join(map(str, c)))
+def test_backward_few_rows_single_w_read(case, device, monkeypatch):
+    """At most 64 dH rows: each W row is read once and added into every dH row it serves
+    (rows held in registers, per-range partials added in range order). Against the oracle,
+    bitwise repeatable, dW and dbias bitwise those of the five-kernel path, dH within fp32
+    rounding of it (the two sum in different orders)."""
+    say(f"backward few rows, single W read, case {case}")
+    H, W, b, m, G = make_case(*case)
+    Hd, Wd, md, Gd = H.to(device), W.to(device), m.to(device), G.to(device)
+    bd = None if b is None else b.to(device)
+    _, idx, reps32 = torch.ops.sparton.fused_sparton_fwd_train(Hd, Wd, bd, md)
+    outs = [[None if t is None else t.clone()
+             for t in torch.ops.sparton.fused_sparton_bwd(Gd, reps32, idx, Hd, Wd, bd, md)]
+            for _ in range(2)]
+    monkeypatch.setenv("SPARTON_BWD_FEW", "0")
+    other = torch.ops.sparton.fused_sparton_bwd(Gd, reps32, idx, Hd, Wd, bd, md)
+    torch.cuda.synchronize()
+    for a, c in zip(*outs):
+        assert (a is None and c is None) or torch.equal(a, c)
+    torch.testing.assert_close(outs[0][0], other[0], **BWD_TOL)
+    assert torch.equal(outs[0][1], other[1])
+    assert (outs[0][2] is None and other[2] is None) or torch.equal(outs[0][2], other[2])
+    if Hd.dtype != torch.float32:
+        # gradients in the input dtype: dW and dbias the same bits, dH within one rounding
+        tr_other = torch.ops.sparton.fused_sparton_bwd_train(Gd, reps32, idx, Hd, Wd, bd, md)
+        monkeypatch.delenv("SPARTON_BWD_FEW")
+        tr = torch.ops.sparton.fused_sparton_bwd_train(Gd, reps32, idx, Hd, Wd, bd, md)
+        torch.cuda.synchronize()
+        assert tr[1].dtype == Hd.dtype and torch.equal(tr[1], tr_other[1])
+        assert torch.equal(tr[2], tr_other[2])
+        torch.testing.assert_close(tr[0].float(), tr_other[0].float(), rtol=1e-2, atol=1e-6)
+    check_bwd_isolated(H, W, b, m, G, reps32, idx, *outs[0])
+
+
+def _bwd_capi(Gd, reps32, idx, Hd, Wd, md, dH, dW, db):
+    """sparton_bwd through the C ABI with any of the three outputs left out (None)."""
+    B, S, D = Hd.shape
+    V = Wd.shape[0]
+    L = _lib.load()
+    ws_bytes = int(L.sparton_bwd_workspace_bytes(B, S, D, V))
+    ws = torch.empty((max(ws_bytes, 1),), dtype=torch.uint8, device=Hd.device)
+    ptr = lambda t: None if t is None else t.data_ptr()
+    Gd = Gd.to(Hd.dtype).contiguous()
+    rc = L.sparton_bwd(Gd.data_ptr(), reps32.data_ptr(), _lib.DTYPE_CODE[reps32.dtype],
+                       idx.data_ptr(), md.data_ptr(), _lib.MASK_CODE[md.dtype], Hd.data_ptr(),
+                       Wd.data_ptr(), ptr(dH), ptr(dW), ptr(db), _lib.DTYPE_CODE[torch.float32],
+                       ws.data_ptr(), ws_bytes, B, S, D, V, _lib.DTYPE_CODE[Hd.dtype],
+                       torch.cuda.current_stream().cuda_stream)
+    assert rc == 0, L.sparton_strerror(rc)
+
+
+@pytest.mark.parametrize("case", [FEW_ROW_CASES[0], FEW_ROW_CASES[2], FEW_ROW_CASES[5]],
+                         ids=lambda c: "-".join(map(str, c)))
+def test_backward_few_rows_partial_outputs(case, device):
+    """The few-row launch asked for dH with dbias but no dW, and for dH with dW but no
+    dbias: the outputs it does write are bitwise those of the full call."""
+    say(f"backward few rows, partial outputs, case {case}")
+    H, W, b, m, G = make_case(*case)
+    Hd, Wd, md, Gd = H.to(device), W.to(device), m.to(device), G.to(device)
+    bd = None if b is None else b.to(device)
+    _, idx, reps32 = torch.ops.sparton.fused_sparton_fwd_train(Hd, Wd, bd, md)
+    B, S, D = Hd.shape
+    V = Wd.shape[0]
+    f32 = dict(dtype=torch.float32, device=device)
+    full = [torch.empty((B, S, D), **f32), torch.empty((V, D), **f32), torch.empty((V,), **f32)]
+    _bwd_capi(Gd, reps32, idx, Hd, Wd, md, *full)
+    no_dw = [torch.empty((B, S, D), **f32), torch.empty((V,), **f32)]
+    _bwd_capi(Gd, reps32, idx, Hd, Wd, md, no_dw[0], None, no_dw[1])
+    no_db = [torch.empty((B, S, D), **f32), torch.empty((V, D), **f32)]
+    _bwd_capi(Gd, reps32, idx, Hd, Wd, md, no_db[0], no_db[1], None)
+    torch.cuda.synchronize()
+    assert torch.equal(no_dw[0], full[0]) and torch.equal(no_dw[1], full[2])
+    assert torch.equal(no_db[0], full[0]) and torch.equal(no_db[1], full[1])
 
 
 @pytest.mark.parametrize("case,long_rows", [
@@ -673,6 +760,7 @@ def test_backward_dw_in_dh_launch(case, long_rows, device, monkeypatch):
     Hd, Wd, md, Gd = H.to(device), W.to(device), m.to(device), G.to(device)
     bd = None if b is None else b.to(device)
     monkeypatch.setenv("SPARTON_BWD_PATH", "five")
+    monkeypatch.setenv("SPARTON_BWD_FEW", "0")
     if long_rows:
         monkeypatch.setenv("SPARTON_BWD_DH_LONG", "1")
     _, idx, reps32 = torch.ops.sparton.fused_sparton_fwd_train(Hd, Wd, bd, md)
