@@ -712,12 +712,6 @@ __device__ __forceinline__ void wait_all() {
   asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
 }
 
-// Step 0 of a prefetched unit: wait for every memory operation but the three metadata loads
-// issued last (vector memory operations complete in issue order). Slab 1's copies, issued
-// before them, have landed; the metadata is waited for at step 1.
-__device__ __forceinline__ void wait_all_but_meta() {
-  asm volatile("s_waitcnt vmcnt(3) lgkmcnt(0)" ::: "memory");
-}
 
 // ---- the workgroup's unit sequence ----
 //
@@ -729,8 +723,9 @@ __device__ __forceinline__ void wait_all_but_meta() {
 // The copy waves issue slab k+1 at the start of step k (k >= 1; slab 1 is issued before
 // step 0), into the stage that slab k-1 left at B_(k-1), and wait for it before B_k.
 // With prefetch the next unit's slab 0 is issued at step nk-1 and its slab 1 after
-// B_(nk-1), and its metadata is fetched during steps 0, 2 and 3 (step 1 writes the
-// previous unit's results; they and the metadata share a buffer).
+// B_(nk-1). Its metadata is loaded into registers one unit ahead (with the unit's slab 1)
+// and written to the metadata buffer at steps 2 and 3: step 1 writes the previous unit's
+// results, which read that buffer.
 constexpr int PREFETCH_MIN_NK = 5;
 
 struct Unit {
@@ -873,7 +868,25 @@ __device__ void copy_path(Smem& sm, const Args<T>& a, const Outputs<T>& o, int w
   cu.n_valid = cur.n_valid;
   copy_start(sm, a, o, sm.um[0], cu, buf, prev, sm.um[1], ct, c, lane);
 
+  // The metadata of a prefetched unit (this copy thread's mask row, group-list entry and
+  // bias bits) is loaded into registers one unit ahead, with the unit's slab 1 (before E),
+  // so step 0's wait covers it; steps 2 and 3 write it to the metadata buffer.
+  struct MetaRegs {
+    float mv;
+    int code;
+    uint32_t bias;
+  };
+  auto load_meta = [&](const Unit& x) {
+    MetaRegs mr{0.0f, 0, 0u};
+    if (x.u >= 0 && nk >= PREFETCH_MIN_NK) {
+      mr.mv = a.rowmask[(int64_t)x.m * BM + ct];
+      mr.code = a.list[min(max(group_entry(x.m, min(ct, NGRP + 1)), 0), a.n_grp - 1)];
+      if (a.bias != nullptr) mr.bias = load_bits(a.bias + min(x.v0 + ct, a.V - 1), 0);
+    }
+    return mr;
+  };
   Unit next = unit_of(w, 1, G, n_units, n_mt, n_vt, a.n_grp);
+  MetaRegs meta = load_meta(next);
   for (int r = 1;; ++r) {
     const bool pre = next.u >= 0 && nk >= PREFETCH_MIN_NK;
     UnitMeta& um_next = sm.um[par ^ 1];
@@ -882,9 +895,6 @@ __device__ void copy_path(Smem& sm, const Args<T>& a, const Outputs<T>& o, int w
     nx.m = next.m;
     nx.v0 = next.v0;
     nx.n_valid = next.n_valid;
-    int code_bits = 0;
-    uint32_t bias_bits = 0;
-    float mv = 0.0f;
     for (int k = 0; k < nk; ++k) {
       if (k >= 1) {
         if (k + 1 < nk)
@@ -893,27 +903,16 @@ __device__ void copy_path(Smem& sm, const Args<T>& a, const Outputs<T>& o, int w
           issue_slab(sm, a, nx, 0, buf_next, c, lane);
       }
       if (pre) {
-        if (k == 0) {
-          if (ct == 0) um_next.mask_binary = 1;
-          __builtin_amdgcn_global_load_lds((const void*)(a.rowmask + (int64_t)nx.m * BM + ct),
-                                           (lds_void*)&um_next.maskf[c * 64], 4, 0, 0);
-          // Exactly three vector memory loads per wave, issued whatever the lane: the mask
-          // copy above, the list entry (used by lanes < NGRP + 2) and the bias bits (a dummy
-          // read of the list without bias), so that step 0 can wait for slab 1 alone. Both
-          // addresses depend on the lane, so neither can become a scalar load (which the
-          // vector memory count would not track).
-          code_bits = a.list[min(max(group_entry(nx.m, min(ct, NGRP + 1)), 0), a.n_grp - 1)];
-          const T* bsrc = a.bias != nullptr ? a.bias + min(nx.v0 + ct, a.V - 1)
-                                            : reinterpret_cast<const T*>(a.list + min(ct, a.n_grp - 1));
-          bias_bits = load_bits(bsrc, 0);
+        if (k == 1) {
+          if (ct == 0) um_next.mask_binary = 1;  // cleared at step 2 by any other value
         } else if (k == 2) {
           const int e = group_entry(nx.m, ct);
           const bool ok = e >= 0 && e < a.n_grp && (ct >= NGRP || ct < nx.n_valid);
-          put_groups(um_next, ok ? code_bits : -1, a.ngrp, ct);
-          mv = um_next.maskf[ct];
-          put_mask_words(um_next, mv, ct, lane);
+          put_groups(um_next, ok ? meta.code : -1, a.ngrp, ct);
+          um_next.maskf[ct] = meta.mv;
+          put_mask_words(um_next, meta.mv, ct, lane);
           const int col = nx.v0 + ct;
-          um_next.bias[ct] = (a.bias != nullptr && col < a.V) ? bits_to_f32<T>(bias_bits) : 0.0f;
+          um_next.bias[ct] = (a.bias != nullptr && col < a.V) ? bits_to_f32<T>(meta.bias) : 0.0f;
         } else if (k == 3) {
           row_offsets(um_next, nx.n_valid, a.S, a.row_bytes, c, lane, nx.a_off);
         }
@@ -923,10 +922,7 @@ __device__ void copy_path(Smem& sm, const Args<T>& a, const Outputs<T>& o, int w
                       o.reps_f32, o.part);
         prev.u = -1;
       }
-      if (k == 0 && pre)
-        wait_all_but_meta();  // slab 1 (issued before E) landed; the metadata loads may not have
-      else
-        wait_all();
+      wait_all();
       if (k + 1 < nk) {
         if (k + 1 >= a.nk_full) zero_tail(sm, a.row_bytes, k + 1, buf ^ ((k + 1) & 1), c, lane);
       } else if (pre && 0 >= a.nk_full) {
@@ -935,8 +931,10 @@ __device__ void copy_path(Smem& sm, const Args<T>& a, const Outputs<T>& o, int w
       lds_barrier();  // B_k
     }
     if (pre) issue_slab(sm, a, nx, 1, buf_next ^ 1, c, lane);
-    // the unit after next, worked out while the compute waves run their epilogue
+    // the unit after next, worked out while the compute waves run their epilogue, and its
+    // metadata loads
     const Unit next2 = next.u >= 0 ? unit_of(w, r + 1, G, n_units, n_mt, n_vt, a.n_grp) : next;
+    if (pre) meta = load_meta(next2);
     lds_barrier();  // E: the compute waves' keys are written
     if (next.u < 0) {
       write_unit<T>(sm, sm.um[par], cur.m, cur.v0, a.V, cur.n_valid, ct, o.reps, o.argmax,
