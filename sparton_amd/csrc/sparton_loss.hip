@@ -24,6 +24,10 @@
 // The whole loss moves each of Q and R once forward and once backward: HBM-bound, small.
 
 #include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include <type_traits>
 
 #include "sparton_common.h"
 
@@ -609,6 +613,196 @@ __global__ __launch_bounds__(64) void loss_final_large_kernel(const float* __res
   }
 }
 
+// ---- 16-bit reps on 16-bit MFMAs ----
+//
+// A product of two bf16 (or two fp16) values is exact in fp32, so for 16-bit reps the score
+// GEMM runs on v_mfma_f32_32x32x16_{bf16,f16}: 8 times the k per instruction of the fp32
+// MFMA, in the same 32 x 32 output layout. The stage's operands are kept in LDS as [row][k]
+// 16-bit values, rows LDH apart: 80 bytes, so the 16 rows of one ds_read_b128 phase fall in
+// distinct banks. A lane's MFMA operand (8 consecutive k of one row) is one 16-byte read.
+// The global loads are those of the fp32 path (element by element: a row of V elements is
+// not 16-byte aligned in general).
+// The gradients' products P R and P^T Q take P (fp32) as two bf16 parts, p = hi + lo + r
+// with |r| <= 2^-18 |p| (both round to nearest even, p - hi is exact), against R or Q exact
+// in bf16: two MFMAs per step, lo first. fp16 reps keep the fp32 MFMA there (P's range does
+// not fit fp16).
+constexpr int LDH = 40;
+
+template <typename T> struct Mfma16;
+template <> struct Mfma16<bf16> {
+  static __device__ __forceinline__ f32x16 run(const u32x4& a, const u32x4& b, const f32x16& c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  }
+};
+template <> struct Mfma16<f16> {
+  static __device__ __forceinline__ f32x16 run(const u32x4& a, const u32x4& b, const f32x16& c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+};
+
+template <typename T> __device__ __forceinline__ uint16_t bits16(T x) {
+  return __builtin_bit_cast(uint16_t, x);
+}
+
+// load_kc's registers (thread t: k = t % 32 of rows t / 32 + 8 u) into a [rows][KS] tile.
+template <typename T>
+__device__ __forceinline__ void store_kc16(uint16_t* s, const T (&v)[16]) {
+  const int t = threadIdx.x, kk = t & 31, rb = t >> 5;
+#pragma unroll
+  for (int u = 0; u < 16; ++u) s[(rb + 8 * u) * LDH + kk] = bits16(v[u]);
+}
+
+// The operand of lane (l32, h) for k step s of a stage: row `row`, k = 16 s + 8 h .. + 7.
+__device__ __forceinline__ u32x4 frag16(const uint16_t* s, int row, int ks) {
+  const int h = (threadIdx.x & 63) >> 5;
+  return *(const u32x4*)(s + row * LDH + 16 * ks + 8 * h);
+}
+
+// acc[bi][bj] += A[am0 + 32 bi .., :] B[bn0 + 32 bj .., :]^T over one stage.
+template <typename T, int BI, int BJ>
+__device__ __forceinline__ void mma16_stage(const uint16_t* sA, int am0, const uint16_t* sB, int bn0,
+                                            f32x16 (&acc)[BI][BJ]) {
+  const int l32 = threadIdx.x & 31;
+#pragma unroll
+  for (int ks = 0; ks < KS / 16; ++ks) {
+    u32x4 a[BI], b[BJ];
+#pragma unroll
+    for (int i = 0; i < BI; ++i) a[i] = frag16(sA, am0 + 32 * i + l32, ks);
+#pragma unroll
+    for (int j = 0; j < BJ; ++j) b[j] = frag16(sB, bn0 + 32 * j + l32, ks);
+#pragma unroll
+    for (int i = 0; i < BI; ++i)
+#pragma unroll
+      for (int j = 0; j < BJ; ++j) acc[i][j] = Mfma16<T>::run(a[i], b[j], acc[i][j]);
+  }
+}
+
+// loss_score_kernel for 16-bit reps.
+template <typename T>
+__global__ __launch_bounds__(NT) void loss_score16_kernel(const T* __restrict__ Q,
+                                                          const T* __restrict__ R, int Bq, int Bd,
+                                                          int V, int chunk, float* __restrict__ part) {
+  __shared__ __attribute__((aligned(16))) uint16_t sA[TM * LDH];
+  __shared__ __attribute__((aligned(16))) uint16_t sB[TM * LDH];
+  const int tj = (Bd + TM - 1) / TM;
+  const int i0 = (blockIdx.x / tj) * TM, j0 = (blockIdx.x % tj) * TM;
+  const int kc0 = blockIdx.y * chunk, kc1 = min(V, kc0 + chunk);
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, wm = wave >> 1, wn = wave & 1;
+  f32x16 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = zero16();
+  T ra[16], rb[16];
+  load_kc(Q, V, i0, Bq, kc0, kc1, ra);
+  load_kc(R, V, j0, Bd, kc0, kc1, rb);
+  for (int k0 = kc0; k0 < kc1; k0 += KS) {
+    __syncthreads();  // the previous stage is read
+    store_kc16(sA, ra);
+    store_kc16(sB, rb);
+    __syncthreads();
+    if (k0 + KS < kc1) {  // the next stage's loads run under this stage's MFMAs
+      load_kc(Q, V, i0, Bq, k0 + KS, kc1, ra);
+      load_kc(R, V, j0, Bd, k0 + KS, kc1, rb);
+    }
+    mma16_stage<T, 2, 2>(sA, wm * 64, sB, wn * 64, acc);
+  }
+  float* out = part + (size_t)blockIdx.y * Bq * Bd;
+  const int l32 = lane & 31, h = lane >> 5;
+#pragma unroll
+  for (int bi = 0; bi < 2; ++bi)
+#pragma unroll
+    for (int bj = 0; bj < 2; ++bj) {
+      const int j = j0 + wn * 64 + 32 * bj + l32;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int i = i0 + wm * 64 + 32 * bi + acc_row(r, h);
+        if (i < Bq && j < Bd) out[(size_t)i * Bd + j] = acc[bi][bj][r];
+      }
+    }
+}
+
+// p as bf16 hi and lo bits.
+__device__ __forceinline__ void split_bf16(float p, uint16_t& hi, uint16_t& lo) {
+  const bf16 h = (bf16)p;
+  hi = bits16(h);
+  lo = bits16((bf16)(p - (float)h));
+}
+
+// grad_tile for bf16 reps: A (P rows or columns) as two bf16 parts, B = the bf16 rows of R or Q.
+template <bool A_KC>
+__device__ __forceinline__ void grad_tile16(uint16_t* sAh, uint16_t* sAl, uint16_t* sB,
+                                            const float* __restrict__ P, int Bq, int Bd,
+                                            const bf16* __restrict__ Bsrc, int K,
+                                            const bf16* __restrict__ X, int rows, int m0, int c0,
+                                            int V, float c_ce, float c_s, float c_f,
+                                            const float* colsum, bf16* __restrict__ G) {
+  const int t = threadIdx.x, wave = t >> 6, lane = t & 63, l32 = lane & 31, h = lane >> 5;
+  f32x16 acc[2] = {zero16(), zero16()};
+  if (K > 0) {
+    float pa[16];
+    bf16 rbv[KS * NC / NT];
+    auto load_a = [&](int k0) {
+      if (A_KC) load_kc(P, Bd, m0, Bq, k0, K, pa);          // A[m][k] = P[m0 + m][k]
+      else load_nc<float, TM>(P, Bd, k0, K, m0, Bd, pa);    // A[m][k] = P[k][m0 + m]
+    };
+    load_a(0);
+    load_nc<bf16, NC>(Bsrc, V, 0, K, c0, V, rbv);
+    for (int k0 = 0; k0 < K; k0 += KS) {
+      __syncthreads();
+#pragma unroll
+      for (int u = 0; u < 16; ++u) {
+        // load_kc: k = t % 32 of rows t / 32 + 8 u; load_nc<TM>: m = t % 128 of k rows t / 128 + 2 u
+        const int m = A_KC ? (t >> 5) + 8 * u : t % TM;
+        const int k = A_KC ? (t & 31) : t / TM + 2 * u;
+        uint16_t hi, lo;
+        split_bf16(pa[u], hi, lo);
+        sAh[m * LDH + k] = hi;
+        sAl[m * LDH + k] = lo;
+      }
+#pragma unroll
+      for (int u = 0; u < KS * NC / NT; ++u)  // load_nc<NC>: n = t % 64 of k rows t / 64 + 4 u
+        sB[(t % NC) * LDH + t / NC + (NT / NC) * u] = bits16(rbv[u]);
+      __syncthreads();
+      if (k0 + KS < K) {
+        load_a(k0 + KS);
+        load_nc<bf16, NC>(Bsrc, V, k0 + KS, K, c0, V, rbv);
+      }
+#pragma unroll
+      for (int ks = 0; ks < KS / 16; ++ks) {
+        const u32x4 ah = frag16(sAh, wave * 32 + l32, ks), al = frag16(sAl, wave * 32 + l32, ks);
+#pragma unroll
+        for (int bj = 0; bj < 2; ++bj) {
+          const u32x4 b = frag16(sB, 32 * bj + l32, ks);
+          acc[bj] = Mfma16<bf16>::run(al, b, acc[bj]);
+          acc[bj] = Mfma16<bf16>::run(ah, b, acc[bj]);
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int bj = 0; bj < 2; ++bj) {
+    const int cl = 32 * bj + l32, c = c0 + cl;
+    bf16 xv[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int i = m0 + wave * 32 + acc_row(r, h);
+      xv[r] = (i < rows && c < V) ? X[(int64_t)i * V + c] : bf16(0.0f);
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int i = m0 + wave * 32 + acc_row(r, h);
+      if (i < rows && c < V) {
+        const float x = to_f32(xv[r]);
+        const float sg = x > 0.0f ? 1.0f : (x < 0.0f ? -1.0f : 0.0f);
+        G[(int64_t)i * V + c] = from_f32<bf16>(c_ce * acc[bj][r] + c_s * sg + c_f * colsum[cl]);
+      }
+    }
+  }
+}
+
 // 128 rows of one gradient over the workgroup's 64 columns: acc = sum_k A[m][k] B[k][n] with A
 // from a K-contiguous (P rows, dQ) or N-contiguous (P columns, dR) source; wave w owns rows
 // 32 w .. 32 w + 31 (two 32 x 32 blocks). Then G = c_ce acc + c_s sign(X) + c_f colsum, in T.
@@ -666,14 +860,13 @@ __device__ __forceinline__ void grad_tile(float* sA, float* sB, const float* __r
   }
 }
 
-template <typename T>
+// M16: bf16 reps, the products on bf16 MFMAs (P in two parts); else the fp32 MFMA.
+template <typename T, bool M16>
 __global__ __launch_bounds__(NT) void loss_bwd_large_kernel(const T* __restrict__ Q, const T* __restrict__ R,
                                                             const float* __restrict__ P, const Grads6 g,
                                                             int Bq, int Bd, int V, float w_ce, float w_l1,
                                                             float w_fl, T* __restrict__ GQ,
                                                             T* __restrict__ GR) {
-  __shared__ float sA[KS * LDA];
-  __shared__ float sB[KS * LDB];
   __shared__ float cpart[2][4][NC];
   __shared__ float colsum[2][NC];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -711,10 +904,24 @@ __global__ __launch_bounds__(NT) void loss_bwd_large_kernel(const T* __restrict_
   const float c_sd = Bd > 0 ? (g0 * w_l1 + grad_of(g, 3)) / (float)Bd : 0.0f;
   const float c_fq = 2.0f * (g0 * w_fl + grad_of(g, 4)) / (float)V;
   const float c_fd = 2.0f * (g0 * w_fl + grad_of(g, 5)) / (float)V;
-  for (int i0 = 0; i0 < Bq; i0 += TM)  // dQ = c_ce P R + ...
-    grad_tile<T, true>(sA, sB, P, Bq, Bd, R, Bd, Q, Bq, i0, c0, V, c_ce, c_sq, c_fq, colsum[0], GQ);
-  for (int j0 = 0; j0 < Bd; j0 += TM)  // dR = c_ce P^T Q + ...
-    grad_tile<T, false>(sA, sB, P, Bq, Bd, Q, Bq, R, Bd, j0, c0, V, c_ce, c_sd, c_fd, colsum[1], GR);
+  if constexpr (M16) {
+    __shared__ __attribute__((aligned(16))) uint16_t sAh[TM * LDH];
+    __shared__ __attribute__((aligned(16))) uint16_t sAl[TM * LDH];
+    __shared__ __attribute__((aligned(16))) uint16_t sB[NC * LDH];
+    for (int i0 = 0; i0 < Bq; i0 += TM)  // dQ = c_ce P R + ...
+      grad_tile16<true>(sAh, sAl, sB, P, Bq, Bd, R, Bd, Q, Bq, i0, c0, V, c_ce, c_sq, c_fq,
+                        colsum[0], GQ);
+    for (int j0 = 0; j0 < Bd; j0 += TM)  // dR = c_ce P^T Q + ...
+      grad_tile16<false>(sAh, sAl, sB, P, Bq, Bd, Q, Bq, R, Bd, j0, c0, V, c_ce, c_sd, c_fd,
+                         colsum[1], GR);
+  } else {
+    __shared__ float sA[KS * LDA];
+    __shared__ float sB[KS * LDB];
+    for (int i0 = 0; i0 < Bq; i0 += TM)  // dQ = c_ce P R + ...
+      grad_tile<T, true>(sA, sB, P, Bq, Bd, R, Bd, Q, Bq, i0, c0, V, c_ce, c_sq, c_fq, colsum[0], GQ);
+    for (int j0 = 0; j0 < Bd; j0 += TM)  // dR = c_ce P^T Q + ...
+      grad_tile<T, false>(sA, sB, P, Bq, Bd, Q, Bq, R, Bd, j0, c0, V, c_ce, c_sd, c_fd, colsum[1], GR);
+  }
 }
 
 // Score chunking: about 512 workgroups, chunks of whole LDS stages.
@@ -737,6 +944,12 @@ static int64_t workspace_floats(int64_t Bq, int64_t Bd, int64_t V) {
   return s + (slices(V) + 1) * stats_entries(Bq, Bd) + Bq;
 }
 
+// SPARTON_LOSS_MFMA16=0 keeps 16-bit reps on the fp32 MFMA (tests compare the two).
+static bool mfma16_on() {
+  const char* e = getenv("SPARTON_LOSS_MFMA16");
+  return e == nullptr || strcmp(e, "0") != 0;
+}
+
 template <typename T>
 static void fwd(const void* q, const void* d, int Bq, int Bd, int V, float inv_t, float w_ce,
                 float w_l1, float w_fl, float* out, float* probs, float* ws, hipStream_t st) {
@@ -745,8 +958,19 @@ static void fwd(const void* q, const void* d, int Bq, int Bd, int V, float inv_t
   if (Bd > 0) {
     const ScorePlan p = score_plan(Bq, Bd, V);
     S = spart + (size_t)p.nchunk * Bq * Bd;
-    hipLaunchKernelGGL((loss_score_kernel<T>), dim3((unsigned)p.tiles, (unsigned)p.nchunk), dim3(NT), 0,
-                       st, (const T*)q, (const T*)d, Bq, Bd, V, p.chunk, spart);
+    const dim3 grid((unsigned)p.tiles, (unsigned)p.nchunk);
+    if constexpr (sizeof(T) == 2) {
+      if (mfma16_on()) {
+        hipLaunchKernelGGL((loss_score16_kernel<T>), grid, dim3(NT), 0, st, (const T*)q, (const T*)d,
+                           Bq, Bd, V, p.chunk, spart);
+      } else {
+        hipLaunchKernelGGL((loss_score_kernel<T>), grid, dim3(NT), 0, st, (const T*)q, (const T*)d,
+                           Bq, Bd, V, p.chunk, spart);
+      }
+    } else {
+      hipLaunchKernelGGL((loss_score_kernel<T>), grid, dim3(NT), 0, st, (const T*)q, (const T*)d,
+                         Bq, Bd, V, p.chunk, spart);
+    }
     const int K = Bq * Bd;
     hipLaunchKernelGGL(loss_slice_sum_kernel, dim3((unsigned)cdiv(K, 64)), dim3(64 * SUM_WAVES), 0, st,
                        (const float*)spart, p.nchunk, K, S);
@@ -769,8 +993,16 @@ static void fwd(const void* q, const void* d, int Bq, int Bd, int V, float inv_t
 template <typename T>
 static void bwd(const void* q, const void* d, const float* P, const Grads6& g, int Bq, int Bd, int V,
                 float w_ce, float w_l1, float w_fl, void* gq, void* gd, hipStream_t st) {
-  hipLaunchKernelGGL((loss_bwd_large_kernel<T>), dim3((unsigned)cdiv(V, NC)), dim3(NT), 0, st,
-                     (const T*)q, (const T*)d, P, g, Bq, Bd, V, w_ce, w_l1, w_fl, (T*)gq, (T*)gd);
+  const dim3 grid((unsigned)cdiv(V, NC));
+  if constexpr (std::is_same<T, bf16>::value) {
+    if (mfma16_on()) {
+      hipLaunchKernelGGL((loss_bwd_large_kernel<T, true>), grid, dim3(NT), 0, st, (const T*)q,
+                         (const T*)d, P, g, Bq, Bd, V, w_ce, w_l1, w_fl, (T*)gq, (T*)gd);
+      return;
+    }
+  }
+  hipLaunchKernelGGL((loss_bwd_large_kernel<T, false>), grid, dim3(NT), 0, st, (const T*)q,
+                     (const T*)d, P, g, Bq, Bd, V, w_ce, w_l1, w_fl, (T*)gq, (T*)gd);
 }
 }  // namespace big
 

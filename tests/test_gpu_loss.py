@@ -94,9 +94,9 @@ LARGE_CASES = [  # dtype, Bq, Bd, V
 
 @pytest.mark.parametrize("dt,Bq,Bd,V", LARGE_CASES, ids=[f"{c[0]}-{c[1]}x{c[2]}-V{c[3]}" for c in LARGE_CASES])
 def test_loss_large_batches_match_oracle(dt, Bq, Bd, V, device):
-    """More than 128 rows on a side: the GEMM kernels on the fp32 matrix cores (split-vocabulary
-    score GEMM, per-slice statistics, row softmax; a backward that forms both gradients tile
-    by tile). Values and gradients against the float64 oracle, weighting the six terms as the
+    """More than 128 rows on a side: the GEMM kernels (split-vocabulary score GEMM, per-slice
+    statistics, row softmax; a backward that forms both gradients tile by tile), on the bf16 /
+    fp16 matrix cores for 16-bit reps and the fp32 ones for fp32 reps. Values and gradients against the float64 oracle, weighting the six terms as the
     kernel test does, through splade_loss (the eager C++ op) and the single-term functions."""
     say(f"loss large batch {dt} Bq={Bq} Bd={Bd} V={V}")
     T, w_l1, w_fl = 0.5, 1e-2, 1e-3
@@ -120,6 +120,32 @@ def test_loss_large_batches_match_oracle(dt, Bq, Bd, V, device):
     np.testing.assert_allclose(sl.l1_regularization(qd).item(), want[2], rtol=1e-4)
     np.testing.assert_allclose(sl.flops_regularization(qd).item(), want[4], rtol=1e-4)
     say(f"  total {res.total.item():.6f} (oracle {want[0]:.6f})")
+
+
+@pytest.mark.parametrize("dt,Bq,Bd,V", [("bf16", 300, 400, 5000), ("fp16", 130, 257, 3001),
+                                         ("bf16", 1, 129, 64)])
+def test_loss_large_batch_16bit_mfma_matches_fp32_mfma(dt, Bq, Bd, V, device, monkeypatch):
+    """16-bit reps: the score GEMM on the 16-bit MFMA (exact products) and, for bf16, the
+    gradients' products with P in two bf16 parts, against the same kernels on the fp32 MFMA
+    (SPARTON_LOSS_MFMA16=0): the six terms within fp32 summation-order differences, the
+    gradients within one rounding of the reps' dtype."""
+    say(f"loss large batch 16-bit MFMA vs fp32 MFMA {dt} Bq={Bq} Bd={Bd} V={V}")
+    q = reps_like(Bq, V, dt, seed=7).to(device)
+    d = reps_like(Bd, V, dt, seed=8).to(device)
+    out = []
+    for mode in ("1", "0"):
+        monkeypatch.setenv("SPARTON_LOSS_MFMA16", mode)
+        qs, ds = q.clone().requires_grad_(), d.clone().requires_grad_()
+        res = sl.splade_loss(qs, ds, 0.6, 1e-3, 1e-3)
+        (res.total + 0.5 * res.contrastive).backward()
+        torch.cuda.synchronize()
+        out.append((torch.stack(list(res)).detach().double(), qs.grad.float(), ds.grad.float()))
+    (s16, gq16, gd16), (s32, gq32, gd32) = out
+    torch.testing.assert_close(s16, s32, rtol=1e-5, atol=1e-7)
+    tol = {"bf16": 2 ** -7, "fp16": 2 ** -10}[dt]
+    for a, b in ((gq16, gq32), (gd16, gd32)):
+        scale = b.abs().max().item() + 1e-30
+        assert (a - b).abs().max().item() <= tol * scale, (a - b).abs().max().item() / scale
 
 
 def test_loss_large_batch_deterministic_and_paths_agree(device):
