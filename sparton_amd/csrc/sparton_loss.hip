@@ -731,27 +731,42 @@ __device__ __forceinline__ void split_bf16(float p, uint16_t& hi, uint16_t& lo) 
   lo = bits16((bf16)(p - (float)h));
 }
 
-// grad_tile for bf16 reps: A (P rows or columns) as two bf16 parts, B = the bf16 rows of R or Q.
-template <bool A_KC>
-__device__ __forceinline__ void grad_tile16(uint16_t* sAh, uint16_t* sAl, uint16_t* sB,
-                                            const float* __restrict__ P, int Bq, int Bd,
-                                            const bf16* __restrict__ Bsrc, int K,
-                                            const bf16* __restrict__ X, int rows, int m0, int c0,
-                                            int V, float c_ce, float c_s, float c_f,
-                                            const float* colsum, bf16* __restrict__ G) {
-  const int t = threadIdx.x, wave = t >> 6, lane = t & 63, l32 = lane & 31, h = lane >> 5;
-  f32x16 acc[2] = {zero16(), zero16()};
-  if (K > 0) {
-    float pa[16];
-    bf16 rbv[KS * NC / NT];
-    auto load_a = [&](int k0) {
-      if (A_KC) load_kc(P, Bd, m0, Bq, k0, K, pa);          // A[m][k] = P[m0 + m][k]
-      else load_nc<float, TM>(P, Bd, k0, K, m0, Bd, pa);    // A[m][k] = P[k][m0 + m]
-    };
-    load_a(0);
-    load_nc<bf16, NC>(Bsrc, V, 0, K, c0, V, rbv);
-    for (int k0 = 0; k0 < K; k0 += KS) {
-      __syncthreads();
+// ---- bf16 gradients as one tiled GEMM grid ----
+//
+// Both gradients are GEMMs over the other side's rows plus per-element terms:
+//   dQ = c_ce P R + ...  (K = Bd),   dR = c_ce P^T Q + ...  (K = Bq).
+// A workgroup owns GC columns and row tile t of both (dQ rows and dR rows 128 t ..
+// 128 t + 127; either may be empty), four waves of 64 x 64 per tile. The dQ GEMM streams
+// all of R's rows for its columns, so it also sums R's columns (the FLOPS term of dR), and
+// the dR GEMM sums Q's (that of dQ); a workgroup with only one of the tiles streams the
+// other side for its sums alone. No workspace: everything stays in the workgroup.
+constexpr int GC = 128;
+
+// One GEMM tile: acc += A B^T over k in [0, K), A = P rows m0.. (A_KC) or P columns m0..,
+// B = X[k][c0 ..] (bf16). cs accumulates thread t's share of X's column sums (column
+// t % GC, k rows of parity t / GC). With MM false only the sums are taken.
+template <bool A_KC, bool MM>
+__device__ __forceinline__ void gemm16(uint16_t* sAh, uint16_t* sAl, uint16_t* sB,
+                                       const float* __restrict__ P, int Bq, int Bd,
+                                       const bf16* __restrict__ X, int K, int m0, int c0, int V,
+                                       f32x16 (&acc)[2][2], float& cs) {
+  const int t = threadIdx.x, wave = t >> 6, l32 = t & 31, wm = wave >> 1, wn = wave & 1;
+  if (K <= 0) return;
+  float pa[16];
+  bf16 rbv[KS * GC / NT];
+  auto load = [&](int k0) {
+    if (MM) {
+      if (A_KC) load_kc(P, Bd, m0, Bq, k0, K, pa);         // A[m][k] = P[m0 + m][k]
+      else load_nc<float, TM>(P, Bd, k0, K, m0, Bd, pa);   // A[m][k] = P[k][m0 + m]
+    }
+    load_nc<bf16, GC>(X, V, k0, K, c0, V, rbv);            // B[n][k] = X[k][c0 + n]
+  };
+  load(0);
+  for (int k0 = 0; k0 < K; k0 += KS) {
+#pragma unroll
+    for (int u = 0; u < KS * GC / NT; ++u) cs += to_f32(rbv[u]);
+    if (MM) {
+      __syncthreads();  // the previous stage is read
 #pragma unroll
       for (int u = 0; u < 16; ++u) {
         // load_kc: k = t % 32 of rows t / 32 + 8 u; load_nc<TM>: m = t % 128 of k rows t / 128 + 2 u
@@ -763,44 +778,108 @@ __device__ __forceinline__ void grad_tile16(uint16_t* sAh, uint16_t* sAl, uint16
         sAl[m * LDH + k] = lo;
       }
 #pragma unroll
-      for (int u = 0; u < KS * NC / NT; ++u)  // load_nc<NC>: n = t % 64 of k rows t / 64 + 4 u
-        sB[(t % NC) * LDH + t / NC + (NT / NC) * u] = bits16(rbv[u]);
+      for (int u = 0; u < KS * GC / NT; ++u)  // load_nc<GC>: n = t % GC of k rows t / GC + 2 u
+        sB[(t % GC) * LDH + t / GC + (NT / GC) * u] = bits16(rbv[u]);
       __syncthreads();
-      if (k0 + KS < K) {
-        load_a(k0 + KS);
-        load_nc<bf16, NC>(Bsrc, V, k0 + KS, K, c0, V, rbv);
-      }
+    }
+    if (k0 + KS < K) load(k0 + KS);  // the next stage's loads run under this stage's MFMAs
+    if (MM) {
 #pragma unroll
       for (int ks = 0; ks < KS / 16; ++ks) {
-        const u32x4 ah = frag16(sAh, wave * 32 + l32, ks), al = frag16(sAl, wave * 32 + l32, ks);
+        u32x4 ah[2], al[2], b[2];
 #pragma unroll
-        for (int bj = 0; bj < 2; ++bj) {
-          const u32x4 b = frag16(sB, 32 * bj + l32, ks);
-          acc[bj] = Mfma16<bf16>::run(al, b, acc[bj]);
-          acc[bj] = Mfma16<bf16>::run(ah, b, acc[bj]);
+        for (int i = 0; i < 2; ++i) {
+          ah[i] = frag16(sAh, wm * 64 + 32 * i + l32, ks);
+          al[i] = frag16(sAl, wm * 64 + 32 * i + l32, ks);
+        }
+#pragma unroll
+        for (int j = 0; j < 2; ++j) b[j] = frag16(sB, wn * 64 + 32 * j + l32, ks);
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+          for (int j = 0; j < 2; ++j) {
+            acc[i][j] = Mfma16<bf16>::run(al[i], b[j], acc[i][j]);
+            acc[i][j] = Mfma16<bf16>::run(ah[i], b[j], acc[i][j]);
+          }
+      }
+    }
+  }
+}
+
+// G[i][c] = c_ce acc + c_s sign(X[i][c]) + c_f colsum[c] for the tile's rows below `rows`.
+__device__ __forceinline__ void grad16_epilogue(const f32x16 (&acc)[2][2], const bf16* __restrict__ X,
+                                                int rows, int m0, int c0, int V, float c_ce,
+                                                float c_s, float c_f, const float* colsum,
+                                                bf16* __restrict__ G) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, l32 = lane & 31, h = lane >> 5;
+  const int wm = wave >> 1, wn = wave & 1;
+#pragma unroll
+  for (int bj = 0; bj < 2; ++bj) {
+    const int cl = wn * 64 + 32 * bj + l32, c = c0 + cl;
+#pragma unroll
+    for (int bi = 0; bi < 2; ++bi) {
+      bf16 xv[16];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int i = m0 + wm * 64 + 32 * bi + acc_row(r, h);
+        xv[r] = (i < rows && c < V) ? X[(int64_t)i * V + c] : bf16(0.0f);
+      }
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int i = m0 + wm * 64 + 32 * bi + acc_row(r, h);
+        if (i < rows && c < V) {
+          const float x = to_f32(xv[r]);
+          const float sg = x > 0.0f ? 1.0f : (x < 0.0f ? -1.0f : 0.0f);
+          G[(int64_t)i * V + c] = from_f32<bf16>(c_ce * acc[bi][bj][r] + c_s * sg + c_f * colsum[cl]);
         }
       }
     }
   }
+}
+
+__global__ __launch_bounds__(NT) void loss_grad16_kernel(const bf16* __restrict__ Q,
+                                                         const bf16* __restrict__ R,
+                                                         const float* __restrict__ P, const Grads6 g,
+                                                         int Bq, int Bd, int V, float w_ce,
+                                                         float w_l1, float w_fl,
+                                                         bf16* __restrict__ GQ,
+                                                         bf16* __restrict__ GR) {
+  __shared__ __attribute__((aligned(16))) uint16_t sAh[TM * LDH];
+  __shared__ __attribute__((aligned(16))) uint16_t sAl[TM * LDH];
+  __shared__ __attribute__((aligned(16))) uint16_t sB[GC * LDH];
+  __shared__ float csp[2][2][GC];   // [side][k parity][column]
+  __shared__ float colsum[2][GC];
+  const int t = threadIdx.x;
+  const int c0 = blockIdx.x * GC, m0 = blockIdx.y * TM;
+  const bool has_q = m0 < Bq, has_r = m0 < Bd;
+  f32x16 accq[2][2], accr[2][2];
 #pragma unroll
-  for (int bj = 0; bj < 2; ++bj) {
-    const int cl = 32 * bj + l32, c = c0 + cl;
-    bf16 xv[16];
+  for (int i = 0; i < 2; ++i)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int i = m0 + wave * 32 + acc_row(r, h);
-      xv[r] = (i < rows && c < V) ? X[(int64_t)i * V + c] : bf16(0.0f);
+    for (int j = 0; j < 2; ++j) {
+      accq[i][j] = zero16();
+      accr[i][j] = zero16();
     }
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int i = m0 + wave * 32 + acc_row(r, h);
-      if (i < rows && c < V) {
-        const float x = to_f32(xv[r]);
-        const float sg = x > 0.0f ? 1.0f : (x < 0.0f ? -1.0f : 0.0f);
-        G[(int64_t)i * V + c] = from_f32<bf16>(c_ce * acc[bj][r] + c_s * sg + c_f * colsum[cl]);
-      }
-    }
-  }
+  float csq = 0.0f, csr = 0.0f;
+  // dQ streams R (K = Bd): R's column sums for dR
+  if (has_q) gemm16<true, true>(sAh, sAl, sB, P, Bq, Bd, R, Bd, m0, c0, V, accq, csr);
+  else if (has_r) gemm16<true, false>(sAh, sAl, sB, P, Bq, Bd, R, Bd, m0, c0, V, accq, csr);
+  // dR streams Q (K = Bq): Q's column sums for dQ
+  if (has_r) gemm16<false, true>(sAh, sAl, sB, P, Bq, Bd, Q, Bq, m0, c0, V, accr, csq);
+  else if (has_q) gemm16<false, false>(sAh, sAl, sB, P, Bq, Bd, Q, Bq, m0, c0, V, accr, csq);
+  csp[0][t / GC][t % GC] = csq;
+  csp[1][t / GC][t % GC] = csr;
+  __syncthreads();
+  if (t < 2 * GC) colsum[t / GC][t % GC] = csp[t / GC][0][t % GC] + csp[t / GC][1][t % GC];
+  __syncthreads();
+  const float g0 = grad_of(g, 0);
+  const float c_ce = g0 * w_ce + grad_of(g, 1);
+  const float c_sq = (g0 * w_l1 + grad_of(g, 2)) / (float)Bq;
+  const float c_sd = Bd > 0 ? (g0 * w_l1 + grad_of(g, 3)) / (float)Bd : 0.0f;
+  const float c_fq = 2.0f * (g0 * w_fl + grad_of(g, 4)) / (float)V;
+  const float c_fd = 2.0f * (g0 * w_fl + grad_of(g, 5)) / (float)V;
+  if (has_q) grad16_epilogue(accq, Q, Bq, m0, c0, V, c_ce, c_sq, c_fq, colsum[0], GQ);
+  if (has_r) grad16_epilogue(accr, R, Bd, m0, c0, V, c_ce, c_sd, c_fd, colsum[1], GR);
 }
 
 // 128 rows of one gradient over the workgroup's 64 columns: acc = sum_k A[m][k] B[k][n] with A
@@ -860,13 +939,14 @@ __device__ __forceinline__ void grad_tile(float* sA, float* sB, const float* __r
   }
 }
 
-// M16: bf16 reps, the products on bf16 MFMAs (P in two parts); else the fp32 MFMA.
-template <typename T, bool M16>
+template <typename T>
 __global__ __launch_bounds__(NT) void loss_bwd_large_kernel(const T* __restrict__ Q, const T* __restrict__ R,
                                                             const float* __restrict__ P, const Grads6 g,
                                                             int Bq, int Bd, int V, float w_ce, float w_l1,
                                                             float w_fl, T* __restrict__ GQ,
                                                             T* __restrict__ GR) {
+  __shared__ float sA[KS * LDA];
+  __shared__ float sB[KS * LDB];
   __shared__ float cpart[2][4][NC];
   __shared__ float colsum[2][NC];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -904,24 +984,10 @@ __global__ __launch_bounds__(NT) void loss_bwd_large_kernel(const T* __restrict_
   const float c_sd = Bd > 0 ? (g0 * w_l1 + grad_of(g, 3)) / (float)Bd : 0.0f;
   const float c_fq = 2.0f * (g0 * w_fl + grad_of(g, 4)) / (float)V;
   const float c_fd = 2.0f * (g0 * w_fl + grad_of(g, 5)) / (float)V;
-  if constexpr (M16) {
-    __shared__ __attribute__((aligned(16))) uint16_t sAh[TM * LDH];
-    __shared__ __attribute__((aligned(16))) uint16_t sAl[TM * LDH];
-    __shared__ __attribute__((aligned(16))) uint16_t sB[NC * LDH];
-    for (int i0 = 0; i0 < Bq; i0 += TM)  // dQ = c_ce P R + ...
-      grad_tile16<true>(sAh, sAl, sB, P, Bq, Bd, R, Bd, Q, Bq, i0, c0, V, c_ce, c_sq, c_fq,
-                        colsum[0], GQ);
-    for (int j0 = 0; j0 < Bd; j0 += TM)  // dR = c_ce P^T Q + ...
-      grad_tile16<false>(sAh, sAl, sB, P, Bq, Bd, Q, Bq, R, Bd, j0, c0, V, c_ce, c_sd, c_fd,
-                         colsum[1], GR);
-  } else {
-    __shared__ float sA[KS * LDA];
-    __shared__ float sB[KS * LDB];
-    for (int i0 = 0; i0 < Bq; i0 += TM)  // dQ = c_ce P R + ...
-      grad_tile<T, true>(sA, sB, P, Bq, Bd, R, Bd, Q, Bq, i0, c0, V, c_ce, c_sq, c_fq, colsum[0], GQ);
-    for (int j0 = 0; j0 < Bd; j0 += TM)  // dR = c_ce P^T Q + ...
-      grad_tile<T, false>(sA, sB, P, Bq, Bd, Q, Bq, R, Bd, j0, c0, V, c_ce, c_sd, c_fd, colsum[1], GR);
-  }
+  for (int i0 = 0; i0 < Bq; i0 += TM)  // dQ = c_ce P R + ...
+    grad_tile<T, true>(sA, sB, P, Bq, Bd, R, Bd, Q, Bq, i0, c0, V, c_ce, c_sq, c_fq, colsum[0], GQ);
+  for (int j0 = 0; j0 < Bd; j0 += TM)  // dR = c_ce P^T Q + ...
+    grad_tile<T, false>(sA, sB, P, Bq, Bd, Q, Bq, R, Bd, j0, c0, V, c_ce, c_sd, c_fd, colsum[1], GR);
 }
 
 // Score chunking: about 512 workgroups, chunks of whole LDS stages.
@@ -993,16 +1059,16 @@ static void fwd(const void* q, const void* d, int Bq, int Bd, int V, float inv_t
 template <typename T>
 static void bwd(const void* q, const void* d, const float* P, const Grads6& g, int Bq, int Bd, int V,
                 float w_ce, float w_l1, float w_fl, void* gq, void* gd, hipStream_t st) {
-  const dim3 grid((unsigned)cdiv(V, NC));
   if constexpr (std::is_same<T, bf16>::value) {
     if (mfma16_on()) {
-      hipLaunchKernelGGL((loss_bwd_large_kernel<T, true>), grid, dim3(NT), 0, st, (const T*)q,
-                         (const T*)d, P, g, Bq, Bd, V, w_ce, w_l1, w_fl, (T*)gq, (T*)gd);
+      const dim3 grid((unsigned)cdiv(V, GC), (unsigned)cdiv(std::max(Bq, Bd), TM));
+      hipLaunchKernelGGL(loss_grad16_kernel, grid, dim3(NT), 0, st, (const bf16*)q, (const bf16*)d, P,
+                         g, Bq, Bd, V, w_ce, w_l1, w_fl, (bf16*)gq, (bf16*)gd);
       return;
     }
   }
-  hipLaunchKernelGGL((loss_bwd_large_kernel<T, false>), grid, dim3(NT), 0, st, (const T*)q,
-                     (const T*)d, P, g, Bq, Bd, V, w_ce, w_l1, w_fl, (T*)gq, (T*)gd);
+  hipLaunchKernelGGL((loss_bwd_large_kernel<T>), dim3((unsigned)cdiv(V, NC)), dim3(NT), 0, st,
+                     (const T*)q, (const T*)d, P, g, Bq, Bd, V, w_ce, w_l1, w_fl, (T*)gq, (T*)gd);
 }
 }  // namespace big
 
