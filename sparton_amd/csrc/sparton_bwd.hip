@@ -1385,7 +1385,7 @@ constexpr int FEW_THREADS = 64 * FEW_WAVES;
 constexpr int FEW_COLS = 256;                         // columns of D per slice (4 per lane)
 constexpr int FEW_RPW = FEW_ROWS / FEW_WAVES;         // dH rows per wave
 constexpr int FEW_IPW = FEW_TILE / FEW_WAVES;         // dW ids per wave
-constexpr int FEW_IDC = 4;                            // dW ids summed together
+constexpr int FEW_IDC = 8;                            // dW ids summed together
 constexpr int FEW_NJ = FEW_ROWS * FEW_TILE / FEW_THREADS;  // entry rounds: batch rows per wave
 constexpr int FEW_ES_LD = 68;   // bytes per id of the index table: 17 words, odd, so a wave's
                                 // 64 ids fall in 64 different banks
