@@ -399,7 +399,7 @@ constexpr int KS = 32;    // K per LDS stage
 constexpr int LDA = 161;  // floats per k row of a [KS][128] tile
 constexpr int NC = 64;    // backward: vocabulary columns per workgroup
 constexpr int LDB = 97;   // floats per k row of a [KS][64] tile
-constexpr int ST_ROWS = 4;  // stats: rows whose loads are in flight together per wave
+constexpr int ST_ROWS = 32;  // stats: rows whose loads are in flight together per wave
 
 __device__ __forceinline__ f32x16 zero16() {
   f32x16 z;
@@ -536,12 +536,14 @@ __global__ __launch_bounds__(NT) void loss_stats_kernel(const T* __restrict__ Q,
     const int rows = side ? Bd : Bq, o = side ? Bq : 0;
     float cs = 0.0f;
     for (int b0 = wave; b0 < rows; b0 += 4 * ST_ROWS) {  // uniform per wave
+      // every load issued, from clamped indices, before any is used
       T v[ST_ROWS];
 #pragma unroll
-      for (int u = 0; u < ST_ROWS; ++u) {
-        const int b = b0 + 4 * u;
-        v[u] = (b < rows && cv) ? X[(int64_t)b * V + c] : T(0.0f);
-      }
+      for (int u = 0; u < ST_ROWS; ++u)
+        v[u] = X[(int64_t)min(b0 + 4 * u, rows - 1) * V + min(c, V - 1)];
+#pragma unroll
+      for (int u = 0; u < ST_ROWS; ++u)
+        if (!(b0 + 4 * u < rows && cv)) v[u] = T(0.0f);
 #pragma unroll
       for (int u = 0; u < ST_ROWS; ++u) {
         const int b = b0 + 4 * u;
@@ -962,10 +964,11 @@ __global__ __launch_bounds__(NT) void loss_bwd_large_kernel(const T* __restrict_
       for (int b0 = wave; b0 < rows; b0 += 4 * ST_ROWS) {
         T v[ST_ROWS];
 #pragma unroll
-        for (int u = 0; u < ST_ROWS; ++u) {
-          const int b = b0 + 4 * u;
-          v[u] = (b < rows && cv) ? X[(int64_t)b * V + c] : T(0.0f);
-        }
+        for (int u = 0; u < ST_ROWS; ++u)
+          v[u] = X[(int64_t)min(b0 + 4 * u, rows - 1) * V + min(c, V - 1)];
+#pragma unroll
+        for (int u = 0; u < ST_ROWS; ++u)
+          if (!(b0 + 4 * u < rows && cv)) v[u] = T(0.0f);
 #pragma unroll
         for (int u = 0; u < ST_ROWS; ++u) cs += to_f32(v[u]);
       }
