@@ -37,7 +37,7 @@ namespace loss {
 constexpr int SLICE = 64;            // vocabulary columns per workgroup, one per lane
 constexpr int NWAVES = 4;
 constexpr int NT = 64 * NWAVES;
-constexpr int MAX_B = 128;           // rows of Q and of R
+constexpr int MAX_B = 64;            // rows of Q and of R (past it the GEMM kernels are faster)
 constexpr int LD = SLICE + 4;        // LDS row stride (floats) of a staged slice
 constexpr int SUM_WAVES = 16;        // slice reduction: 64 entries x 16 waves per workgroup
 
@@ -46,23 +46,26 @@ __host__ __device__ constexpr int round4(int x) { return (x + 3) & ~3; }
 // Rows [0, Bq) of Q then [0, Bd) of R, columns [c0, c0 + 64), as fp32 into sq / sd, zeros past
 // V and in the padding rows up to a multiple of 4. Wave w stages rows w, w + 4, ...; lane l
 // column c0 + l (one 128-byte segment per row for 16-bit types). All of a wave's loads are
-// issued before the first is used, so they share one round trip. Then row_fn(isq, row, x)
-// runs for every real row with the lane's value (wave-uniform control flow).
+// issued before the first is used, so they share one round trip: every lane loads from a
+// clamped, valid address and the values of padding rows and columns past V are replaced by
+// zeros afterwards (a load under a per-lane condition is waited for before the next one is
+// issued). Bq >= 1, and R is read only when Bd > 0. Then row_fn(isq, row, x) runs for every
+// real row with the lane's value (wave-uniform control flow).
 template <typename T, int MB, typename F>
 __device__ __forceinline__ void stage_slice(const T* __restrict__ Q, const T* __restrict__ R, int Bq,
                                             int Bd, int V, int c0, float* sq, float* sd, F row_fn) {
   constexpr int RPW = 2 * MB / NWAVES;  // rows per wave at most (Q and R padded to MB each)
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int c = c0 + lane;
+  const int cl = min(c, V - 1);
   const int Bqp = round4(Bq), Bdp = round4(Bd);
   T raw[RPW];
 #pragma unroll
   for (int k = 0; k < RPW; ++k) {
     const int r = wave + k * NWAVES;
-    const bool isq = r < Bqp;
-    const int row = isq ? r : r - Bqp;
-    const bool real = r < Bqp + Bdp && row < (isq ? Bq : Bd) && c < V;
-    raw[k] = real ? (isq ? Q : R)[(size_t)row * V + c] : T(0.0f);
+    const bool isq = r < Bqp || Bd == 0;
+    const int row = isq ? min(r, Bq - 1) : min(r - Bqp, Bd - 1);
+    raw[k] = (isq ? Q : R)[(size_t)row * V + cl];
   }
 #pragma unroll
   for (int k = 0; k < RPW; ++k) {
@@ -70,6 +73,7 @@ __device__ __forceinline__ void stage_slice(const T* __restrict__ Q, const T* __
     if (r >= Bqp + Bdp) break;
     const bool isq = r < Bqp;
     const int row = isq ? r : r - Bqp;
+    if (!(row < (isq ? Bq : Bd) && c < V)) raw[k] = T(0.0f);
     const float x = to_f32(raw[k]);
     (isq ? sq : sd)[row * LD + lane] = x;
     if (row < (isq ? Bq : Bd)) row_fn(isq, row, x);
@@ -151,9 +155,9 @@ __global__ __launch_bounds__(64 * SUM_WAVES) void loss_slice_sum_kernel(const fl
     for (int s0 = beg; s0 < end; s0 += 8) {
       float v[8];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) v[j] = s0 + j < end ? part[(size_t)(s0 + j) * K + k] : 0.0f;
+      for (int j = 0; j < 8; ++j) v[j] = part[(size_t)min(s0 + j, end - 1) * K + k];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) acc += v[j];
+      for (int j = 0; j < 8; ++j) acc += s0 + j < end ? v[j] : 0.0f;
     }
   }
   wsum[wave][lane] = acc;
@@ -181,8 +185,7 @@ __global__ __launch_bounds__(NT) void loss_final_kernel(const float* __restrict_
     float v[8];
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
-      const int k = k0 + u * NT + threadIdx.x;
-      v[u] = k < n ? sums[k] : 0.0f;
+      v[u] = sums[min(k0 + u * NT + (int)threadIdx.x, n - 1)];
     }
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
@@ -252,14 +255,23 @@ __global__ __launch_bounds__(NT) void loss_bwd_kernel(const T* __restrict__ Q, c
   const int c0 = blockIdx.x * SLICE;
   const int Bqp = round4(Bq), Bdp = round4(Bd);
   // P, zero-padded to Bqp x Bdp: its loads are issued first, so that they are in flight
-  // together with the slice's
+  // together with the slice's (clamped addresses, padding zeroed afterwards; P exists only
+  // when Bd > 0)
   constexpr int PPT = MB * MB / NT;  // P entries per thread at most
   float pr[PPT];
+  if (Bdp > 0) {
 #pragma unroll
-  for (int u = 0; u < PPT; ++u) {
-    const int e = u * NT + threadIdx.x;
-    const int i = Bdp > 0 ? e / Bdp : 0, j = e - i * Bdp;
-    pr[u] = (Bdp > 0 && e < Bqp * Bdp && i < Bq && j < Bd) ? P[(size_t)i * Bd + j] : 0.0f;
+    for (int u = 0; u < PPT; ++u) {
+      const int e = u * NT + threadIdx.x;
+      const int i = e / Bdp, j = e - i * Bdp;
+      pr[u] = P[(size_t)min(i, Bq - 1) * Bd + min(j, Bd - 1)];
+    }
+#pragma unroll
+    for (int u = 0; u < PPT; ++u) {
+      const int e = u * NT + threadIdx.x;
+      const int i = e / Bdp, j = e - i * Bdp;
+      if (!(e < Bqp * Bdp && i < Bq && j < Bd)) pr[u] = 0.0f;
+    }
   }
   stage_slice<T, MB>(Q, R, Bq, Bd, V, c0, sq, sd, [](bool, int, float) {});
 #pragma unroll
@@ -361,24 +373,24 @@ static void fwd_partial(const void* q, const void* d, int Bq, int Bd, int V, flo
                         hipStream_t st) {
   const int mb = Bq > Bd ? Bq : Bd;
   if (mb <= 32) launch_fwd<T, 32>(q, d, Bq, Bd, V, part, K, st);
-  else if (mb <= 64) launch_fwd<T, 64>(q, d, Bq, Bd, V, part, K, st);
-  else launch_fwd<T, 128>(q, d, Bq, Bd, V, part, K, st);
+  else launch_fwd<T, MAX_B>(q, d, Bq, Bd, V, part, K, st);
 }
 template <typename T>
 static void bwd_all(const void* q, const void* d, const float* P, const Grads6& g, int Bq, int Bd,
                     int V, float w_ce, float w_l1, float w_fl, void* gq, void* gd, hipStream_t st) {
   const int mb = Bq > Bd ? Bq : Bd;
   if (mb <= 32) launch_bwd<T, 32>(q, d, P, g, Bq, Bd, V, w_ce, w_l1, w_fl, gq, gd, st);
-  else if (mb <= 64) launch_bwd<T, 64>(q, d, P, g, Bq, Bd, V, w_ce, w_l1, w_fl, gq, gd, st);
-  else launch_bwd<T, 128>(q, d, P, g, Bq, Bd, V, w_ce, w_l1, w_fl, gq, gd, st);
+  else launch_bwd<T, MAX_B>(q, d, P, g, Bq, Bd, V, w_ce, w_l1, w_fl, gq, gd, st);
 }
 
 // ---- batches past MAX_B rows ---------------------------------------------------------------
 //
 // The kernels above stage every row of a 64-column slice and keep per-slice partials of all
-// Bq x Bd scores, so they stop at MAX_B rows. Larger batches take GEMM-shaped kernels on the
+// Bq x Bd scores; their per-thread work grows with the rows, and past 64 rows a side the
+// kernels below are faster (V 30522, fwd+bwd device time: 96 rows 134 us against 81 us, 128
+// rows 190 against 90; 64 rows 62 against 70). Larger batches take GEMM-shaped kernels on the
 // fp32 matrix cores (v_mfma_f32_32x32x2f32: the products of any reps dtype are exact in fp32,
-// and the sums accumulate in fp32, as above):
+// and the sums accumulate in fp32, as above; 16-bit reps have the variants further down):
 //   forward   loss_stats_kernel   per 64-column slice: each row's sum of |x| over the slice,
 //                                 and sum_v (sum_b x)^2 of Q and of R;
 //             loss_score_kernel   S = Q R^T in 128 x 128 tiles, the vocabulary split into

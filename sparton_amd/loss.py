@@ -17,7 +17,7 @@ runs in the reps dtype), deterministically. Device tensors only, like the head.
         -> (out[6] fp32 = (total, CE, L1 q, L1 d, FLOPS q, FLOPS d), probs [Bq, Bd] fp32)
     sparton::splade_loss_bwd(grad_out[6], q, d?, probs, w_ce, w_l1, w_flops) -> (dq, dd)
 
-Batches of up to 128 rows on each side take the slice-staged kernels above. Larger batches
+Batches of up to 64 rows on each side take the slice-staged kernels above. Larger batches
 take GEMM-shaped HIP kernels on the fp32 matrix cores: a split-vocabulary score GEMM with a
 fixed-order sum of its partials, per-slice row and column statistics, a row softmax, and a
 backward that recomputes each vocabulary slice's column sums and forms both gradients tile by

@@ -364,7 +364,7 @@ def test_loss_workspace_size():
     assert L.sparton_loss_workspace_bytes(32, 32, 30522) == (477 + 1) * (1024 + 64 + 2) * 4
     assert L.sparton_loss_workspace_bytes(4, 0, 64) == 2 * (4 + 2) * 4
     assert L.sparton_loss_workspace_bytes(0, 4, 64) == 0
-    # past 128 rows: 16 score tiles of 128 x 128 -> 32 vocabulary chunks of 960 columns, one
+    # past 64 rows: 16 score tiles of 128 x 128 -> 32 vocabulary chunks of 960 columns, one
     # partial S each, S itself, per-slice row/column statistics plus their sums, and Bq row
     # CE terms
     assert L.sparton_loss_workspace_bytes(512, 512, 30522) == (
