@@ -76,11 +76,13 @@ template <typename T> using vec4_t = typename Vec4<T>::type;
 
 template <bool FULL>
 __device__ __forceinline__ bool in_row(int d, int D) { return FULL || d < D; }
+// Past the row end a lane loads the row's last group instead (D >= 4): every load is
+// unconditional, so a wave's loads are in flight together (a load under a per-lane condition,
+// or one whose value is selected right away, is waited for before the next is issued). The
+// values past the row end are not zeros: every use masks them with in_row.
 template <typename T, bool FULL>
 __device__ __forceinline__ vec4_t<T> load4(const T* p, int d, int D) {
-  vec4_t<T> v = {};
-  if (in_row<FULL>(d, D)) v = *(const vec4_t<T>*)(p + d);
-  return v;
+  return *(const vec4_t<T>*)(p + (FULL ? d : min(d, D - 4)));
 }
 template <typename T>
 __device__ __forceinline__ f32x4 to_f32(vec4_t<T> v) {
@@ -100,7 +102,7 @@ __device__ __forceinline__ void store4t(T* p, int d, int D, f32x4 v) {
 }
 template <bool FULL>
 __device__ __forceinline__ f32x4 load4p(const float* p, int d, int D) {
-  return in_row<FULL>(d, D) ? *(const f32x4*)(p + d) : f32x4{0.f, 0.f, 0.f, 0.f};
+  return *(const f32x4*)(p + (FULL ? d : min(d, D - 4)));
 }
 
 // ---- forward epilogue: one wave per row ------------------------------------------------
@@ -236,7 +238,7 @@ __global__ __launch_bounds__(BwdCfg<NP>::threads) void xf_bwd_kernel(
         const float zb = zz[e] + bb[e];
         const float cdf = norm_cdf(zb);
         const float x = in_row<FULL>(d, D) ? (zb * cdf - mu) * rs : 0.0f;
-        const float g = dy[e] * ga[e];
+        const float g = in_row<FULL>(d, D) ? dy[e] * ga[e] : 0.0f;
         s1 += g;
         s2 += g * x;
         pg[p][e] += dy[e] * x;
@@ -319,9 +321,9 @@ __global__ __launch_bounds__(64 * COL_WAVES) void xf_colsum_kernel(const float* 
     for (int k0 = beg; k0 < end; k0 += 8) {
       float v[8];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) v[j] = k0 + j < end ? part[(size_t)(k0 + j) * ncol + col] : 0.0f;
+      for (int j = 0; j < 8; ++j) v[j] = part[(size_t)min(k0 + j, end - 1) * ncol + col];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) acc += v[j];
+      for (int j = 0; j < 8; ++j) acc += k0 + j < end ? v[j] : 0.0f;
     }
   }
   wsum[wave][lane] = acc;
