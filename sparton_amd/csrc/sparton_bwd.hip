@@ -712,7 +712,9 @@ __device__ __forceinline__ void entries_n(const T* grad, const RT* reps, const i
 
 // ---- 5. dW and dbias -------------------------------------------------------------
 // One wave per vocab row v: lanes hold batch rows b (64 per pass), a ballot lists the
-// active ones, and their H rows are gathered in ascending b, two at a time.
+// active ones, and their H rows are gathered in ascending b, two at a time. Lanes past the
+// row end load the row's last group (D >= 4 whenever D > 0), so the loads carry no per-lane
+// condition and are in flight together; those lanes' sums are never stored.
 template <typename T, typename O, int NP, typename RT>
 __global__ __launch_bounds__(256) void bwd_dw_kernel(
     const T* __restrict__ grad, const RT* __restrict__ reps,
@@ -748,21 +750,23 @@ __global__ __launch_bounds__(256) void bwd_dw_kernel(
           const float g1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(g), l1));
           const T* h1 = H + ((int64_t)(b0 + l1) * S + s1) * D;
           bsum += g1;
-          f32x4 x0[NP], x1[NP];
+          if (D > 0) {  // (H may be null without columns)
+            f32x4 x0[NP], x1[NP];
 #pragma unroll
-          for (int p = 0; p < NP; ++p) {
-            const int d = d0 + p * 256 + lane * 4;
-            x0[p] = d < D ? load4(h0 + d) : f32x4{0.f, 0.f, 0.f, 0.f};
-            x1[p] = d < D ? load4(h1 + d) : f32x4{0.f, 0.f, 0.f, 0.f};
+            for (int p = 0; p < NP; ++p) {
+              const int d = min(d0 + p * 256 + lane * 4, D - 4);
+              x0[p] = load4(h0 + d);
+              x1[p] = load4(h1 + d);
+            }
+#pragma unroll
+            for (int p = 0; p < NP; ++p) acc[p] += g0 * x0[p] + g1 * x1[p];
           }
+        } else if (D > 0) {
+          f32x4 x0[NP];
 #pragma unroll
-          for (int p = 0; p < NP; ++p) acc[p] += g0 * x0[p] + g1 * x1[p];
-        } else {
+          for (int p = 0; p < NP; ++p) x0[p] = load4(h0 + min(d0 + p * 256 + lane * 4, D - 4));
 #pragma unroll
-          for (int p = 0; p < NP; ++p) {
-            const int d = d0 + p * 256 + lane * 4;
-            if (d < D) acc[p] += g0 * load4(h0 + d);
-          }
+          for (int p = 0; p < NP; ++p) acc[p] += g0 * x0[p];
         }
       }
     }
@@ -800,7 +804,7 @@ constexpr int DW_WAVES = 16;
 constexpr int DW_LD = DW_STAGE_B + 1;  // odd row stride: conflict-free column and row access
 constexpr int DW_STAGE_S = 1 << 16;
 
-template <typename T, typename RT, int NIDS, int NW>
+template <typename T, typename RT, int NIDS, int NW, int LD = DW_LD>
 __device__ __forceinline__ void dw_stage(float* gl, uint16_t* sl, const T* __restrict__ grad,
                                          const RT* __restrict__ reps,
                                          const int32_t* __restrict__ idx,
@@ -817,14 +821,14 @@ __device__ __forceinline__ void dw_stage(float* gl, uint16_t* sl, const T* __res
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       if (bs[i] < B) {
-        gl[idl * DW_LD + bs[i]] = g[i];
-        sl[idl * DW_LD + bs[i]] = (uint16_t)s[i];
+        gl[idl * LD + bs[i]] = g[i];
+        sl[idl * LD + bs[i]] = (uint16_t)s[i];
       }
     }
   }
 }
 
-template <typename T, typename O, int NP, typename RT, int NIDS, int NW>
+template <typename T, typename O, int NP, typename RT, int NIDS, int NW, int LD = DW_LD>
 __device__ __forceinline__ void dw_gather(const float* gl, const uint16_t* sl,
                                           const T* __restrict__ H, O* __restrict__ dW,
                                           O* __restrict__ dbias, int B, int S, int D, int V,
@@ -858,8 +862,8 @@ __device__ __forceinline__ void dw_gather(const float* gl, const uint16_t* sl,
         for (int i = 0; i < IDC; ++i) {
           const int vl = wave * IDS + i0 + i;
           const bool in = bb < B && v0 + vl < V;
-          g[i] = in ? gl[vl * DW_LD + bb] : 0.0f;
-          s[i] = in ? (int)sl[vl * DW_LD + bb] : 0;
+          g[i] = in ? gl[vl * LD + bb] : 0.0f;
+          s[i] = in ? (int)sl[vl * LD + bb] : 0;
           pend[i] = __ballot(g[i] != 0.0f);
           left += __popcll(pend[i]);
         }
@@ -943,6 +947,28 @@ __global__ __launch_bounds__(64 * DW_WAVES) void bwd_dw_staged_kernel(
   dw_stage<T, RT, 64, DW_WAVES>(gl, sl, grad, reps, idx, mask, mdt, B, S, V, v0, wave, lane);
   __syncthreads();
   dw_gather<T, O, NP, RT, 64, DW_WAVES>(gl, sl, H, dW, dbias, B, S, D, V, v0, wave, lane);
+}
+
+// dW / dbias for DW_STAGE_B < B <= DW_WIDE_B and S <= DW_STAGE_S: the staged kernel with
+// fewer ids per workgroup, so that every batch row of them fits LDS (NIDS ids x (ROWS + 1)
+// x 6 bytes, ~99 KB: 64 ids up to 256 rows, 32 up to 512, 16 up to 1024). The rows are
+// staged once and each id sums its rows in ascending b, as above.
+constexpr int DW_WIDE_IDS_ROWS = 16384;  // NIDS x ROWS
+constexpr int DW_WIDE_B = 1024;
+template <typename T, typename O, int NP, typename RT, int NIDS>
+__global__ __launch_bounds__(64 * DW_WAVES) void bwd_dw_wide_kernel(
+    const T* __restrict__ grad, const RT* __restrict__ reps,
+    const int32_t* __restrict__ idx, const void* __restrict__ mask, int mdt,
+    const T* __restrict__ H, O* __restrict__ dW, O* __restrict__ dbias, int B, int S, int D,
+    int V) {
+  constexpr int LD = DW_WIDE_IDS_ROWS / NIDS + 1;  // odd: conflict-free
+  __shared__ float gl[NIDS * LD];
+  __shared__ uint16_t sl[NIDS * LD];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int v0 = blockIdx.x * NIDS;
+  dw_stage<T, RT, NIDS, DW_WAVES, LD>(gl, sl, grad, reps, idx, mask, mdt, B, S, V, v0, wave, lane);
+  __syncthreads();
+  dw_gather<T, O, NP, RT, NIDS, DW_WAVES, LD>(gl, sl, H, dW, dbias, B, S, D, V, v0, wave, lane);
 }
 
 // dH and the staged dW in one launch, for the five-kernel path when it makes one pass
@@ -1682,6 +1708,24 @@ static bool fused_path_enabled() {
   return e == nullptr || strcmp(e, "five") != 0;
 }
 
+// The wide staged dW with 16 ids per workgroup (B <= DW_WIDE_B), for 16-bit types: fp32
+// rows gather two ids at a time, which 16 ids over 16 waves cannot give. Returns whether it
+// launched.
+template <typename T, typename O, int DNP, typename RT>
+static bool wide16(const T* g, const RT* r, const int32_t* idx, const void* mask, int mdt,
+                   const T* H, O* dW, O* dbias, int64_t B, int64_t S, int64_t D, int64_t V,
+                   hipStream_t st) {
+  if constexpr (sizeof(T) == 2) {
+    if (B <= DW_WIDE_B && S <= DW_STAGE_S) {
+      hipLaunchKernelGGL((bwd_dw_wide_kernel<T, O, DNP, RT, 16>), dim3((unsigned)cdiv(V, 16)),
+                         dim3(64 * DW_WAVES), 0, st, g, r, idx, mask, mdt, H, dW, dbias, (int)B,
+                         (int)S, (int)D, (int)V);
+      return true;
+    }
+  }
+  return false;
+}
+
 template <typename T, typename O, int NP, typename RT>
 static void launch_rows(const T* g, const RT* r, const int32_t* idx, const void* mask,
                         int mdt, const T* H, const T* W, O* dH, O* dW, O* dbias, void* ws,
@@ -1836,11 +1880,20 @@ static void launch_rows(const T* g, const RT* r, const int32_t* idx, const void*
     }
   }
   if ((dW != nullptr || dbias != nullptr) && V > 0 && !merged_dw) {
+    constexpr int DNP = DwPasses<T, NP>::value;
     if (B <= DW_STAGE_B && S <= DW_STAGE_S)
-      hipLaunchKernelGGL((bwd_dw_staged_kernel<T, O, DwPasses<T, NP>::value, RT>),
+      hipLaunchKernelGGL((bwd_dw_staged_kernel<T, O, DNP, RT>),
                          dim3((unsigned)cdiv(V, 64)), dim3(64 * DW_WAVES), 0,
                          st, g, r, idx, mask, mdt, H, dW, dbias, (int)B, (int)S, (int)D, (int)V);
-    else
+    else if (B <= DW_WIDE_IDS_ROWS / 64 && S <= DW_STAGE_S)
+      hipLaunchKernelGGL((bwd_dw_wide_kernel<T, O, DNP, RT, 64>), dim3((unsigned)cdiv(V, 64)),
+                         dim3(64 * DW_WAVES), 0, st, g, r, idx, mask, mdt, H, dW, dbias, (int)B,
+                         (int)S, (int)D, (int)V);
+    else if (B <= DW_WIDE_IDS_ROWS / 32 && S <= DW_STAGE_S)
+      hipLaunchKernelGGL((bwd_dw_wide_kernel<T, O, DNP, RT, 32>), dim3((unsigned)cdiv(V, 32)),
+                         dim3(64 * DW_WAVES), 0, st, g, r, idx, mask, mdt, H, dW, dbias, (int)B,
+                         (int)S, (int)D, (int)V);
+    else if (!wide16<T, O, DNP, RT>(g, r, idx, mask, mdt, H, dW, dbias, B, S, D, V, st))
       hipLaunchKernelGGL((bwd_dw_kernel<T, O, NP, RT>), dim3((unsigned)cdiv(V, 4)), dim3(256), 0, st,
                          g, r, idx, mask, mdt, H, dW, dbias, (int)B, (int)S, (int)D, (int)V);
   }

@@ -79,7 +79,11 @@ CASES = [
     ("fp16", 3, 130, 24, 520, True, "int64"),   # rows shorter than one slab, 3 vocab tiles
     ("bf16", 3, 900, 64, 2100, True, "gaps"),   # fully masked middle chunk, masked row
     ("bf16", 37, 40, 64, 700, True, "int64"),   # many short rows: several rows per row tile
-    ("fp32", 130, 3, 16, 70, True, "int64"),    # B > 128: the unstaged dW path
+    ("fp32", 130, 3, 16, 70, True, "int64"),    # B > 128: staged dW, 64 ids per workgroup
+    ("fp32", 300, 4, 40, 333, True, "holes"),   # B > 256: staged dW, 32 ids per workgroup
+    ("bf16", 250, 6, 264, 500, False, "frac"),  # staged dW, 64 ids, two passes with a tail
+    ("fp16", 1024, 2, 8, 50, True, "bool"),     # B = 1024: staged dW, 16 ids per workgroup
+    ("fp32", 700, 3, 16, 90, True, "int64"),    # fp32 B > 512: the unstaged dW path
     ("bf16", 100, 24, 64, 900, True, "frac"),   # 64 < B <= 128: staged dW, two batch passes
     ("bf16", 8, 3000, 64, 700, True, "gaps"),   # B*S > 16384: plan with the mask in global memory
     ("fp16", 1100, 8, 16, 200, True, "int64"),  # more groups than plan threads
