@@ -172,16 +172,21 @@ def cpu_baseline(torch, w, inp, budget_s):
         fn()
         return time.perf_counter() - t0
 
-    # Size the sample so that about 5 timed steps fill the budget.
+    # Size the sample so that about 5 timed steps fill the budget; when the whole batch takes
+    # less, repeat it so that the timed steps fill about 60% of the budget and the timed
+    # forwards about 20% (at least 5 of each, at most 50).
     prepare(1)
     timed()  # first call pays one-time costs
     per_row = timed()
     rows = max(1, min(w.B, int(budget_s / (5 * per_row))))
     prepare(rows)
-    timed()  # warm-up at the final size
-    times = [timed() for _ in range(5)]
+    t_warm = timed()  # warm-up at the final size
+    reps = max(5, min(50, int(0.6 * budget_s / max(t_warm, 1e-6))))
+    times = [timed() for _ in range(reps)]
     t = statistics.median(times)
-    fwd_times = [timed(fwd) for _ in range(5)]
+    t_fwd_warm = timed(fwd)
+    fwd_reps = max(5, min(50, int(0.2 * budget_s / max(t_fwd_warm, 1e-6))))
+    fwd_times = [timed(fwd) for _ in range(fwd_reps)]
     t_fwd = statistics.median(fwd_times)
     # peak memory of one fwd+bwd step above what the process held before it
     hwm_reset = _reset_peak_rss()
@@ -211,7 +216,8 @@ def cpu_baseline(torch, w, inp, budget_s):
         "fp32_matmul_precision": torch.get_float32_matmul_precision(),
         "sample": (f"torch head (training/model.py:56-62, restated in oracle/) fwd+bwd autograd "
                    f"(value) and fwd alone, {DTYPE_NAME[str(w.dtype)]}, {rows} of {w.B} batch rows "
-                   f"({rows * w.S} tokens), V-chunked by 8192, median of {n} after 1 warm-up; "
+                   f"({rows * w.S} tokens), V-chunked by 8192, median of {n} fwd+bwd steps and of "
+                   f"{len(fwd_times)} forwards, each after 1 warm-up; "
                    f"host CPU: {cpu_model()}"),
     }
 
