@@ -57,6 +57,8 @@ CASES = [
     ("fp32", (9, 64), 2048, 1e-12),    # wide rows, full passes
     ("bf16", (64, 512), 768, 1e-12),   # M = 32768: dW as 16 row chunks
     ("bf16", (16, 512), 1024, 1e-5),   # BERT-large width, dW as 8 row chunks
+    ("fp16", (300,), 1500, 1e-5),      # wide rows, lanes past the row end in the 6th pass
+    ("bf16", (2, 40), 3000, 1e-5),     # widest passes, the last one partial
 ]
 
 
