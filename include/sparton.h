@@ -222,8 +222,9 @@ int sparton_transform_chunk_sum(const float* part, void* out, int64_t C, int64_t
  *   total = w_ce CE + w_l1 (L1(q) + L1(d)) + w_flops (FL(q) + FL(d))   (:196-197)
  * Limits: Bq >= 1, Bd >= 0, Bq <= Bd when Bd > 0 (the labels index d's rows), temperature
  * > 0 and finite when Bd > 0; sizes whose scores or offsets pass the kernels' int range return
- * SPARTON_EUNSUPPORTED. Up to 128 rows per side run slice-staged kernels, larger batches
- * GEMM kernels on the fp32 matrix cores (the workspace size follows). Computed in fp32
+ * SPARTON_EUNSUPPORTED. Up to 64 rows per side run slice-staged kernels, larger batches
+ * tiled GEMM kernels on the matrix cores (16-bit reps on the 16-bit MFMA, whose products are
+ * exact in fp32; fp32 reps on the fp32 MFMA); the workspace size follows. Accumulated in fp32
  * whatever the reps dtype.
  */
 size_t sparton_loss_workspace_bytes(int64_t Bq, int64_t Bd, int64_t V);

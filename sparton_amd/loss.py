@@ -18,7 +18,8 @@ runs in the reps dtype), deterministically. Device tensors only, like the head.
     sparton::splade_loss_bwd(grad_out[6], q, d?, probs, w_ce, w_l1, w_flops) -> (dq, dd)
 
 Batches of up to 64 rows on each side take the slice-staged kernels above. Larger batches
-take GEMM-shaped HIP kernels on the fp32 matrix cores: a split-vocabulary score GEMM with a
+take GEMM-shaped HIP kernels on the matrix cores (16-bit reps on the bf16/fp16 MFMA, whose
+products are exact in fp32; fp32 reps on the fp32 MFMA): a split-vocabulary score GEMM with a
 fixed-order sum of its partials, per-slice row and column statistics, a row softmax, and a
 backward that recomputes each vocabulary slice's column sums and forms both gradients tile by
 tile (sparton_loss.hip). Limits: 1 <= Bq <= Bd when documents are given (the labels
@@ -33,7 +34,7 @@ from torch import Tensor
 
 from . import _eager, _lib
 
-SMALL_MAX_ROWS = 128   # rows per side taken by the slice-staged kernels; larger batches take the GEMM kernels
+SMALL_MAX_ROWS = 64    # rows per side taken by the slice-staged kernels (the library's own rule); larger batches take the GEMM kernels
 _FLOAT_DTYPES = tuple(_lib.DTYPE_CODE)
 
 
