@@ -50,6 +50,7 @@
 
 #include <algorithm>
 #include <mutex>
+#include <type_traits>
 
 #include "sparton_common.h"
 
@@ -463,11 +464,21 @@ template <> struct Mfma<bf16> {
     c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
                                                  __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
   }
+  static __device__ __forceinline__ void run_from(const u32x4& a, const u32x4& b, const f32x16& c,
+                                                  f32x16& d) {
+    d = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                 __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  }
 };
 template <> struct Mfma<f16> {
   static constexpr int kInsts = 1;
   static __device__ __forceinline__ void run(const u32x4& a, const u32x4& b, f32x16& c) {
     c = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
+                                               __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ void run_from(const u32x4& a, const u32x4& b, const f32x16& c,
+                                                  f32x16& d) {
+    d = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
                                                __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
   }
 };
@@ -480,6 +491,14 @@ template <> struct Mfma<float> {
 #pragma unroll
     for (int j = 0; j < 4; ++j)
       c = __builtin_amdgcn_mfma_f32_32x32x2f32(__uint_as_float(a[j]), __uint_as_float(b[j]), c,
+                                               0, 0, 0);
+  }
+  static __device__ __forceinline__ void run_from(const u32x4& a, const u32x4& b, const f32x16& c,
+                                                  f32x16& d) {
+    d = __builtin_amdgcn_mfma_f32_32x32x2f32(__uint_as_float(a[0]), __uint_as_float(b[0]), c, 0, 0, 0);
+#pragma unroll
+    for (int j = 1; j < 4; ++j)
+      d = __builtin_amdgcn_mfma_f32_32x32x2f32(__uint_as_float(a[j]), __uint_as_float(b[j]), d,
                                                0, 0, 0);
   }
 };
@@ -963,14 +982,19 @@ __device__ __forceinline__ void compute_unit(Smem& sm, const UnitMeta& um, int n
                                              int lane, int wm, int wn) {
   constexpr int JA = JM > 0 ? JM : 1;
   const int l32 = lane & 31, h = lane >> 5;
+  // Accumulators start at the bias of their column. Only the last block's are set here: the
+  // unit's first MFMA of every other block takes them as its C operand, so each block still
+  // sums bias + products in the same order, with 32 register moves instead of 16 JA.
   f32x16 acc[JA][NB_PER_WAVE];
 #pragma unroll
   for (int nb = 0; nb < NB_PER_WAVE; ++nb) {
     const float bv = um.bias[wn * 64 + nb * 32 + l32];
 #pragma unroll
-    for (int j = 0; j < JA; ++j)
+    for (int i = 0; i < 16; ++i) acc[JA - 1][nb][i] = bv;
+    if (nk == 0) {  // no MFMAs: x = bias
 #pragma unroll
-      for (int i = 0; i < 16; ++i) acc[j][nb][i] = bv;
+      for (int j = 0; j < JA - 1; ++j) acc[j][nb] = acc[JA - 1][nb];
+    }
   }
 
   // Every operand row is (multiple of 32) + l32, so its swizzle key is key(l32): a
@@ -985,21 +1009,28 @@ __device__ __forceinline__ void compute_unit(Smem& sm, const UnitMeta& um, int n
   // last MFMA that uses it. MFMAs run B-fragment-major, so B fragment 0 frees first,
   // then A fragments 0..JM-1, then B fragment 1.
   u32x4 bf[NB_PER_WAVE], af[JA];
-  // MFMAs of the fragments at hand; rolling reads of K step p of stage st.
-  auto step = [&](int st, int p) {
+  // MFMAs of the fragments at hand; rolling reads of K step p of stage st. With `first`
+  // (the unit's first K step), blocks 0..JM-2 start from block JM-1's bias registers, which
+  // block JM-1 itself overwrites only after them.
+  auto step_x = [&](int st, int p, auto first) {
     const u32x4* an = abase + st * A_STAGE;
     const u32x4* bn = bbase + st * B_STAGE;
     const int cn = chunk(p);
 #pragma unroll
-    for (int j = 0; j < JM; ++j) Mfma<T>::run(af[j], bf[0], acc[j][0]);
+    for (int j = 0; j < JM; ++j) {
+      if (decltype(first)::value && j < JM - 1) Mfma<T>::run_from(af[j], bf[0], acc[JM - 1][0], acc[j][0]);
+      else Mfma<T>::run(af[j], bf[0], acc[j][0]);
+    }
     bf[0] = bn[cn];
 #pragma unroll
     for (int j = 0; j < JM; ++j) {
-      Mfma<T>::run(af[j], bf[1], acc[j][1]);
+      if (decltype(first)::value && j < JM - 1) Mfma<T>::run_from(af[j], bf[1], acc[JM - 1][1], acc[j][1]);
+      else Mfma<T>::run(af[j], bf[1], acc[j][1]);
       af[j] = an[j * WAVES_M * 32 * CHUNKS + cn];
     }
     bf[1] = bn[32 * CHUNKS + cn];
   };
+  auto step = [&](int st, int p) { step_x(st, p, std::false_type{}); };
   // Keep that order: each read right after the MFMA that frees its registers.
   auto order = [&](int steps) {
     constexpr int KI = Mfma<T>::kInsts;
@@ -1024,7 +1055,20 @@ __device__ __forceinline__ void compute_unit(Smem& sm, const UnitMeta& um, int n
   // Software-pipelined over the step barrier: K steps 0..2 of slab k, then B_k, then
   // K step 3 of slab k with the reads of slab k+1's first K step, whose latency the
   // MFMAs hide. (After the last slab those reads fetch stale data, never used.)
-  for (int k = 0; k < nk; ++k) {
+  if (nk > 0) {  // slab 0, peeled: it holds the unit's first MFMAs
+    if (JM > 0) {
+      step_x(buf, 1, std::true_type{});
+#pragma unroll
+      for (int p = 2; p < CHUNKS / 2; ++p) step(buf, p);
+      order(CHUNKS / 2 - 1);
+    }
+    lds_barrier();  // B_0
+    if (JM > 0) {
+      step(buf ^ 1, 0);
+      order(1);
+    }
+  }
+  for (int k = 1; k < nk; ++k) {
     const int cur = buf ^ (k & 1);
     if (JM > 0) {
 #pragma unroll
