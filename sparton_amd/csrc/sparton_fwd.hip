@@ -441,7 +441,8 @@ struct Smem {
   u32x4 a[2][BM * CHUNKS];   // [stage][row * 8 + (chunk ^ f(row))]
   u32x4 b[2][BN * CHUNKS];
   int key[NGRP][BN];         // per group, per column: the epilogue key of the group's
-                             // maximum (value and row; 0 when no value is positive)
+                             // maximum (value and row); a value that is not positive (0,
+                             // negative or NaN) never wins the merge
   UnitMeta um[2];
 };
 
@@ -1136,7 +1137,7 @@ __device__ __forceinline__ void compute_unit(Smem& sm, const UnitMeta& um, int n
         const int k = kmax[g][nb] - 4 * h;
         const int ko = (int)__builtin_amdgcn_permlane32_swap((unsigned)k, (unsigned)k, false, false)[1];
         const int kb = max(k, ko);
-        if (h == 0) kw[(j * 2 * WAVES_M + g) * BN + nb * 32] = __int_as_float(kb & ~31) > 0.0f ? kb : 0;
+        if (h == 0) kw[(j * 2 * WAVES_M + g) * BN + nb * 32] = kb;
       }
   }
   lds_barrier();  // E
