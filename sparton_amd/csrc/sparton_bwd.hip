@@ -377,13 +377,20 @@ __global__ __launch_bounds__(256) void bwd_scatter_kernel(
   }
 }
 
-// Store four fp32 values as O.
-__device__ __forceinline__ void store4(float* p, const f32x4& a) { *(f32x4*)p = a; }
+// Store four fp32 values as O. The gradients are written once and read by nothing in the
+// backward, so the stores are nontemporal: they stream to memory instead of evicting from
+// L2 the W and H rows that the gathers re-read (cfg 4 backward 342 -> 320 us, cfg 5
+// 535 -> 482 us).
+__device__ __forceinline__ void store4(float* p, const f32x4& a) {
+  __builtin_nontemporal_store(a, (f32x4*)p);
+}
 __device__ __forceinline__ void store4(bf16* p, const f32x4& a) {
-  *(bf16x4*)p = bf16x4{(bf16)a[0], (bf16)a[1], (bf16)a[2], (bf16)a[3]};
+  const bf16x4 v = bf16x4{(bf16)a[0], (bf16)a[1], (bf16)a[2], (bf16)a[3]};
+  __builtin_nontemporal_store(__builtin_bit_cast(uint64_t, v), (uint64_t*)p);
 }
 __device__ __forceinline__ void store4(f16* p, const f32x4& a) {
-  *(f16x4*)p = f16x4{(f16)a[0], (f16)a[1], (f16)a[2], (f16)a[3]};
+  const f16x4 v = f16x4{(f16)a[0], (f16)a[1], (f16)a[2], (f16)a[3]};
+  __builtin_nontemporal_store(__builtin_bit_cast(uint64_t, v), (uint64_t*)p);
 }
 
 // Four consecutive elements of a row, loaded raw (8 bytes for 16-bit types, 16 for
