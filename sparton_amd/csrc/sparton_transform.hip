@@ -91,13 +91,16 @@ __device__ __forceinline__ f32x4 to_f32(vec4_t<T> v) {
   for (int e = 0; e < 4; ++e) r[e] = (float)v[e];
   return r;
 }
+// The epilogues' row outputs (H forward, dZ backward) stream out with nontemporal stores:
+// nothing re-reads them before the next kernel (8192 x 768 bf16: forward 9.0 -> 8.0 us,
+// backward 17.6 -> 16.7 us).
 template <typename T, bool FULL>
 __device__ __forceinline__ void store4t(T* p, int d, int D, f32x4 v) {
   if (in_row<FULL>(d, D)) {
     vec4_t<T> o;
 #pragma unroll
     for (int e = 0; e < 4; ++e) o[e] = from_f32<T>(v[e]);
-    *(vec4_t<T>*)(p + d) = o;
+    __builtin_nontemporal_store(o, (vec4_t<T>*)(p + d));
   }
 }
 template <bool FULL>
